@@ -1,0 +1,189 @@
+"""CPU restatement of the reference ``TransformerLM`` forward and a greedy token loop.
+
+Follows ``src/llmlab/model/layers.py``, ``attention.py`` and ``transformer.py``:
+the numerics that decide rounding are kept as the reference has them --
+RMSNorm computes in fp32 and divides by ``sqrt(mean(x^2)+eps)``
+(``layers.py:133-141``); the RoPE table is built in fp32 and cast to the
+activation dtype before the multiply (``attention.py:31-42,49-50``); attention
+scales after ``QK^T`` and runs softmax in fp32 for 16-bit inputs
+(``attention.py:68-98``); SwiGLU is ``w2(silu(w1 x) * w3 x)`` (``layers.py:114-115``).
+Weights are a plain ``state_dict`` with the reference's keys.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+EPS = 1e-5
+
+
+def rope_tables(theta: float, d_k: int, max_seq_len: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """fp32 cos/sin ``[max_seq_len, d_k/2]`` as ``attention.py:31-42`` builds them."""
+    positions = torch.arange(max_seq_len)
+    pairs = torch.arange(0, d_k, 2)
+    inverse = 1.0 / (theta ** (pairs / d_k))
+    angles = positions.to(torch.float32)[:, None] * inverse[None, :]
+    return torch.cos(angles), torch.sin(angles)
+
+
+def rmsnorm(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+    """``layers.py:133-141``."""
+    dtype = x.dtype
+    x = x.to(torch.float32)
+    rms = torch.sqrt(torch.mean(x * x, dim=-1, keepdim=True) + EPS)
+    return ((x / rms) * weight).to(dtype)
+
+
+def rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, positions: torch.Tensor) -> torch.Tensor:
+    """Interleaved-pair rotation, ``attention.py:44-58``; x is ``[..., T, d_k]``."""
+    c = cos[positions].to(x.dtype)
+    s = sin[positions].to(x.dtype)
+    even, odd = x[..., 0::2], x[..., 1::2]
+    out = torch.empty_like(x)
+    out[..., 0::2] = even * c - odd * s
+    out[..., 1::2] = even * s + odd * c
+    return out
+
+
+def attention_core(q, k, v, mask):
+    """Eager masked attention, ``attention.py:61-98``; mask True = allowed."""
+    scores = torch.matmul(q, k.transpose(-1, -2)) / math.sqrt(q.shape[-1])
+    scores = scores.masked_fill(~mask, float("-inf"))
+    work = scores.float() if scores.dtype in (torch.bfloat16, torch.float16) else scores
+    peak = torch.max(work, dim=-1, keepdim=True).values
+    e = torch.exp(work - peak)
+    weights = (e / torch.sum(e, dim=-1, keepdim=True)).to(scores.dtype)
+    return torch.matmul(weights, v)
+
+
+def _linear(x, w):
+    return torch.matmul(x, w.t())
+
+
+def _split_heads(x, heads):
+    *lead, t, d = x.shape
+    return x.reshape(*lead, t, heads, d // heads).transpose(-3, -2)
+
+
+def _merge_heads(x):
+    *lead, h, t, dk = x.shape
+    return x.transpose(-3, -2).reshape(*lead, t, h * dk)
+
+
+def _layer(sd, prefix, x, heads, cos, sin, positions, mask):
+    h = rmsnorm(x, sd[prefix + "attn_norm.weight"])
+    q = _split_heads(_linear(h, sd[prefix + "attn.q_proj.weight"]), heads)
+    k = _split_heads(_linear(h, sd[prefix + "attn.k_proj.weight"]), heads)
+    v = _split_heads(_linear(h, sd[prefix + "attn.v_proj.weight"]), heads)
+    q = rope(q, cos, sin, positions)
+    k = rope(k, cos, sin, positions)
+    a = _merge_heads(attention_core(q, k, v, mask))
+    x = x + _linear(a, sd[prefix + "attn.output_proj.weight"])
+    h = rmsnorm(x, sd[prefix + "ffn_norm.weight"])
+    a = _linear(h, sd[prefix + "ffn.w1.weight"])
+    g = a * torch.sigmoid(a)
+    x = x + _linear(g * _linear(h, sd[prefix + "ffn.w3.weight"]), sd[prefix + "ffn.w2.weight"])
+    return x
+
+
+@torch.no_grad()
+def forward(sd: dict, config, input_ids: torch.Tensor, dtype=torch.float32) -> torch.Tensor:
+    """``TransformerLM.forward`` (``transformer.py:121-139``): logits ``[..., T, V]``."""
+    if not 0 < input_ids.shape[-1] <= config.context_length:
+        raise ValueError("sequence length must be between 1 and context_length")
+    sd = {name: t.to(dtype) for name, t in sd.items()}
+    cos, sin = rope_tables(config.rope_theta, config.d_model // config.num_heads, config.context_length)
+    t = input_ids.shape[-1]
+    positions = torch.arange(t)
+    mask = torch.tril(torch.ones(t, t, dtype=torch.bool))
+    x = sd["token_embeddings.weight"][input_ids]
+    for layer in range(config.num_layers):
+        x = _layer(sd, f"layers.{layer}.", x, config.num_heads, cos, sin, positions, mask)
+    x = rmsnorm(x, sd["ln_final.weight"])
+    return _linear(x, sd["lm_head.weight"])
+
+
+def greedy_argmax(logits: torch.Tensor) -> torch.Tensor:
+    """First maximal index along the last dim (``torch.argmax`` documents first-index ties)."""
+    return torch.argmax(logits, dim=-1)
+
+
+@torch.no_grad()
+def greedy_recompute(sd, config, prompt: torch.Tensor, steps: int, dtype=torch.float32):
+    """The reference's decode: recompute the whole forward for every new token.
+
+    Returns ``(ids [B, P+steps], margins [B, steps])`` where margins are the gap
+    between the largest and second-largest last-position logit of each step.
+    """
+    ids = prompt.clone()
+    margins = []
+    for _ in range(steps):
+        last = forward(sd, config, ids, dtype)[:, -1, :].float()
+        top = torch.topk(last, 2, dim=-1).values
+        margins.append(top[:, 0] - top[:, 1])
+        ids = torch.cat([ids, greedy_argmax(last)[:, None]], dim=1)
+    return ids, torch.stack(margins, dim=1)
+
+
+class KVCacheOracle:
+    """KV-cached restatement of the same forward, one position at a time.
+
+    Equal to ``forward`` up to float reassociation; used as the teacher-forced
+    checker for long decodes and as the CPU baseline.
+    """
+
+    def __init__(self, sd, config, batch: int, capacity: int | None = None, dtype=torch.float32):
+        self.config = config
+        self.dtype = dtype
+        self.sd = {n: t.to(dtype) for n, t in sd.items()}
+        self.heads = config.num_heads
+        self.dk = config.d_model // config.num_heads
+        cap = capacity or config.context_length
+        shape = (config.num_layers, batch, self.heads, cap, self.dk)
+        self.k = torch.zeros(shape, dtype=dtype)
+        self.v = torch.zeros(shape, dtype=dtype)
+        self.cos, self.sin = rope_tables(config.rope_theta, self.dk, config.context_length)
+        self.length = 0
+
+    @torch.no_grad()
+    def step(self, tokens: torch.Tensor) -> torch.Tensor:
+        """Append ``tokens [B, T]`` at the current length; return logits ``[B, T, V]``."""
+        sd, cfg = self.sd, self.config
+        t = tokens.shape[1]
+        start = self.length
+        positions = torch.arange(start, start + t)
+        total = start + t
+        mask = torch.arange(total)[None, :] <= positions[:, None]
+        x = sd["token_embeddings.weight"][tokens]
+        for layer in range(cfg.num_layers):
+            p = f"layers.{layer}."
+            h = rmsnorm(x, sd[p + "attn_norm.weight"])
+            q = rope(_split_heads(_linear(h, sd[p + "attn.q_proj.weight"]), self.heads), self.cos, self.sin, positions)
+            k = rope(_split_heads(_linear(h, sd[p + "attn.k_proj.weight"]), self.heads), self.cos, self.sin, positions)
+            v = _split_heads(_linear(h, sd[p + "attn.v_proj.weight"]), self.heads)
+            self.k[layer, :, :, start:total] = k
+            self.v[layer, :, :, start:total] = v
+            a = attention_core(q, self.k[layer, :, :, :total], self.v[layer, :, :, :total], mask)
+            x = x + _linear(_merge_heads(a), sd[p + "attn.output_proj.weight"])
+            h = rmsnorm(x, sd[p + "ffn_norm.weight"])
+            a1 = _linear(h, sd[p + "ffn.w1.weight"])
+            x = x + _linear(a1 * torch.sigmoid(a1) * _linear(h, sd[p + "ffn.w3.weight"]), sd[p + "ffn.w2.weight"])
+        self.length = total
+        return _linear(rmsnorm(x, sd["ln_final.weight"]), sd["lm_head.weight"])
+
+
+@torch.no_grad()
+def greedy_cached(sd, config, prompt: torch.Tensor, steps: int, dtype=torch.float32):
+    """Greedy decode through ``KVCacheOracle``; returns ``(ids, last-position logits per step)``."""
+    cache = KVCacheOracle(sd, config, prompt.shape[0], prompt.shape[1] + steps, dtype)
+    logits = cache.step(prompt)[:, -1, :]
+    ids = [prompt]
+    history = []
+    for _ in range(steps):
+        history.append(logits.float())
+        nxt = greedy_argmax(logits.float())[:, None]
+        ids.append(nxt)
+        logits = cache.step(nxt)[:, -1, :]
+    return torch.cat(ids, dim=1), torch.stack(history, dim=1)

@@ -1,0 +1,135 @@
+"""Pin the CPU oracle against the reference's own outputs and invariants (no GPU)."""
+
+import hashlib
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import model as om
+from oracle.attention import decode_reference, dense_mask, masked_attention
+from systems_for_llms_amd.config import ModelConfig, load_model_config
+from systems_for_llms_amd.weights import seeded_prompt, seeded_state_dict, state_dict_sha256
+
+
+def _sha(t):
+    return hashlib.sha256(t.contiguous().numpy().tobytes()).hexdigest()
+
+
+def _tiny(meta):
+    return ModelConfig(**meta["tiny"]["config"])
+
+
+def test_rope_tables_bit_exact_with_reference(golden):
+    meta, _ = golden
+    for case in meta["rope"]:
+        cos, sin = om.rope_tables(case["theta"], case["d_k"], case["max_seq_len"])
+        assert _sha(cos) == case["cos_sha256"], case
+        assert _sha(sin) == case["sin_sha256"], case
+
+
+def test_weight_generator_matches_fixture(golden):
+    meta, _ = golden
+    assert state_dict_sha256(seeded_state_dict(_tiny(meta), meta["tiny"]["seed"])) == meta["tiny"]["weights_sha256"]
+
+
+def test_tiny_forward_matches_reference_logits(golden):
+    meta, arrays = golden
+    cfg = _tiny(meta)
+    sd = seeded_state_dict(cfg, meta["tiny"]["seed"])
+    ids = torch.from_numpy(arrays["tiny_ids"])
+    assert torch.equal(ids, seeded_prompt(cfg.vocab_size, 3, 24, meta["tiny"]["prompt_seed"]))
+    logits = om.forward(sd, cfg, ids)
+    for backend in ("sdpa", "eager"):
+        expected = torch.from_numpy(arrays[f"tiny_logits_fp32_{backend}"])
+        torch.testing.assert_close(logits, expected, atol=2e-6, rtol=2e-5)
+
+
+def test_tiny_forward_bf16_matches_reference(golden):
+    meta, arrays = golden
+    cfg = _tiny(meta)
+    sd = seeded_state_dict(cfg, meta["tiny"]["seed"])
+    logits = om.forward(sd, cfg, torch.from_numpy(arrays["tiny_ids"]), dtype=torch.bfloat16).float()
+    expected = torch.from_numpy(arrays["tiny_logits_bf16_eager"])
+    # bf16 matmul reassociation: a few bf16 ulps of logits of magnitude ~0.5.
+    torch.testing.assert_close(logits, expected, atol=1.6e-2, rtol=0)
+
+
+def test_planted_mistake_is_caught(golden):
+    """A plausible oracle slip (RoPE pairs rotated the other way) must fail the golden check."""
+    meta, arrays = golden
+    cfg = _tiny(meta)
+    sd = seeded_state_dict(cfg, meta["tiny"]["seed"])
+    real = om.rope
+    try:
+        om.rope = lambda x, c, s, p: real(x, c, -s, p)
+        wrong = om.forward(sd, cfg, torch.from_numpy(arrays["tiny_ids"]))
+    finally:
+        om.rope = real
+    assert not torch.allclose(wrong, torch.from_numpy(arrays["tiny_logits_fp32_sdpa"]), atol=1e-4)
+
+
+def test_kv_cached_equals_recompute_and_prefix_invariance(golden):
+    meta, arrays = golden
+    cfg = _tiny(meta)
+    sd = seeded_state_dict(cfg, meta["tiny"]["seed"])
+    ids = torch.from_numpy(arrays["tiny_ids"])
+    full = om.forward(sd, cfg, ids)
+    cache = om.KVCacheOracle(sd, cfg, ids.shape[0])
+    pieces = [cache.step(ids[:, :5]), cache.step(ids[:, 5:6]), cache.step(ids[:, 6:])]
+    torch.testing.assert_close(torch.cat(pieces, dim=1), full, atol=2e-6, rtol=2e-5)
+    changed = ids.clone()
+    changed[:, 9:] = (changed[:, 9:] + 1) % cfg.vocab_size
+    torch.testing.assert_close(om.forward(sd, cfg, changed)[:, :9], full[:, :9], atol=1e-6, rtol=1e-5)
+
+
+@pytest.mark.slow
+def test_config1_greedy_sequence_matches_reference(golden):
+    meta, arrays = golden
+    c1 = meta["c1"]
+    cfg = load_model_config("pilot-22m-s256")
+    sd = seeded_state_dict(cfg, c1["seed"])
+    assert state_dict_sha256(sd) == c1["weights_sha256"]
+    prompt = seeded_prompt(cfg.vocab_size, 1, c1["prompt_length"], c1["prompt_seed"])
+    ids, history = om.greedy_cached(sd, cfg, prompt, c1["steps"])
+    assert torch.equal(ids, torch.from_numpy(arrays["c1_ids"]))
+    for step in c1["snapshot_steps"]:
+        torch.testing.assert_close(history[0, step], torch.from_numpy(arrays[f"c1_logits_step{step}"]),
+                                   atol=2e-5, rtol=1e-4)
+
+
+def test_decode_reference_matches_sdpa_with_repeated_heads():
+    torch.manual_seed(7)
+    q = torch.randn(3, 8, 64)
+    k = torch.randn(3, 2, 17, 64)
+    v = torch.randn_like(k)
+    lengths = torch.tensor([0, 3, 17], dtype=torch.int32)
+    actual = decode_reference(q, k, v, lengths)
+    allowed = torch.arange(17)[None, :] < lengths[:, None]
+    expected = F.scaled_dot_product_attention(
+        q.unsqueeze(2), k.repeat_interleave(4, dim=1), v.repeat_interleave(4, dim=1),
+        attn_mask=allowed[:, None, None, :]).squeeze(2)
+    torch.testing.assert_close(actual[1:], expected[1:])
+    assert torch.equal(actual[0], torch.zeros_like(actual[0]))
+    scaled = decode_reference(q[1:], k[1:], v[1:], lengths[1:], scale=0.37)
+    expected = F.scaled_dot_product_attention(
+        q[1:].unsqueeze(2), k[1:].repeat_interleave(4, dim=1), v[1:].repeat_interleave(4, dim=1),
+        attn_mask=allowed[1:, None, None, :], scale=0.37).squeeze(2)
+    torch.testing.assert_close(scaled, expected)
+
+
+def test_masked_attention_matches_sdpa_fp64_and_empty_rows():
+    g = torch.Generator().manual_seed(2026)
+    n = 33
+    q, k, v = (torch.randn(1, 2, n, 8, dtype=torch.float64, generator=g) for _ in range(3))
+    for mask in (dense_mask(n, causal=True), dense_mask(n, window_left=7, window_right=3),
+                 dense_mask(n, causal=True, window_left=4, global_prefix=6)):
+        out, lse = masked_attention(q, k, v, mask)
+        ref = F.scaled_dot_product_attention(q, k, v, attn_mask=mask)
+        torch.testing.assert_close(out, ref, atol=1e-10, rtol=1e-10)
+        scores = (q @ k.transpose(-1, -2)) / np.sqrt(8)
+        torch.testing.assert_close(lse, torch.logsumexp(scores.masked_fill(~mask, -np.inf), -1))
+    empty = torch.zeros(n, n, dtype=torch.bool)
+    out, lse = masked_attention(q, k, v, empty)
+    assert torch.equal(out, torch.zeros_like(out)) and torch.isneginf(lse).all()
