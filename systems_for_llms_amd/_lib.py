@@ -1,0 +1,74 @@
+"""ctypes binding of ``libsfl.so`` (the C ABI in ``include/sfl.h``).
+
+The library is loaded from the package's ``lib/`` directory, where
+``systems_for_llms_amd.build`` writes it. There is no fallback: if the library
+is missing every GPU entry point raises, naming the build command.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from ctypes import c_float, c_int, c_int64, c_void_p, c_char_p
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "lib" / "libsfl.so"
+
+DTYPE_CODES = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
+
+P = c_void_p
+SIGNATURES: dict[str, list] = {
+    "sfl_decode_attention": [P, P, P, P, P, P, P, P, c_int, c_int, c_int, c_int, c_int, c_int,
+                             c_float, c_int, P],
+}
+
+_LIB = None
+
+
+class LibraryMissing(RuntimeError):
+    pass
+
+
+def lib() -> ctypes.CDLL:
+    global _LIB
+    if _LIB is None:
+        if not LIB_PATH.exists():
+            raise LibraryMissing(
+                f"{LIB_PATH} is not built; run `python -m systems_for_llms_amd.build` "
+                "(or __graft_entry__.build()) before using the GPU path")
+        handle = ctypes.CDLL(str(LIB_PATH))
+        handle.sfl_version.restype = c_char_p
+        handle.sfl_version.argtypes = []
+        handle.sfl_last_error.restype = c_char_p
+        handle.sfl_last_error.argtypes = []
+        for name, args in SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.argtypes = args
+            fn.restype = c_int
+        _LIB = handle
+    return _LIB
+
+
+def call(name: str, *args) -> None:
+    """Invoke an entry point; a nonzero status becomes RuntimeError with the library's message."""
+    handle = lib()
+    status = getattr(handle, name)(*args)
+    if status != 0:
+        message = handle.sfl_last_error().decode(errors="replace")
+        raise RuntimeError(f"{name} failed ({status}): {message}")
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def stream_handle(device: torch.device | None = None) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    try:
+        return DTYPE_CODES[dtype]
+    except KeyError:
+        raise TypeError(f"unsupported dtype {dtype}; expected float32, bfloat16 or float16") from None

@@ -1,0 +1,131 @@
+"""Single-query attention over a contiguous KV cache (the ``cuda_decode`` operator API).
+
+Drop-in for ``attention_lab/cuda_decode/kernel.py``: the same ``prepare`` /
+``decode`` / ``PreparedDecode`` surface, argument meaning and errors, backed by
+the gfx950 split-KV kernels of ``libsfl.so`` instead of a JIT-built CUDA
+extension. The prepared operation owns its fp32 scratch and output and holds
+its inputs by reference; the output is overwritten by every call; ``lengths``
+may be changed in place between calls and graph replays; concurrent calls on
+one prepared operation race on its scratch (``kernel.py:1-6``).
+
+Differences, all widenings of the reference contract:
+
+* head dimension 32 is accepted besides 64 and 128, and fp32 besides fp16/bf16
+  (the 22.7M parity model has 16 heads of 32 and runs in fp32);
+* ``splits=None`` (the default here) picks the split count from the shape; an
+  integer in [1, 128] is honoured exactly as in the reference;
+* ``variant`` accepts ``"token"`` and ``"tile"`` and both run the same kernel:
+  the gfx950 kernel always updates its softmax state once per tile of keys.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+
+SUPPORTED_DIMS = (32, 64, 128)
+SUPPORTED_GROUPS = (1, 2, 4, 8)
+MAX_SPLITS = 128
+
+
+def _validate(q, k, v, lengths, splits):
+    """Mirrors ``kernel.py:27-53`` (messages kept so callers' regexes still match)."""
+    if splits is not None and (type(splits) is not int or not 1 <= splits <= MAX_SPLITS):
+        raise ValueError("splits must be an integer in [1, 128]")
+    if q.ndim != 3 or k.ndim != 4 or v.shape != k.shape:
+        raise ValueError("expected q[B,Hq,D], k/v[B,Hkv,N,D]")
+    batch, query_heads, dim = q.shape
+    if min(q.shape) <= 0 or k.shape[0] != batch or k.shape[3] != dim:
+        raise ValueError("Q/K/V batch and head dimensions must match and be nonempty")
+    kv_heads, capacity = k.shape[1:3]
+    if kv_heads <= 0 or capacity <= 0 or query_heads % kv_heads:
+        raise ValueError("query heads must be divisible by positive KV heads")
+    if dim not in SUPPORTED_DIMS or query_heads // kv_heads not in SUPPORTED_GROUPS:
+        raise ValueError("supported head dimensions are 32/64/128 and GQA ratios 1/2/4/8")
+    if q.dtype not in _lib.DTYPE_CODES or k.dtype != q.dtype or v.dtype != q.dtype:
+        raise TypeError("Q/K/V must have the same FP16, BF16 or FP32 dtype")
+    if not q.is_cuda or any(x.device != q.device for x in (k, v, lengths)):
+        raise ValueError("all tensors must be on the same CUDA device")
+    if any(not x.is_contiguous() for x in (q, k, v, lengths)):
+        raise ValueError("all tensors must be contiguous")
+    if lengths.dtype != torch.int32 or lengths.shape != (batch,):
+        raise ValueError("lengths must be an int32 tensor of shape [B]")
+    low, high = torch.aminmax(lengths)
+    if low.item() < 0 or high.item() > capacity:
+        raise ValueError("each length must be in [0, cache capacity]")
+    return batch, query_heads, dim
+
+
+def auto_splits(batch: int, kv_heads: int, capacity: int, target_items: int = 2048,
+                keys_per_item: int = 256, min_keys: int = 64) -> int:
+    """Split count giving about ``target_items`` wave work items of >= ``min_keys`` keys.
+
+    One wave streams one chunk of ceil(capacity/splits) keys; 256 keys per wave
+    is 64 KB of bf16 K+V at D=64, enough to keep its loads in flight, and a few
+    thousand items fill the 256 CUs several times over.
+    """
+    splits = max(math.ceil(capacity / keys_per_item), math.ceil(target_items / (batch * kv_heads)))
+    return max(1, min(MAX_SPLITS, splits, math.ceil(capacity / min_keys)))
+
+
+@dataclass
+class PreparedDecode:
+    q: torch.Tensor
+    k: torch.Tensor
+    v: torch.Tensor
+    lengths: torch.Tensor
+    partial_max: torch.Tensor
+    partial_sum: torch.Tensor
+    partial_output: torch.Tensor
+    output: torch.Tensor
+    splits: int
+    scale: float
+    variant: str
+
+    def __call__(self) -> torch.Tensor:
+        batch, heads, dim = self.q.shape
+        kv_heads, capacity = self.k.shape[1:3]
+        _lib.call("sfl_decode_attention", self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(),
+                  self.lengths.data_ptr(), self.partial_max.data_ptr(), self.partial_sum.data_ptr(),
+                  self.partial_output.data_ptr(), self.output.data_ptr(), batch, heads, kv_heads,
+                  capacity, dim, self.splits, self.scale, _lib.dtype_code(self.q.dtype),
+                  _lib.stream_handle(self.q.device))
+        return self.output
+
+    @property
+    def scratch_bytes(self) -> int:
+        return sum(x.numel() * x.element_size() for x in
+                   (self.partial_max, self.partial_sum, self.partial_output))
+
+
+def prepare(q, k, v, lengths=None, *, splits=None, scale=None, variant="token") -> PreparedDecode:
+    """Validate and allocate outside capture, then return a reusable operation (``kernel.py:85-113``)."""
+    if variant not in ("token", "tile"):
+        raise ValueError("variant must be 'token' or 'tile'")
+    if lengths is None:
+        if q.ndim != 3 or k.ndim != 4:
+            raise ValueError("expected q[B,Hq,D], k/v[B,Hkv,N,D]")
+        lengths = torch.full((q.shape[0],), k.shape[2], device=q.device, dtype=torch.int32)
+    batch, heads, dim = _validate(q, k, v, lengths, splits)
+    if scale is None:
+        scale = dim ** -0.5
+    if not math.isfinite(scale) or scale <= 0:
+        raise ValueError("scale must be finite and positive")
+    _lib.lib()  # fail here, before allocation, if the library is not built
+    if splits is None:
+        splits = auto_splits(batch, k.shape[1], k.shape[2])
+    maximum = torch.empty((batch, heads, splits), device=q.device, dtype=torch.float32)
+    normalizer = torch.empty_like(maximum)
+    numerator = torch.empty((batch, heads, splits, dim), device=q.device, dtype=torch.float32)
+    output = torch.empty_like(q)
+    return PreparedDecode(q, k, v, lengths, maximum, normalizer, numerator, output, splits,
+                          float(scale), variant)
+
+
+def decode(q, k, v, lengths=None, *, splits=None, scale=None, variant="token") -> torch.Tensor:
+    """Allocate scratch and compute one decode step on the current stream (``kernel.py:116-118``)."""
+    return prepare(q, k, v, lengths, splits=splits, scale=scale, variant=variant)()

@@ -1,0 +1,48 @@
+"""The C-ABI library loads and exports every symbol include/sfl.h declares (no GPU calls)."""
+
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def declared_symbols():
+    text = (ROOT / "include" / "sfl.h").read_text()
+    return sorted(set(re.findall(r"\b(sfl_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_entry_points():
+    names = declared_symbols()
+    assert "sfl_decode_attention" in names and "sfl_last_error" in names
+
+
+def test_library_exports_every_declared_symbol():
+    from systems_for_llms_amd import _lib
+
+    if not _lib.LIB_PATH.exists():
+        pytest.skip("libsfl.so not built (run __graft_entry__.build())")
+    handle = _lib.lib()
+    missing = [name for name in declared_symbols() if not hasattr(handle, name)]
+    assert not missing
+    assert handle.sfl_version().decode().startswith("sfl")
+    assert set(_lib.SIGNATURES) <= set(declared_symbols())
+
+
+def test_argument_errors_are_reported_without_a_launch():
+    import ctypes
+
+    from systems_for_llms_amd import _lib
+
+    if not _lib.LIB_PATH.exists():
+        pytest.skip("libsfl.so not built")
+    with pytest.raises(RuntimeError, match="null pointer"):
+        _lib.call("sfl_decode_attention", None, None, None, None, None, None, None, None,
+                  1, 1, 1, 1, 64, 1, 0.125, 1, None)
+    buf = ctypes.create_string_buffer(64)
+    p = ctypes.addressof(buf)
+    with pytest.raises(RuntimeError, match="divisible"):
+        _lib.call("sfl_decode_attention", p, p, p, p, p, p, p, p, 1, 3, 2, 16, 64, 1, 0.125, 1, None)
+    with pytest.raises(RuntimeError, match="head dim"):
+        _lib.call("sfl_decode_attention", p, p, p, p, p, p, p, p, 1, 2, 2, 16, 48, 1, 0.125, 1, None)

@@ -1,0 +1,43 @@
+"""Host-side contract of the decode operator (no GPU): validation before any launch."""
+
+import pytest
+import torch
+
+from systems_for_llms_amd.decode import auto_splits, prepare
+
+
+def test_cpu_input_rejected_before_launch():
+    q = torch.zeros(1, 8, 64, dtype=torch.float16)
+    k = torch.zeros(1, 2, 17, 64, dtype=torch.float16)
+    with pytest.raises(ValueError, match="same CUDA"):
+        prepare(q, k, k)
+
+
+def test_invalid_split_count_rejected():
+    q = torch.zeros(1, 8, 64, dtype=torch.float16)
+    k = torch.zeros(1, 2, 17, 64, dtype=torch.float16)
+    for splits in (0, 129, True, 2.5):
+        with pytest.raises(ValueError, match="splits"):
+            prepare(q, k, k, splits=splits)
+
+
+def test_unknown_variant_and_bad_ratio_rejected():
+    q = torch.zeros(1, 8, 64, dtype=torch.float16)
+    k = torch.zeros(1, 2, 17, 64, dtype=torch.float16)
+    with pytest.raises(ValueError, match="variant"):
+        prepare(q, k, k, variant="approximate")
+    with pytest.raises(ValueError, match="divisible"):
+        prepare(torch.zeros(1, 7, 64, dtype=torch.float16), k, k)
+    with pytest.raises(ValueError, match="head dimensions"):
+        prepare(torch.zeros(1, 8, 48, dtype=torch.float16), torch.zeros(1, 2, 17, 48, dtype=torch.float16),
+                torch.zeros(1, 2, 17, 48, dtype=torch.float16))
+
+
+def test_auto_splits_bounds():
+    assert auto_splits(64, 16, 16384) == 64
+    assert auto_splits(16, 16, 4096) == 16
+    assert auto_splits(1, 4, 1024) == 16
+    assert auto_splits(1, 1, 10) == 1
+    for b, h, n in ((1, 1, 1), (3, 5, 999), (128, 32, 65536)):
+        s = auto_splits(b, h, n)
+        assert 1 <= s <= 128
