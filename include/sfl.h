@@ -10,7 +10,10 @@
  * call leaves every buffer untouched.
  *
  * Tensor layouts are row-major and contiguous unless a stride is passed.
- * Element types are selected by an SFL_DTYPE_* code.
+ * Element types are selected by an SFL_DTYPE_* code. In the decode-step
+ * entry points weights and the KV cache use the model dtype while
+ * activations (x, q, attention output, SwiGLU hidden) are fp32; with bf16
+ * weights each activation is split into two bf16 halves for the MFMAs.
  */
 #ifndef SFL_H_
 #define SFL_H_
@@ -53,13 +56,86 @@ const char* sfl_last_error(void);
  *
  * The cache is partitioned by capacity into `splits` chunks of
  * ceil(cap/splits) keys (decode.cu:50-52); chunks past a row's length do no
- * work. D in {32, 64, 128}; Hq/Hkv in {1, 2, 4, 8}; splits in [1, 1024].
- * dtype: F32, BF16 or F16; softmax state is fp32.
+ * work. D in {16, 32, 64, 128}; Hq/Hkv in {1, 2, 4, 8}; splits in [1, 1024].
+ * dtype: element type of k and v (F32, BF16 or F16); io_dtype: element type
+ * of q and out, either the same as dtype or F32. Softmax state is fp32.
  */
 int sfl_decode_attention(const void* q, const void* k, const void* v, const int32_t* lengths,
                          float* partial_max, float* partial_sum, float* partial_out, void* out,
                          int batch, int q_heads, int kv_heads, int capacity, int head_dim,
-                         int splits, float scale, int dtype, void* stream);
+                         int splits, float scale, int dtype, int io_dtype, void* stream);
+
+
+/* ---- decode step of the llmlab decoder (model dtype F32 or BF16) ----------
+ * One step processes one token per sequence for `batch` <= 16 sequences per
+ * launch. x is the fp32 residual stream [batch, d_model]; weights are the
+ * reference's [out, in] matrices in the model dtype.
+ */
+
+/*
+ * q/k/v projections of RMSNorm(x) with RoPE and the KV-cache append.
+ * Replaces, for one position, TransformerBlock's attn_norm + q/k/v_proj + RoPE
+ * (src/llmlab/model/transformer.py:46, layers.py:133-141,
+ * attention.py:160-185); the reference recomputes K/V for every position.
+ *   w_qkv    [3*d_model, d_model]: q_proj, k_proj, v_proj rows stacked
+ *   cos_t, sin_t [capacity, head_dim/2] fp32 (the table of attention.py:31-42)
+ *   pos      [batch] int32 position of this token; k/v are written at pos[b]
+ *   q_out    [batch, heads, head_dim] fp32; k_cache, v_cache [batch, heads, capacity, head_dim]
+ */
+int sfl_rmsnorm_qkv_rope_append(const float* x, const void* norm_w, const void* w_qkv,
+                                const float* cos_t, const float* sin_t, const int32_t* pos,
+                                void* q_out, void* k_cache, void* v_cache, int batch,
+                                int d_model, int heads, int capacity, int dtype, void* stream);
+
+/*
+ * x_out = x + act @ w^T (act [batch, k] fp32, w [n, k], x/x_out fp32 [batch, n],
+ * x_out may alias x). Replaces output_proj + residual and ffn.w2 + residual
+ * (transformer.py:46-47, attention.py:199-203, layers.py:114-115).
+ */
+int sfl_linear_residual(const void* act, const void* w, const float* x, float* x_out, int batch,
+                        int n, int k, int dtype, void* stream);
+
+/*
+ * h = silu(RMSNorm(x) @ w1^T) * (RMSNorm(x) @ w3^T), h [batch, d_ff] fp32.
+ * Replaces ffn_norm + SwiGLU's w1/w3 half (transformer.py:47, layers.py:73-115).
+ */
+int sfl_rmsnorm_swiglu(const float* x, const void* norm_w, const void* w1, const void* w3,
+                       void* h_out, int batch, int d_model, int d_ff, int dtype, void* stream);
+
+/*
+ * logits = RMSNorm(x) @ w_head^T plus a per-tile argmax (lowest index on ties).
+ * Replaces ln_final + lm_head (transformer.py:137-138) for the last position.
+ *   logits   optional [.., vocab] fp32; row b is written at
+ *            logits + b*logits_batch_stride + pos[b]*logits_pos_stride (pos may be NULL)
+ *   best_val, best_idx [sfl_lm_head_tiles(vocab), best_stride]: the tile maxima
+ */
+int sfl_rmsnorm_lm_head(const float* x, const void* norm_w, const void* w_head, void* logits,
+                        long logits_batch_stride, const int32_t* pos, long logits_pos_stride,
+                        float* best_val, int32_t* best_idx, int best_stride, int batch,
+                        int d_model, int vocab, int dtype, void* stream);
+
+/* Number of lm_head tiles (rows of best_val/best_idx) for a vocabulary size. */
+int sfl_lm_head_tiles(int vocab);
+
+/*
+ * x[b] = emb[tokens[b*token_stride + pos[b]]] in fp32 (Embedding.forward, layers.py:68-70).
+ */
+int sfl_embedding_gather(const int64_t* tokens, long token_stride, const int32_t* pos,
+                         const void* emb, float* x, int batch, int d_model, int dtype,
+                         void* stream);
+
+/*
+ * Greedy step: argmax over the lm_head tiles (first maximal index, as
+ * torch.argmax), then, with np = pos[b] + 1: predicted[b, np] = argmax;
+ * tokens[b, np] = argmax unless np < prompt_len[b] (the prompt token is kept);
+ * x[b] = emb[tokens[b, np]]; pos[b] = np; lengths[b] = np + 1. Nothing changes
+ * for a row whose np would reach capacity. The reference has no token loop;
+ * its greedy continuation is argmax(TransformerLM.forward(ids)[:, -1]).
+ */
+int sfl_next_token(const float* best_val, const int32_t* best_idx, int tiles, int64_t* tokens,
+                   int64_t* predicted, long token_stride, const int32_t* prompt_len, int32_t* pos,
+                   int32_t* lengths, const void* emb, float* x, int batch, int d_model,
+                   int capacity, int dtype, void* stream);
 
 #ifdef __cplusplus
 }

@@ -72,13 +72,16 @@ def _merge_heads(x):
     return x.transpose(-3, -2).reshape(*lead, t, h * dk)
 
 
-def _layer(sd, prefix, x, heads, cos, sin, positions, mask):
+def _layer(sd, prefix, x, heads, cos, sin, positions, mask, kv_dtype=None):
     h = rmsnorm(x, sd[prefix + "attn_norm.weight"])
     q = _split_heads(_linear(h, sd[prefix + "attn.q_proj.weight"]), heads)
     k = _split_heads(_linear(h, sd[prefix + "attn.k_proj.weight"]), heads)
     v = _split_heads(_linear(h, sd[prefix + "attn.v_proj.weight"]), heads)
     q = rope(q, cos, sin, positions)
     k = rope(k, cos, sin, positions)
+    if kv_dtype is not None:  # keys/values stored in a narrower cache format
+        k = k.to(kv_dtype).to(x.dtype)
+        v = v.to(kv_dtype).to(x.dtype)
     a = _merge_heads(attention_core(q, k, v, mask))
     x = x + _linear(a, sd[prefix + "attn.output_proj.weight"])
     h = rmsnorm(x, sd[prefix + "ffn_norm.weight"])
@@ -89,8 +92,12 @@ def _layer(sd, prefix, x, heads, cos, sin, positions, mask):
 
 
 @torch.no_grad()
-def forward(sd: dict, config, input_ids: torch.Tensor, dtype=torch.float32) -> torch.Tensor:
-    """``TransformerLM.forward`` (``transformer.py:121-139``): logits ``[..., T, V]``."""
+def forward(sd: dict, config, input_ids: torch.Tensor, dtype=torch.float32, kv_dtype=None) -> torch.Tensor:
+    """``TransformerLM.forward`` (``transformer.py:121-139``): logits ``[..., T, V]``.
+
+    ``kv_dtype`` (not in the reference) rounds keys and values through a cache
+    storage format, to bound what a narrower KV cache alone changes.
+    """
     if not 0 < input_ids.shape[-1] <= config.context_length:
         raise ValueError("sequence length must be between 1 and context_length")
     sd = {name: t.to(dtype) for name, t in sd.items()}
@@ -100,9 +107,18 @@ def forward(sd: dict, config, input_ids: torch.Tensor, dtype=torch.float32) -> t
     mask = torch.tril(torch.ones(t, t, dtype=torch.bool))
     x = sd["token_embeddings.weight"][input_ids]
     for layer in range(config.num_layers):
-        x = _layer(sd, f"layers.{layer}.", x, config.num_heads, cos, sin, positions, mask)
+        x = _layer(sd, f"layers.{layer}.", x, config.num_heads, cos, sin, positions, mask, kv_dtype)
     x = rmsnorm(x, sd["ln_final.weight"])
     return _linear(x, sd["lm_head.weight"])
+
+
+def round_weights(sd: dict, dtype=torch.bfloat16) -> dict:
+    """The same state_dict with every tensor rounded through ``dtype`` and back to fp32.
+
+    ``forward(round_weights(sd), ...)`` is the bf16-weight model with exact
+    fp32 arithmetic: the accuracy floor of any kernel that stores bf16 weights.
+    """
+    return {name: t.to(dtype).to(torch.float32) for name, t in sd.items()}
 
 
 def greedy_argmax(logits: torch.Tensor) -> torch.Tensor:

@@ -8,7 +8,7 @@ is missing every GPU entry point raises, naming the build command.
 from __future__ import annotations
 
 import ctypes
-from ctypes import c_float, c_int, c_int64, c_void_p, c_char_p
+from ctypes import c_char_p, c_float, c_int, c_long, c_void_p
 from pathlib import Path
 
 import torch
@@ -20,7 +20,14 @@ DTYPE_CODES = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
 P = c_void_p
 SIGNATURES: dict[str, list] = {
     "sfl_decode_attention": [P, P, P, P, P, P, P, P, c_int, c_int, c_int, c_int, c_int, c_int,
-                             c_float, c_int, P],
+                             c_float, c_int, c_int, P],
+    "sfl_rmsnorm_qkv_rope_append": [P, P, P, P, P, P, P, P, P, c_int, c_int, c_int, c_int, c_int, P],
+    "sfl_linear_residual": [P, P, P, P, c_int, c_int, c_int, c_int, P],
+    "sfl_rmsnorm_swiglu": [P, P, P, P, P, c_int, c_int, c_int, c_int, P],
+    "sfl_rmsnorm_lm_head": [P, P, P, P, c_long, P, c_long, P, P, c_int, c_int, c_int, c_int, c_int, P],
+    "sfl_lm_head_tiles": [c_int],
+    "sfl_embedding_gather": [P, c_long, P, P, P, c_int, c_int, c_int, P],
+    "sfl_next_token": [P, P, c_int, P, P, c_long, P, P, P, P, P, c_int, c_int, c_int, c_int, P],
 }
 
 _LIB = None

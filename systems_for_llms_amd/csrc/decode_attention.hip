@@ -29,9 +29,9 @@ struct DecodeShape {
   static_assert(LPT >= 1 && LPT <= kWave, "head dim does not fit a wave");
 };
 
-template <typename T, int D, int G>
+template <typename T, typename TQ, int D, int G>
 __global__ __launch_bounds__(256) void decode_partial_kernel(
-    const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
+    const TQ* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
     const int32_t* __restrict__ lengths, float* __restrict__ pmax, float* __restrict__ psum,
     float* __restrict__ pout, int batch, int kv_heads, int cap, int splits, int chunk,
     float qscale) {
@@ -56,10 +56,9 @@ __global__ __launch_bounds__(256) void decode_partial_kernel(
   float qv[G][EPL];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
-    const T* qp = q + (long(b) * q_heads + h * G + g) * D + dg * EPL;
-    unpack16<T>(load16(qp), qv[g]);
+    const TQ* qp = q + (long(b) * q_heads + h * G + g) * D + dg * EPL;
 #pragma unroll
-    for (int e = 0; e < EPL; ++e) qv[g][e] *= qscale;
+    for (int e = 0; e < EPL; ++e) qv[g][e] = load_scalar<TQ>(qp + e) * qscale;
   }
   float m[G], l[G], acc[G][EPL];
 #pragma unroll
@@ -207,46 +206,47 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(
   }
 }
 
-template <typename T, int D, int G>
+template <typename T, typename TQ, int D, int G>
 int launch_decode(const void* q, const void* k, const void* v, const int32_t* lengths, float* pmax,
                   float* psum, float* pout, void* out, int batch, int q_heads, int kv_heads,
                   int cap, int splits, float scale, hipStream_t stream) {
   const int chunk = (cap + splits - 1) / splits;
   const long items = long(batch) * kv_heads * splits;
   const long rows = long(batch) * q_heads;
-  hipLaunchKernelGGL((decode_partial_kernel<T, D, G>), dim3(unsigned((items + 3) / 4)), dim3(256), 0,
-                     stream, static_cast<const T*>(q), static_cast<const T*>(k),
+  hipLaunchKernelGGL((decode_partial_kernel<T, TQ, D, G>), dim3(unsigned((items + 3) / 4)), dim3(256), 0,
+                     stream, static_cast<const TQ*>(q), static_cast<const T*>(k),
                      static_cast<const T*>(v), lengths, pmax, psum, pout, batch, kv_heads, cap,
                      splits, chunk, scale * kLog2e);
   int rc = check_launch("decode_partial");
   if (rc) return rc;
-  hipLaunchKernelGGL((decode_merge_kernel<T, D>), dim3(unsigned((rows + 3) / 4)), dim3(256), 0, stream,
-                     pmax, psum, pout, lengths, static_cast<T*>(out), batch, q_heads, cap, splits,
+  hipLaunchKernelGGL((decode_merge_kernel<TQ, D>), dim3(unsigned((rows + 3) / 4)), dim3(256), 0, stream,
+                     pmax, psum, pout, lengths, static_cast<TQ*>(out), batch, q_heads, cap, splits,
                      chunk);
   return check_launch("decode_merge");
 }
 
-template <typename T, int D>
+template <typename T, typename TQ, int D>
 int dispatch_groups(int groups, const void* q, const void* k, const void* v, const int32_t* lengths,
                     float* pmax, float* psum, float* pout, void* out, int batch, int q_heads,
                     int kv_heads, int cap, int splits, float scale, hipStream_t stream) {
   switch (groups) {
-    case 1: return launch_decode<T, D, 1>(q, k, v, lengths, pmax, psum, pout, out, batch, q_heads, kv_heads, cap, splits, scale, stream);
-    case 2: return launch_decode<T, D, 2>(q, k, v, lengths, pmax, psum, pout, out, batch, q_heads, kv_heads, cap, splits, scale, stream);
-    case 4: return launch_decode<T, D, 4>(q, k, v, lengths, pmax, psum, pout, out, batch, q_heads, kv_heads, cap, splits, scale, stream);
-    case 8: return launch_decode<T, D, 8>(q, k, v, lengths, pmax, psum, pout, out, batch, q_heads, kv_heads, cap, splits, scale, stream);
+    case 1: return launch_decode<T, TQ, D, 1>(q, k, v, lengths, pmax, psum, pout, out, batch, q_heads, kv_heads, cap, splits, scale, stream);
+    case 2: return launch_decode<T, TQ, D, 2>(q, k, v, lengths, pmax, psum, pout, out, batch, q_heads, kv_heads, cap, splits, scale, stream);
+    case 4: return launch_decode<T, TQ, D, 4>(q, k, v, lengths, pmax, psum, pout, out, batch, q_heads, kv_heads, cap, splits, scale, stream);
+    case 8: return launch_decode<T, TQ, D, 8>(q, k, v, lengths, pmax, psum, pout, out, batch, q_heads, kv_heads, cap, splits, scale, stream);
   }
   return set_error(SFL_ERR_UNSUPPORTED, "decode_attention: unsupported GQA ratio %d", groups);
 }
 
-template <typename T>
+template <typename T, typename TQ>
 int dispatch_dim(int dim, int groups, const void* q, const void* k, const void* v,
                  const int32_t* lengths, float* pmax, float* psum, float* pout, void* out, int batch,
                  int q_heads, int kv_heads, int cap, int splits, float scale, hipStream_t stream) {
   switch (dim) {
-    case 32: return dispatch_groups<T, 32>(groups, q, k, v, lengths, pmax, psum, pout, out, batch, q_heads, kv_heads, cap, splits, scale, stream);
-    case 64: return dispatch_groups<T, 64>(groups, q, k, v, lengths, pmax, psum, pout, out, batch, q_heads, kv_heads, cap, splits, scale, stream);
-    case 128: return dispatch_groups<T, 128>(groups, q, k, v, lengths, pmax, psum, pout, out, batch, q_heads, kv_heads, cap, splits, scale, stream);
+    case 16: return dispatch_groups<T, TQ, 16>(groups, q, k, v, lengths, pmax, psum, pout, out, batch, q_heads, kv_heads, cap, splits, scale, stream);
+    case 32: return dispatch_groups<T, TQ, 32>(groups, q, k, v, lengths, pmax, psum, pout, out, batch, q_heads, kv_heads, cap, splits, scale, stream);
+    case 64: return dispatch_groups<T, TQ, 64>(groups, q, k, v, lengths, pmax, psum, pout, out, batch, q_heads, kv_heads, cap, splits, scale, stream);
+    case 128: return dispatch_groups<T, TQ, 128>(groups, q, k, v, lengths, pmax, psum, pout, out, batch, q_heads, kv_heads, cap, splits, scale, stream);
   }
   return set_error(SFL_ERR_UNSUPPORTED, "decode_attention: unsupported head dim %d", dim);
 }
@@ -258,7 +258,7 @@ extern "C" int sfl_decode_attention(const void* q, const void* k, const void* v,
                                     const int32_t* lengths, float* partial_max,
                                     float* partial_sum, float* partial_out, void* out, int batch,
                                     int q_heads, int kv_heads, int capacity, int head_dim,
-                                    int splits, float scale, int dtype, void* stream) {
+                                    int splits, float scale, int dtype, int io_dtype, void* stream) {
   using namespace sfl;
   if (!q || !k || !v || !lengths || !partial_max || !partial_sum || !partial_out || !out)
     return set_error(SFL_ERR_INVALID, "decode_attention: null pointer argument");
@@ -270,12 +270,20 @@ extern "C" int sfl_decode_attention(const void* q, const void* k, const void* v,
     return set_error(SFL_ERR_INVALID, "decode_attention: splits must be in [1, 1024]");
   if (!(scale > 0.f) || !__builtin_isfinite(scale))
     return set_error(SFL_ERR_INVALID, "decode_attention: scale must be finite and positive");
+  if (io_dtype != dtype && io_dtype != SFL_DTYPE_F32)
+    return set_error(SFL_ERR_UNSUPPORTED, "decode_attention: q/out dtype must equal the KV dtype or be F32");
   const int groups = q_heads / kv_heads;
+  const bool f32_io = io_dtype == SFL_DTYPE_F32;
   hipStream_t s = static_cast<hipStream_t>(stream);
+#define SFL_DECODE_ARGS head_dim, groups, q, k, v, lengths, partial_max, partial_sum, partial_out, out, \
+    batch, q_heads, kv_heads, capacity, splits, scale, s
   switch (dtype) {
-    case SFL_DTYPE_F32: return dispatch_dim<float>(head_dim, groups, q, k, v, lengths, partial_max, partial_sum, partial_out, out, batch, q_heads, kv_heads, capacity, splits, scale, s);
-    case SFL_DTYPE_BF16: return dispatch_dim<bf16_t>(head_dim, groups, q, k, v, lengths, partial_max, partial_sum, partial_out, out, batch, q_heads, kv_heads, capacity, splits, scale, s);
-    case SFL_DTYPE_F16: return dispatch_dim<f16_t>(head_dim, groups, q, k, v, lengths, partial_max, partial_sum, partial_out, out, batch, q_heads, kv_heads, capacity, splits, scale, s);
+    case SFL_DTYPE_F32: return dispatch_dim<float, float>(SFL_DECODE_ARGS);
+    case SFL_DTYPE_BF16:
+      return f32_io ? dispatch_dim<bf16_t, float>(SFL_DECODE_ARGS) : dispatch_dim<bf16_t, bf16_t>(SFL_DECODE_ARGS);
+    case SFL_DTYPE_F16:
+      return f32_io ? dispatch_dim<f16_t, float>(SFL_DECODE_ARGS) : dispatch_dim<f16_t, f16_t>(SFL_DECODE_ARGS);
   }
+#undef SFL_DECODE_ARGS
   return set_error(SFL_ERR_UNSUPPORTED, "decode_attention: unsupported dtype %d", dtype);
 }

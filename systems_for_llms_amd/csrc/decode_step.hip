@@ -1,0 +1,115 @@
+// Token-loop bookkeeping kernels: embedding gather and the greedy next-token step.
+//
+// The reference has no token loop (its forward always recomputes from
+// position 0, src/llmlab/model/transformer.py:121-139); its greedy
+// continuation is argmax(forward(ids)[:, -1]), and torch.argmax returns the
+// first maximal index. These kernels keep the whole loop on the device so a
+// decode step can be captured once and replayed: the next token, the position
+// and the attention lengths are advanced in place.
+#include "common.hpp"
+
+namespace sfl {
+namespace {
+
+__device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
+  return v > bv || (v == bv && i < bi);
+}
+
+// x[b, :] = emb[tokens[b, pos[b]], :] as fp32 (Embedding.forward, layers.py:68-70).
+template <typename T>
+__global__ __launch_bounds__(256) void embed_kernel(const int64_t* __restrict__ tokens, long stride,
+                                                    const int32_t* __restrict__ pos,
+                                                    const T* __restrict__ emb, float* __restrict__ x,
+                                                    int d) {
+  const int b = blockIdx.x;
+  const long id = tokens[b * stride + pos[b]];
+  const T* src = emb + id * d;
+  for (int i = threadIdx.x; i < d; i += blockDim.x) x[long(b) * d + i] = load_scalar<T>(src + i);
+}
+
+// One wave per sequence: finish the argmax over the lm_head tiles (lowest
+// index on ties), record it, pick the next token (the given one while the
+// sequence is still inside its prompt, else the argmax), gather its
+// embedding into x and advance pos/lengths by one.
+template <typename T>
+__global__ __launch_bounds__(64) void next_token_kernel(
+    const float* __restrict__ best_val, const int32_t* __restrict__ best_idx, int tiles, int batch,
+    int64_t* __restrict__ tokens, int64_t* __restrict__ predicted, long stride,
+    const int32_t* __restrict__ prompt_len, int32_t* __restrict__ pos, int32_t* __restrict__ lengths,
+    const T* __restrict__ emb, float* __restrict__ x, int d, int cap) {
+  const int b = blockIdx.x;
+  const int lane = threadIdx.x;
+  float bv = -INFINITY;
+  int bi = 0x7fffffff;
+  for (int t = lane; t < tiles; t += kWave) {
+    const float v = best_val[long(t) * batch + b];
+    const int i = best_idx[long(t) * batch + b];
+    if (better(v, i, bv, bi)) { bv = v; bi = i; }
+  }
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    const float ov = __shfl_xor(bv, m, kWave);
+    const int oi = __shfl_xor(bi, m, kWave);
+    if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+  }
+  const int p = pos[b];
+  const int np = p + 1;
+  if (np >= cap) return;  // context full: the host never steps past capacity
+  const bool forced = np < prompt_len[b];
+  const long tok = forced ? tokens[b * stride + np] : long(bi);
+  const T* src = emb + tok * d;
+  for (int i = lane; i < d; i += kWave) x[long(b) * d + i] = load_scalar<T>(src + i);
+  if (lane == 0) {
+    predicted[b * stride + np] = bi;
+    if (!forced) tokens[b * stride + np] = bi;
+    pos[b] = np;
+    lengths[b] = np + 1;
+  }
+}
+
+}  // namespace
+}  // namespace sfl
+
+using namespace sfl;
+
+extern "C" int sfl_embedding_gather(const int64_t* tokens, long token_stride, const int32_t* pos,
+                                    const void* emb, float* x, int batch, int d_model, int dtype,
+                                    void* stream) {
+  if (!tokens || !pos || !emb || !x) return set_error(SFL_ERR_INVALID, "embedding_gather: null pointer argument");
+  if (batch < 1 || d_model < 1) return set_error(SFL_ERR_INVALID, "embedding_gather: sizes must be positive");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == SFL_DTYPE_BF16)
+    hipLaunchKernelGGL(embed_kernel<bf16_t>, dim3(batch), dim3(256), 0, s, tokens, token_stride, pos,
+                       static_cast<const bf16_t*>(emb), x, d_model);
+  else if (dtype == SFL_DTYPE_F32)
+    hipLaunchKernelGGL(embed_kernel<float>, dim3(batch), dim3(256), 0, s, tokens, token_stride, pos,
+                       static_cast<const float*>(emb), x, d_model);
+  else
+    return set_error(SFL_ERR_UNSUPPORTED, "embedding_gather: model dtype must be F32 or BF16");
+  return check_launch("embedding_gather");
+}
+
+extern "C" int sfl_next_token(const float* best_val, const int32_t* best_idx, int tiles,
+                              int64_t* tokens, int64_t* predicted, long token_stride,
+                              const int32_t* prompt_len, int32_t* pos, int32_t* lengths,
+                              const void* emb, float* x, int batch, int d_model, int capacity,
+                              int dtype, void* stream) {
+  if (!best_val || !best_idx || !tokens || !predicted || !prompt_len || !pos || !lengths || !emb || !x)
+    return set_error(SFL_ERR_INVALID, "next_token: null pointer argument");
+  if (batch < 1 || tiles < 1 || d_model < 1 || capacity < 1)
+    return set_error(SFL_ERR_INVALID, "next_token: sizes must be positive");
+  if (token_stride < capacity)
+    return set_error(SFL_ERR_INVALID, "next_token: token_stride must be >= capacity");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == SFL_DTYPE_BF16)
+    hipLaunchKernelGGL(next_token_kernel<bf16_t>, dim3(batch), dim3(64), 0, s, best_val, best_idx, tiles,
+                       batch, tokens, predicted, token_stride, prompt_len, pos, lengths,
+                       static_cast<const bf16_t*>(emb), x, d_model, capacity);
+  else if (dtype == SFL_DTYPE_F32)
+    hipLaunchKernelGGL(next_token_kernel<float>, dim3(batch), dim3(64), 0, s, best_val, best_idx, tiles,
+                       batch, tokens, predicted, token_stride, prompt_len, pos, lengths,
+                       static_cast<const float*>(emb), x, d_model, capacity);
+  else
+    return set_error(SFL_ERR_UNSUPPORTED, "next_token: model dtype must be F32 or BF16");
+  return check_launch("next_token");
+}

@@ -10,7 +10,7 @@ one prepared operation race on its scratch (``kernel.py:1-6``).
 
 Differences, all widenings of the reference contract:
 
-* head dimension 32 is accepted besides 64 and 128, and fp32 besides fp16/bf16
+* head dimensions 16 and 32 are accepted besides 64 and 128, and fp32 besides fp16/bf16
   (the 22.7M parity model has 16 heads of 32 and runs in fp32);
 * ``splits=None`` (the default here) picks the split count from the shape; an
   integer in [1, 128] is honoured exactly as in the reference;
@@ -27,7 +27,7 @@ import torch
 
 from . import _lib
 
-SUPPORTED_DIMS = (32, 64, 128)
+SUPPORTED_DIMS = (16, 32, 64, 128)
 SUPPORTED_GROUPS = (1, 2, 4, 8)
 MAX_SPLITS = 128
 
@@ -45,7 +45,7 @@ def _validate(q, k, v, lengths, splits):
     if kv_heads <= 0 or capacity <= 0 or query_heads % kv_heads:
         raise ValueError("query heads must be divisible by positive KV heads")
     if dim not in SUPPORTED_DIMS or query_heads // kv_heads not in SUPPORTED_GROUPS:
-        raise ValueError("supported head dimensions are 32/64/128 and GQA ratios 1/2/4/8")
+        raise ValueError("supported head dimensions are 16/32/64/128 and GQA ratios 1/2/4/8")
     if q.dtype not in _lib.DTYPE_CODES or k.dtype != q.dtype or v.dtype != q.dtype:
         raise TypeError("Q/K/V must have the same FP16, BF16 or FP32 dtype")
     if not q.is_cuda or any(x.device != q.device for x in (k, v, lengths)):
@@ -93,7 +93,7 @@ class PreparedDecode:
                   self.lengths.data_ptr(), self.partial_max.data_ptr(), self.partial_sum.data_ptr(),
                   self.partial_output.data_ptr(), self.output.data_ptr(), batch, heads, kv_heads,
                   capacity, dim, self.splits, self.scale, _lib.dtype_code(self.q.dtype),
-                  _lib.stream_handle(self.q.device))
+                  _lib.dtype_code(self.q.dtype), _lib.stream_handle(self.q.device))
         return self.output
 
     @property

@@ -1,0 +1,193 @@
+"""Device-resident greedy token loop for ``TransformerLM`` on gfx950.
+
+A ``DecodeSession`` owns everything one decode step touches -- packed weights,
+the KV cache ``[L, B, H, cap, dk]`` in the model dtype, the fp32 residual
+stream, scratch, and the token/position/length state -- and issues one step as
+a fixed sequence of C-ABI launches on the current stream:
+
+    per layer:  rmsnorm_qkv_rope_append -> decode_attention (split-KV + merge)
+                -> linear_residual (output_proj) -> rmsnorm_swiglu
+                -> linear_residual (w2)
+    then:       rmsnorm_lm_head (+ tile argmax) -> next_token
+
+All step state lives in device memory and is advanced by ``next_token``, so a
+step has no host inputs: it is captured once into a HIP graph and replayed.
+While a sequence is inside its prompt, ``next_token`` keeps the prompt token
+(teacher forcing) and still records the model's argmax in ``predicted``.
+
+The reference has no KV cache or token loop (``transformer.py:121-139``
+recomputes from position 0); this loop reproduces
+``argmax(forward(ids)[:, -1])`` one position at a time.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+from .decode import auto_splits
+
+ROWS_PER_LAUNCH = 16  # batch rows per decode-step GEMV launch
+
+
+class DecodeSession:
+    def __init__(self, model, batch: int, capacity: int | None = None, *, splits: int | None = None,
+                 record_logits: bool = False):
+        param = model.lm_head.weight
+        if param.device.type != "cuda":
+            raise RuntimeError("systems_for_llms_amd runs on the GPU: move the model to a HIP device first")
+        if param.dtype not in (torch.float32, torch.bfloat16):
+            raise TypeError("model dtype must be float32 or bfloat16")
+        _lib.lib()
+        cap = capacity or model.context_length
+        if not 0 < cap <= model.context_length:
+            raise ValueError("capacity must be in [1, context_length]")
+        self.model = model
+        self.device = param.device
+        self.dtype = param.dtype
+        self.code = _lib.dtype_code(self.dtype)
+        self.batch, self.cap = batch, cap
+        d, h, f, v, n = model.d_model, model.num_heads, model.d_ff, model.vocab_size, model.num_layers
+        self.d, self.heads, self.dk, self.d_ff, self.vocab, self.layers = d, h, d // h, f, v, n
+        dev, dt = self.device, self.dtype
+
+        from .model import rope_tables
+        cos, sin = rope_tables(model.theta, self.dk, cap)
+        self.cos, self.sin = cos.to(dev), sin.to(dev)
+        self.wqkv = [torch.cat([blk.attn.q_proj.weight, blk.attn.k_proj.weight, blk.attn.v_proj.weight])
+                     .contiguous() for blk in model.layers]
+        self.k_cache = torch.zeros((n, batch, h, cap, self.dk), device=dev, dtype=dt)
+        self.v_cache = torch.zeros_like(self.k_cache)
+        self.x = torch.zeros((batch, d), device=dev, dtype=torch.float32)
+        # Activations stay fp32; only weights and the KV cache use the model dtype.
+        self.q = torch.zeros((batch, h, self.dk), device=dev, dtype=torch.float32)
+        self.attn = torch.zeros((batch, h, self.dk), device=dev, dtype=torch.float32)
+        self.hidden = torch.zeros((batch, f), device=dev, dtype=torch.float32)
+        self.splits = splits or auto_splits(batch, h, cap)
+        self.pmax = torch.empty((batch, h, self.splits), device=dev, dtype=torch.float32)
+        self.psum = torch.empty_like(self.pmax)
+        self.pout = torch.empty((batch, h, self.splits, self.dk), device=dev, dtype=torch.float32)
+        self.tiles = _lib.lib().sfl_lm_head_tiles(v)
+        self.best_val = torch.empty((self.tiles, batch), device=dev, dtype=torch.float32)
+        self.best_idx = torch.empty((self.tiles, batch), device=dev, dtype=torch.int32)
+        self.tokens = torch.zeros((batch, cap), device=dev, dtype=torch.int64)
+        self.predicted = torch.full((batch, cap), -1, device=dev, dtype=torch.int64)
+        self.pos = torch.zeros(batch, device=dev, dtype=torch.int32)
+        self.lengths = torch.ones(batch, device=dev, dtype=torch.int32)
+        self.prompt_len = torch.ones(batch, device=dev, dtype=torch.int32)
+        self.logits = (torch.zeros((batch, cap, v), device=dev, dtype=torch.float32)
+                       if record_logits else None)
+        self.graph = None
+        self._calls = self._plan()
+
+    # -- launch plan --------------------------------------------------------
+    def _plan(self):
+        """The ctypes calls of one step, with every argument but the stream bound."""
+        lib = _lib.lib()
+        d, h, dk, f, v, cap, code = self.d, self.heads, self.dk, self.d_ff, self.vocab, self.cap, self.code
+        m = self.model
+        calls = []
+        scale = float(dk) ** -0.5
+        row_chunks = [(r, min(ROWS_PER_LAUNCH, self.batch - r)) for r in range(0, self.batch, ROWS_PER_LAUNCH)]
+        for layer, blk in enumerate(m.layers):
+            kc, vc = self.k_cache[layer], self.v_cache[layer]
+            for r, rows in row_chunks:
+                calls.append((lib.sfl_rmsnorm_qkv_rope_append, (
+                    self.x[r].data_ptr(), blk.attn_norm.weight.data_ptr(), self.wqkv[layer].data_ptr(),
+                    self.cos.data_ptr(), self.sin.data_ptr(), self.pos[r:].data_ptr(),
+                    self.q[r].data_ptr(), kc[r].data_ptr(), vc[r].data_ptr(), rows, d, h, cap, code)))
+            calls.append((lib.sfl_decode_attention, (
+                self.q.data_ptr(), kc.data_ptr(), vc.data_ptr(), self.lengths.data_ptr(),
+                self.pmax.data_ptr(), self.psum.data_ptr(), self.pout.data_ptr(), self.attn.data_ptr(),
+                self.batch, h, h, cap, dk, self.splits, scale, code, _lib.DTYPE_CODES[torch.float32])))
+            for r, rows in row_chunks:
+                calls.append((lib.sfl_linear_residual, (
+                    self.attn[r].data_ptr(), blk.attn.output_proj.weight.data_ptr(), self.x[r].data_ptr(),
+                    self.x[r].data_ptr(), rows, d, d, code)))
+                calls.append((lib.sfl_rmsnorm_swiglu, (
+                    self.x[r].data_ptr(), blk.ffn_norm.weight.data_ptr(), blk.ffn.w1.weight.data_ptr(),
+                    blk.ffn.w3.weight.data_ptr(), self.hidden[r].data_ptr(), rows, d, f, code)))
+                calls.append((lib.sfl_linear_residual, (
+                    self.hidden[r].data_ptr(), blk.ffn.w2.weight.data_ptr(), self.x[r].data_ptr(),
+                    self.x[r].data_ptr(), rows, d, f, code)))
+        for r, rows in row_chunks:
+            logits = self.logits[r].data_ptr() if self.logits is not None else None
+            calls.append((lib.sfl_rmsnorm_lm_head, (
+                self.x[r].data_ptr(), m.ln_final.weight.data_ptr(), m.lm_head.weight.data_ptr(),
+                logits, cap * v, self.pos[r:].data_ptr(), v, self.best_val[:, r:].data_ptr(),
+                self.best_idx[:, r:].data_ptr(), self.batch, rows, d, v, code)))
+        calls.append((lib.sfl_next_token, (
+            self.best_val.data_ptr(), self.best_idx.data_ptr(), self.tiles, self.tokens.data_ptr(),
+            self.predicted.data_ptr(), cap, self.prompt_len.data_ptr(), self.pos.data_ptr(),
+            self.lengths.data_ptr(), m.token_embeddings.weight.data_ptr(), self.x.data_ptr(),
+            self.batch, d, cap, code)))
+        return calls
+
+    # -- state --------------------------------------------------------------
+    @torch.no_grad()
+    def start(self, prompt: torch.Tensor, forced_length: int | None = None) -> None:
+        """Load ``prompt [B, T]`` and set every row to position 0.
+
+        Positions below ``forced_length`` (default T) keep the given token; the
+        step at position p writes the next token at p + 1.
+        """
+        if prompt.shape[0] != self.batch or not 0 < prompt.shape[1] <= self.cap:
+            raise ValueError("prompt must be [batch, T] with 0 < T <= capacity")
+        low, high = torch.aminmax(prompt)
+        if low.item() < 0 or high.item() >= self.vocab:
+            raise ValueError("token ids must be in [0, vocab_size)")
+        self.tokens.zero_()
+        self.tokens[:, :prompt.shape[1]] = prompt.to(self.device)
+        self.predicted.fill_(-1)
+        self.pos.zero_()
+        self.lengths.fill_(1)
+        self.prompt_len.fill_(forced_length or prompt.shape[1])
+        stream = _lib.stream_handle(self.device)
+        _lib.call("sfl_embedding_gather", self.tokens.data_ptr(), self.cap, self.pos.data_ptr(),
+                  self.model.token_embeddings.weight.data_ptr(), self.x.data_ptr(), self.batch,
+                  self.d, self.code, stream)
+
+    def set_position(self, position: int) -> None:
+        """Rewind/advance every row to ``position`` (the cache below it is kept) and re-embed."""
+        self.pos.fill_(position)
+        self.lengths.fill_(position + 1)
+        _lib.call("sfl_embedding_gather", self.tokens.data_ptr(), self.cap, self.pos.data_ptr(),
+                  self.model.token_embeddings.weight.data_ptr(), self.x.data_ptr(), self.batch,
+                  self.d, self.code, _lib.stream_handle(self.device))
+
+    # -- execution ----------------------------------------------------------
+    def step(self) -> None:
+        """Launch one decode step on the current stream (no host synchronisation)."""
+        stream = _lib.stream_handle(self.device)
+        for fn, args in self._calls:
+            status = fn(*args, stream)
+            if status != 0:
+                raise RuntimeError(f"{fn.__name__} failed ({status}): "
+                                   f"{_lib.lib().sfl_last_error().decode(errors='replace')}")
+
+    def capture(self, steps_per_graph: int = 1) -> torch.cuda.CUDAGraph:
+        """Capture ``steps_per_graph`` steps into one HIP graph (replayable, state on device)."""
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for _ in range(steps_per_graph):
+                self.step()
+        self.graph, self.graph_steps = graph, steps_per_graph
+        return graph
+
+    def run(self, steps: int, use_graph: bool = False) -> None:
+        """Advance every row by ``steps`` positions (graph replays when ``use_graph``)."""
+        if steps <= 0:
+            return
+        if not use_graph:
+            for _ in range(steps):
+                self.step()
+            return
+        # Warm up eagerly once (first-call kernel attributes), then capture.
+        self.step()
+        steps -= 1
+        if steps == 0:
+            return
+        if self.graph is None or self.graph_steps != 1:
+            self.capture(1)  # capturing records the launches without executing them
+        for _ in range(steps):
+            self.graph.replay()
