@@ -11,9 +11,10 @@
  *
  * Tensor layouts are row-major and contiguous unless a stride is passed.
  * Element types are selected by an SFL_DTYPE_* code. In the decode-step
- * entry points weights and the KV cache use the model dtype while
- * activations (x, q, attention output, SwiGLU hidden) are fp32; with bf16
- * weights each activation is split into two bf16 halves for the MFMAs.
+ * entry points weights and the KV cache use the model dtype; the residual
+ * stream x and q are fp32; the GEMV inputs that other kernels produce (the
+ * attention output, the SwiGLU hidden state) are fp32 for F32 models and
+ * SFL_DTYPE_BF16X2 for BF16 models.
  */
 #ifndef SFL_H_
 #define SFL_H_
@@ -28,6 +29,11 @@ enum {
   SFL_DTYPE_F32 = 0,
   SFL_DTYPE_BF16 = 1,
   SFL_DTYPE_F16 = 2,
+  /* Activation format of the bf16 decode GEMVs, 4 bytes per value: each group
+   * of 8 consecutive values is stored as 8 bf16 "hi" halves (the values
+   * truncated to bf16) followed by 8 bf16 "lo" halves (the remainders
+   * truncated to bf16); hi + lo keeps ~16 mantissa bits. */
+  SFL_DTYPE_BF16X2 = 3,
 };
 
 enum {
@@ -57,13 +63,14 @@ const char* sfl_last_error(void);
  * The cache is partitioned by capacity into `splits` chunks of
  * ceil(cap/splits) keys (decode.cu:50-52); chunks past a row's length do no
  * work. D in {16, 32, 64, 128}; Hq/Hkv in {1, 2, 4, 8}; splits in [1, 1024].
- * dtype: element type of k and v (F32, BF16 or F16); io_dtype: element type
- * of q and out, either the same as dtype or F32. Softmax state is fp32.
+ * kv_dtype: element type of k and v (F32, BF16 or F16); q_dtype: kv_dtype or
+ * F32; out_dtype: kv_dtype, F32 or BF16X2. Softmax state is fp32.
  */
 int sfl_decode_attention(const void* q, const void* k, const void* v, const int32_t* lengths,
                          float* partial_max, float* partial_sum, float* partial_out, void* out,
                          int batch, int q_heads, int kv_heads, int capacity, int head_dim,
-                         int splits, float scale, int dtype, int io_dtype, void* stream);
+                         int splits, float scale, int kv_dtype, int q_dtype, int out_dtype,
+                         void* stream);
 
 
 /* ---- decode step of the llmlab decoder (model dtype F32 or BF16) ----------
@@ -88,7 +95,8 @@ int sfl_rmsnorm_qkv_rope_append(const float* x, const void* norm_w, const void* 
                                 int d_model, int heads, int capacity, int dtype, void* stream);
 
 /*
- * x_out = x + act @ w^T (act [batch, k] fp32, w [n, k], x/x_out fp32 [batch, n],
+ * x_out = x + act @ w^T (act [batch, k]: fp32 for F32 weights, BF16X2 for
+ * BF16 weights; w [n, k]; x/x_out fp32 [batch, n],
  * x_out may alias x). Replaces output_proj + residual and ffn.w2 + residual
  * (transformer.py:46-47, attention.py:199-203, layers.py:114-115).
  */
@@ -96,7 +104,8 @@ int sfl_linear_residual(const void* act, const void* w, const float* x, float* x
                         int n, int k, int dtype, void* stream);
 
 /*
- * h = silu(RMSNorm(x) @ w1^T) * (RMSNorm(x) @ w3^T), h [batch, d_ff] fp32.
+ * h = silu(RMSNorm(x) @ w1^T) * (RMSNorm(x) @ w3^T), h [batch, d_ff] in the
+ * GEMV activation format (fp32, or BF16X2 for BF16 weights).
  * Replaces ffn_norm + SwiGLU's w1/w3 half (transformer.py:47, layers.py:73-115).
  */
 int sfl_rmsnorm_swiglu(const float* x, const void* norm_w, const void* w1, const void* w3,

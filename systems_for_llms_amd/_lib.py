@@ -16,11 +16,12 @@ import torch
 LIB_PATH = Path(__file__).resolve().parent / "lib" / "libsfl.so"
 
 DTYPE_CODES = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
+DTYPE_BF16X2 = 3  # split-bf16 activation format of the bf16 decode GEMVs
 
 P = c_void_p
 SIGNATURES: dict[str, list] = {
     "sfl_decode_attention": [P, P, P, P, P, P, P, P, c_int, c_int, c_int, c_int, c_int, c_int,
-                             c_float, c_int, c_int, P],
+                             c_float, c_int, c_int, c_int, P],
     "sfl_rmsnorm_qkv_rope_append": [P, P, P, P, P, P, P, P, P, c_int, c_int, c_int, c_int, c_int, P],
     "sfl_linear_residual": [P, P, P, P, c_int, c_int, c_int, c_int, P],
     "sfl_rmsnorm_swiglu": [P, P, P, P, P, c_int, c_int, c_int, c_int, P],

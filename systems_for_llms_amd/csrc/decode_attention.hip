@@ -19,6 +19,9 @@
 namespace sfl {
 namespace {
 
+// Tag type of the split-bf16 output writer (see store_out<split_t>).
+struct split_t {};
+
 template <typename T, int D, int G>
 struct DecodeShape {
   static constexpr int EPL = vec_elems<T>();  // elements per lane per load
@@ -29,36 +32,54 @@ struct DecodeShape {
   static_assert(LPT >= 1 && LPT <= kWave, "head dim does not fit a wave");
 };
 
-template <typename T, typename TQ, int D, int G>
-__global__ __launch_bounds__(256) void decode_partial_kernel(
+template <typename TO>
+__device__ __forceinline__ void store_out(void* out, long f, float v);
+
+// One workgroup of W waves per (batch, kv head, split). The split's keys are
+// divided among the waves; each wave streams its range with the per-slot
+// online softmax, the slots are merged with shuffles, and the W wave states
+// are merged through LDS. With one split the workgroup writes the final
+// output; otherwise it writes its (max, sum, numerator) partial for the merge
+// kernel.
+template <typename T, typename TQ, typename TO, int D, int G, int W>
+__global__ __launch_bounds__(W * kWave) void decode_attn_kernel(
     const TQ* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
     const int32_t* __restrict__ lengths, float* __restrict__ pmax, float* __restrict__ psum,
-    float* __restrict__ pout, int batch, int kv_heads, int cap, int splits, int chunk,
+    float* __restrict__ pout, void* __restrict__ out, int kv_heads, int cap, int splits, int chunk,
     float qscale) {
   using S = DecodeShape<T, D, G>;
   constexpr int EPL = S::EPL, LPT = S::LPT, TPL = S::TPL, NL = S::NL, TILE = S::TILE;
+  __shared__ float sm[W][G][D + 2];
   const int wave = threadIdx.x / kWave;
   const int lane = threadIdx.x % kWave;
-  const long item = long(blockIdx.x) * 4 + wave;
-  if (item >= long(batch) * kv_heads * splits) return;
-  const int split = int(item % splits);
-  const long bh = item / splits;
+  const int split = int(blockIdx.x % splits);
+  const long bh = blockIdx.x / splits;
   const int h = int(bh % kv_heads);
   const int b = int(bh / kv_heads);
-  const int len = min(max(lengths[b], 0), cap);
-  const int begin = split * chunk;
-  if (begin >= len) return;  // the merge reads only chunks below the length
-  const int end = min(len, begin + chunk);
+  const int q_heads = kv_heads * G;
   const int slot = lane / LPT;
   const int dg = lane % LPT;
-  const int q_heads = kv_heads * G;
 
+  // The query does not depend on the length: issue its loads first.
   float qv[G][EPL];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     const TQ* qp = q + (long(b) * q_heads + h * G + g) * D + dg * EPL;
 #pragma unroll
-    for (int e = 0; e < EPL; ++e) qv[g][e] = load_scalar<TQ>(qp + e) * qscale;
+    for (int e = 0; e < EPL; ++e) qv[g][e] = load_scalar<TQ>(qp + e);
+  }
+  const int len = min(max(lengths[b], 0), cap);
+  const int begin = split * chunk;
+  if (splits > 1 && begin >= len) return;  // the merge reads only chunks below the length
+  const int end = min(len, begin + chunk);
+  const int sub = (max(0, end - begin) + W - 1) / W;
+  const int wbegin = begin + wave * sub;
+  const int wend = min(end, wbegin + sub);
+
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) qv[g][e] *= qscale;
   }
   float m[G], l[G], acc[G][EPL];
 #pragma unroll
@@ -73,7 +94,7 @@ __global__ __launch_bounds__(256) void decode_partial_kernel(
   const T* kb = k + row0 * D + dg * EPL;
   const T* vb = v + row0 * D + dg * EPL;
 
-  for (int t0 = begin; t0 < end; t0 += TILE) {
+  for (int t0 = wbegin; t0 < wend; t0 += TILE) {
     uint4 kr[NL], vr[NL];
 #pragma unroll
     for (int i = 0; i < NL; ++i) {
@@ -90,7 +111,7 @@ __global__ __launch_bounds__(256) void decode_partial_kernel(
     for (int i = 0; i < NL; ++i) {
       float kf[EPL];
       unpack16<T>(kr[i], kf);
-      const bool valid = t0 + i * TPL + slot < end;
+      const bool valid = t0 + i * TPL + slot < wend;
 #pragma unroll
       for (int g = 0; g < G; ++g) {
         float d = 0.f;
@@ -152,26 +173,76 @@ __global__ __launch_bounds__(256) void decode_partial_kernel(
       m[g] = mn;
     }
   }
-  if (slot != 0) return;
+  if (slot == 0) {
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
-    const long row = (long(b) * q_heads + h * G + g) * splits + split;
-    float4* dst = reinterpret_cast<float4*>(pout + row * D + dg * EPL);
+    for (int g = 0; g < G; ++g) {
 #pragma unroll
-    for (int e = 0; e < EPL; e += 4) dst[e / 4] = make_float4(acc[g][e], acc[g][e + 1], acc[g][e + 2], acc[g][e + 3]);
-    if (dg == 0) {
-      pmax[row] = m[g];
-      psum[row] = l[g];
+      for (int e = 0; e < EPL; ++e) sm[wave][g][dg * EPL + e] = acc[g][e];
+      if (dg == 0) {
+        sm[wave][g][D] = m[g];
+        sm[wave][g][D + 1] = l[g];
+      }
+    }
+  }
+  __syncthreads();
+
+  // Merge the W waves: one thread per (query head, dim).
+  for (int t = threadIdx.x; t < G * D; t += W * kWave) {
+    const int g = t / D, d = t % D;
+    float top = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < W; ++w) top = fmaxf(top, sm[w][g][D]);
+    float den = 0.f, num = 0.f;
+    if (top != -INFINITY) {
+#pragma unroll
+      for (int w = 0; w < W; ++w) {
+        const float mw = sm[w][g][D];
+        const float c = mw == -INFINITY ? 0.f : exp2f(mw - top);
+        den = fmaf(c, sm[w][g][D + 1], den);
+        num = fmaf(c, sm[w][g][d], num);
+      }
+    }
+    const long qrow = long(b) * q_heads + h * G + g;
+    if (splits == 1) {
+      store_out<TO>(out, qrow * D + d, den > 0.f ? num / den : 0.f);
+    } else {
+      const long prow = qrow * splits + split;
+      pout[prow * D + d] = num;
+      if (d == 0) {
+        pmax[prow] = top;
+        psum[prow] = den;
+      }
     }
   }
 }
 
+// Output writers of the merge: the KV dtype, fp32, or the split-bf16
+// activation format read by the bf16 GEMVs (groups of 8 values stored as 8
+// truncated-bf16 "hi" halves followed by 8 "lo" halves of the remainders).
+template <typename TO>
+__device__ __forceinline__ void store_out(void* out, long f, float v) {
+  store_scalar<TO>(static_cast<TO*>(out) + f, v);
+}
+template <>
+__device__ __forceinline__ void store_out<split_t>(void* out, long f, float v) {
+  const uint32_t hb = __float_as_uint(v) & 0xffff0000u;
+  const uint32_t lb = __float_as_uint(v - __uint_as_float(hb)) & 0xffff0000u;
+  uint16_t* g = reinterpret_cast<uint16_t*>(static_cast<unsigned char*>(out) + (f / 8) * 32) + f % 8;
+  g[0] = uint16_t(hb >> 16);
+  g[8] = uint16_t(lb >> 16);
+}
+
 // One wave per (batch, query head): combine the chunks below the row's length.
-template <typename T, int D>
+// Every load of a round of up to 64 chunks (their max, sum and numerators) is
+// issued before any is used, so a merge of <= 64 chunks costs one round trip.
+// Lane s holds chunk s's max and sum; the numerators are weighted by shuffles.
+template <typename TO, int D>
 __global__ __launch_bounds__(256) void decode_merge_kernel(
     const float* __restrict__ pmax, const float* __restrict__ psum, const float* __restrict__ pout,
-    const int32_t* __restrict__ lengths, T* __restrict__ out, int batch, int q_heads, int cap,
+    const int32_t* __restrict__ lengths, void* __restrict__ out, int batch, int q_heads, int cap,
     int splits, int chunk) {
+  constexpr int DPL = (D + kWave - 1) / kWave;  // dims per lane
+  constexpr int kRound = 16;                     // numerator loads in flight per lane and dim
   const int wave = threadIdx.x / kWave;
   const int lane = threadIdx.x % kWave;
   const long row = long(blockIdx.x) * 4 + wave;
@@ -181,74 +252,138 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(
   const int n = (len + chunk - 1) / chunk;
   const float* rm = pmax + row * splits;
   const float* rl = psum + row * splits;
-  float top = -INFINITY;
-  for (int s = lane; s < n; s += kWave) top = fmaxf(top, rm[s]);
-  top = wave_max(top);
-  float den = 0.f;
-  if (top != -INFINITY) {
-    for (int s = lane; s < n; s += kWave) {
-      const float ms = rm[s];
-      den += (ms == -INFINITY ? 0.f : exp2f(ms - top)) * rl[s];
+  const float* ro = pout + row * splits * D;
+  float top = -INFINITY, den = 0.f;
+  float num[DPL];
+#pragma unroll
+  for (int i = 0; i < DPL; ++i) num[i] = 0.f;
+  for (int s0 = 0; s0 < n; s0 += kRound) {
+    // Unconditional loads from clamped indices; masked after they land.
+    const int s = s0 + (lane % kRound);
+    const bool ok = s < n;
+    const float ms_raw = rm[min(s, n - 1)];
+    const float ls_raw = rl[min(s, n - 1)];
+    float part[kRound][DPL];
+#pragma unroll
+    for (int j = 0; j < kRound; ++j) {
+#pragma unroll
+      for (int i = 0; i < DPL; ++i)
+        part[j][i] = ro[long(min(s0 + j, n - 1)) * D + min(lane + i * kWave, D - 1)];
     }
+    const float ms = ok ? ms_raw : -INFINITY;
+    const float ls = ok ? ls_raw : 0.f;
+#pragma unroll
+    for (int j = 0; j < kRound; ++j) {
+#pragma unroll
+      for (int i = 0; i < DPL; ++i)
+        if (s0 + j >= n) part[j][i] = 0.f;
+    }
+    // Rescale the running state to the new maximum, then add this round.
+    const float round_top = wave_max(ms);
+    const float nt = fmaxf(top, round_top);
+    if (nt == -INFINITY) continue;
+    const float keep = top == -INFINITY ? 0.f : exp2f(top - nt);
+    const float w = ms == -INFINITY ? 0.f : exp2f(ms - nt);
+    den = den * keep + (lane < kRound ? w * ls : 0.f);
+#pragma unroll
+    for (int i = 0; i < DPL; ++i) num[i] *= keep;
+#pragma unroll
+    for (int j = 0; j < kRound; ++j) {
+      const float wj = __shfl(w, j, kWave);
+#pragma unroll
+      for (int i = 0; i < DPL; ++i) num[i] = fmaf(wj, part[j][i], num[i]);
+    }
+    top = nt;
   }
   den = wave_sum(den);
 #pragma unroll
-  for (int d = lane; d < D; d += kWave) {
-    float num = 0.f;
-    if (top != -INFINITY) {
-      for (int s = 0; s < n; ++s) {
-        const float ms = rm[s];
-        const float w = ms == -INFINITY ? 0.f : exp2f(ms - top);
-        num = fmaf(w, pout[(row * splits + s) * D + d], num);
-      }
-    }
-    store_scalar<T>(out + row * D + d, den > 0.f ? num / den : 0.f);
+  for (int i = 0; i < DPL; ++i) {
+    const int d = lane + i * kWave;
+    if (d < D) store_out<TO>(out, row * D + d, den > 0.f ? num[i] / den : 0.f);
   }
 }
 
-template <typename T, typename TQ, int D, int G>
-int launch_decode(const void* q, const void* k, const void* v, const int32_t* lengths, float* pmax,
-                  float* psum, float* pout, void* out, int batch, int q_heads, int kv_heads,
-                  int cap, int splits, float scale, hipStream_t stream) {
+template <typename TO, int D>
+int launch_merge(const float* pmax, const float* psum, const float* pout, const int32_t* lengths, void* out,
+                 int batch, int q_heads, int cap, int splits, hipStream_t stream) {
   const int chunk = (cap + splits - 1) / splits;
-  const long items = long(batch) * kv_heads * splits;
   const long rows = long(batch) * q_heads;
-  hipLaunchKernelGGL((decode_partial_kernel<T, TQ, D, G>), dim3(unsigned((items + 3) / 4)), dim3(256), 0,
-                     stream, static_cast<const TQ*>(q), static_cast<const T*>(k),
-                     static_cast<const T*>(v), lengths, pmax, psum, pout, batch, kv_heads, cap,
-                     splits, chunk, scale * kLog2e);
-  int rc = check_launch("decode_partial");
-  if (rc) return rc;
-  hipLaunchKernelGGL((decode_merge_kernel<TQ, D>), dim3(unsigned((rows + 3) / 4)), dim3(256), 0, stream,
-                     pmax, psum, pout, lengths, static_cast<TQ*>(out), batch, q_heads, cap, splits,
-                     chunk);
+  hipLaunchKernelGGL((decode_merge_kernel<TO, D>), dim3(unsigned((rows + 3) / 4)), dim3(256), 0, stream,
+                     pmax, psum, pout, lengths, out, batch, q_heads, cap, splits, chunk);
   return check_launch("decode_merge");
 }
 
-template <typename T, typename TQ, int D>
-int dispatch_groups(int groups, const void* q, const void* k, const void* v, const int32_t* lengths,
-                    float* pmax, float* psum, float* pout, void* out, int batch, int q_heads,
-                    int kv_heads, int cap, int splits, float scale, hipStream_t stream) {
-  switch (groups) {
-    case 1: return launch_decode<T, TQ, D, 1>(q, k, v, lengths, pmax, psum, pout, out, batch, q_heads, kv_heads, cap, splits, scale, stream);
-    case 2: return launch_decode<T, TQ, D, 2>(q, k, v, lengths, pmax, psum, pout, out, batch, q_heads, kv_heads, cap, splits, scale, stream);
-    case 4: return launch_decode<T, TQ, D, 4>(q, k, v, lengths, pmax, psum, pout, out, batch, q_heads, kv_heads, cap, splits, scale, stream);
-    case 8: return launch_decode<T, TQ, D, 8>(q, k, v, lengths, pmax, psum, pout, out, batch, q_heads, kv_heads, cap, splits, scale, stream);
-  }
-  return set_error(SFL_ERR_UNSUPPORTED, "decode_attention: unsupported GQA ratio %d", groups);
+struct DecodeCall {
+  const void *q, *k, *v;
+  const int32_t* lengths;
+  float *pmax, *psum, *pout;
+  void* out;
+  int batch, q_heads, kv_heads, cap, dim, splits;
+  float scale;
+  hipStream_t stream;
+};
+
+// Waves per workgroup: as many as keep the kernel within the register budget
+// of W waves per CU-quarter (<= 128 VGPRs at W = 16).
+template <typename T, int D, int G> constexpr int waves_for() {
+  return (G == 1 && D <= 64) ? 16 : ((G <= 2 && D <= 128) ? 8 : 4);
 }
 
-template <typename T, typename TQ>
-int dispatch_dim(int dim, int groups, const void* q, const void* k, const void* v,
-                 const int32_t* lengths, float* pmax, float* psum, float* pout, void* out, int batch,
-                 int q_heads, int kv_heads, int cap, int splits, float scale, hipStream_t stream) {
-  switch (dim) {
-    case 16: return dispatch_groups<T, TQ, 16>(groups, q, k, v, lengths, pmax, psum, pout, out, batch, q_heads, kv_heads, cap, splits, scale, stream);
-    case 32: return dispatch_groups<T, TQ, 32>(groups, q, k, v, lengths, pmax, psum, pout, out, batch, q_heads, kv_heads, cap, splits, scale, stream);
-    case 64: return dispatch_groups<T, TQ, 64>(groups, q, k, v, lengths, pmax, psum, pout, out, batch, q_heads, kv_heads, cap, splits, scale, stream);
-    case 128: return dispatch_groups<T, TQ, 128>(groups, q, k, v, lengths, pmax, psum, pout, out, batch, q_heads, kv_heads, cap, splits, scale, stream);
+template <typename T, typename TQ, typename TO, int D, int G>
+int launch_attn(const DecodeCall& c) {
+  constexpr int W = waves_for<T, D, G>();
+  const int chunk = (c.cap + c.splits - 1) / c.splits;
+  const long groups = long(c.batch) * c.kv_heads * c.splits;
+  hipLaunchKernelGGL((decode_attn_kernel<T, TQ, TO, D, G, W>), dim3(unsigned(groups)), dim3(W * kWave), 0,
+                     c.stream, static_cast<const TQ*>(c.q), static_cast<const T*>(c.k),
+                     static_cast<const T*>(c.v), c.lengths, c.pmax, c.psum, c.pout, c.out, c.kv_heads,
+                     c.cap, c.splits, chunk, c.scale * kLog2e);
+  return check_launch("decode_attention");
+}
+
+template <typename T, typename TQ, typename TO, int D>
+int attn_groups(const DecodeCall& c) {
+  switch (c.q_heads / c.kv_heads) {
+    case 1: return launch_attn<T, TQ, TO, D, 1>(c);
+    case 2: return launch_attn<T, TQ, TO, D, 2>(c);
+    case 4: return launch_attn<T, TQ, TO, D, 4>(c);
+    case 8: return launch_attn<T, TQ, TO, D, 8>(c);
   }
-  return set_error(SFL_ERR_UNSUPPORTED, "decode_attention: unsupported head dim %d", dim);
+  return set_error(SFL_ERR_UNSUPPORTED, "decode_attention: unsupported GQA ratio %d", c.q_heads / c.kv_heads);
+}
+
+template <typename T, typename TQ, typename TO>
+int attn_dims(const DecodeCall& c) {
+  switch (c.dim) {
+    case 16: return attn_groups<T, TQ, TO, 16>(c);
+    case 32: return attn_groups<T, TQ, TO, 32>(c);
+    case 64: return attn_groups<T, TQ, TO, 64>(c);
+    case 128: return attn_groups<T, TQ, TO, 128>(c);
+  }
+  return set_error(SFL_ERR_UNSUPPORTED, "decode_attention: unsupported head dim %d", c.dim);
+}
+
+template <typename TO>
+int merge_dims(const DecodeCall& c) {
+  switch (c.dim) {
+    case 16: return launch_merge<TO, 16>(c.pmax, c.psum, c.pout, c.lengths, c.out, c.batch, c.q_heads, c.cap, c.splits, c.stream);
+    case 32: return launch_merge<TO, 32>(c.pmax, c.psum, c.pout, c.lengths, c.out, c.batch, c.q_heads, c.cap, c.splits, c.stream);
+    case 64: return launch_merge<TO, 64>(c.pmax, c.psum, c.pout, c.lengths, c.out, c.batch, c.q_heads, c.cap, c.splits, c.stream);
+    case 128: return launch_merge<TO, 128>(c.pmax, c.psum, c.pout, c.lengths, c.out, c.batch, c.q_heads, c.cap, c.splits, c.stream);
+  }
+  return set_error(SFL_ERR_UNSUPPORTED, "decode_attention: unsupported head dim %d", c.dim);
+}
+
+// The attention kernel's output type is only used with one split; with more
+// splits it writes partials and the merge kernel writes the output type.
+template <typename T, typename TQ>
+int attn_out(const DecodeCall& c, int out_dtype) {
+  if (c.splits > 1) return attn_dims<T, TQ, float>(c);
+  switch (out_dtype) {
+    case SFL_DTYPE_F32: return attn_dims<T, TQ, float>(c);
+    case SFL_DTYPE_BF16X2: return attn_dims<T, TQ, split_t>(c);
+    default: return attn_dims<T, TQ, T>(c);
+  }
 }
 
 }  // namespace
@@ -258,7 +393,8 @@ extern "C" int sfl_decode_attention(const void* q, const void* k, const void* v,
                                     const int32_t* lengths, float* partial_max,
                                     float* partial_sum, float* partial_out, void* out, int batch,
                                     int q_heads, int kv_heads, int capacity, int head_dim,
-                                    int splits, float scale, int dtype, int io_dtype, void* stream) {
+                                    int splits, float scale, int kv_dtype, int q_dtype,
+                                    int out_dtype, void* stream) {
   using namespace sfl;
   if (!q || !k || !v || !lengths || !partial_max || !partial_sum || !partial_out || !out)
     return set_error(SFL_ERR_INVALID, "decode_attention: null pointer argument");
@@ -266,24 +402,37 @@ extern "C" int sfl_decode_attention(const void* q, const void* k, const void* v,
     return set_error(SFL_ERR_INVALID, "decode_attention: batch, heads and capacity must be positive");
   if (q_heads % kv_heads)
     return set_error(SFL_ERR_INVALID, "decode_attention: query heads must be divisible by KV heads");
+  const int groups = q_heads / kv_heads;
+  if (groups != 1 && groups != 2 && groups != 4 && groups != 8)
+    return set_error(SFL_ERR_UNSUPPORTED, "decode_attention: unsupported GQA ratio %d", groups);
+  if (head_dim != 16 && head_dim != 32 && head_dim != 64 && head_dim != 128)
+    return set_error(SFL_ERR_UNSUPPORTED, "decode_attention: unsupported head dim %d", head_dim);
   if (splits < 1 || splits > 1024)
     return set_error(SFL_ERR_INVALID, "decode_attention: splits must be in [1, 1024]");
   if (!(scale > 0.f) || !__builtin_isfinite(scale))
     return set_error(SFL_ERR_INVALID, "decode_attention: scale must be finite and positive");
-  if (io_dtype != dtype && io_dtype != SFL_DTYPE_F32)
-    return set_error(SFL_ERR_UNSUPPORTED, "decode_attention: q/out dtype must equal the KV dtype or be F32");
-  const int groups = q_heads / kv_heads;
-  const bool f32_io = io_dtype == SFL_DTYPE_F32;
-  hipStream_t s = static_cast<hipStream_t>(stream);
-#define SFL_DECODE_ARGS head_dim, groups, q, k, v, lengths, partial_max, partial_sum, partial_out, out, \
-    batch, q_heads, kv_heads, capacity, splits, scale, s
-  switch (dtype) {
-    case SFL_DTYPE_F32: return dispatch_dim<float, float>(SFL_DECODE_ARGS);
-    case SFL_DTYPE_BF16:
-      return f32_io ? dispatch_dim<bf16_t, float>(SFL_DECODE_ARGS) : dispatch_dim<bf16_t, bf16_t>(SFL_DECODE_ARGS);
-    case SFL_DTYPE_F16:
-      return f32_io ? dispatch_dim<f16_t, float>(SFL_DECODE_ARGS) : dispatch_dim<f16_t, f16_t>(SFL_DECODE_ARGS);
+  if (kv_dtype != SFL_DTYPE_F32 && kv_dtype != SFL_DTYPE_BF16 && kv_dtype != SFL_DTYPE_F16)
+    return set_error(SFL_ERR_UNSUPPORTED, "decode_attention: unsupported dtype %d", kv_dtype);
+  if (q_dtype != kv_dtype && q_dtype != SFL_DTYPE_F32)
+    return set_error(SFL_ERR_UNSUPPORTED, "decode_attention: q dtype must equal the KV dtype or be F32");
+  if (out_dtype != kv_dtype && out_dtype != SFL_DTYPE_F32 && out_dtype != SFL_DTYPE_BF16X2)
+    return set_error(SFL_ERR_UNSUPPORTED, "decode_attention: out dtype must be the KV dtype, F32 or BF16X2");
+  if (out_dtype == SFL_DTYPE_BF16X2 && head_dim % 8)
+    return set_error(SFL_ERR_UNSUPPORTED, "decode_attention: BF16X2 output needs head_dim % 8 == 0");
+  const DecodeCall c{q, k, v, lengths, partial_max, partial_sum, partial_out, out, batch, q_heads,
+                     kv_heads, capacity, head_dim, splits, scale, static_cast<hipStream_t>(stream)};
+  int rc;
+  const bool f32q = q_dtype == SFL_DTYPE_F32;
+  switch (kv_dtype) {
+    case SFL_DTYPE_F32: rc = attn_out<float, float>(c, out_dtype); break;
+    case SFL_DTYPE_BF16: rc = f32q ? attn_out<bf16_t, float>(c, out_dtype) : attn_out<bf16_t, bf16_t>(c, out_dtype); break;
+    default: rc = f32q ? attn_out<f16_t, float>(c, out_dtype) : attn_out<f16_t, f16_t>(c, out_dtype); break;
   }
-#undef SFL_DECODE_ARGS
-  return set_error(SFL_ERR_UNSUPPORTED, "decode_attention: unsupported dtype %d", dtype);
+  if (rc || splits == 1) return rc;
+  switch (out_dtype) {
+    case SFL_DTYPE_F32: return merge_dims<float>(c);
+    case SFL_DTYPE_BF16: return merge_dims<bf16_t>(c);
+    case SFL_DTYPE_F16: return merge_dims<f16_t>(c);
+    default: return merge_dims<split_t>(c);
+  }
 }

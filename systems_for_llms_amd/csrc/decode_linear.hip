@@ -41,13 +41,13 @@ enum Epi { EPI_QKV = 0, EPI_RESIDUAL = 1, EPI_SWIGLU = 2, EPI_LOGITS = 3 };
 constexpr int kWaves = 8;       // waves per workgroup (K split)
 constexpr int kTileN = 16;      // output features per workgroup
 constexpr int kMaxRows = 16;    // batch rows per launch
-constexpr int kChunkGroup = 8;  // weight chunks loaded per wave before computing
-constexpr int kPadF = 4;        // LDS row padding (floats) against bank conflicts
+constexpr int kPadBytes = 16;   // LDS row padding against bank conflicts
+constexpr int kNormVecs = 8;    // float4 per lane per row in the RMSNorm prologue: K <= 2048
 constexpr float kEps = 1e-5f;
 
 struct LinearArgs {
   const float* x;        // fp32 residual [B, K] (NORM prologue) / residual base (RESIDUAL)
-  const void* act;       // fp32 activations [B, K] (plain prologue)
+  const void* act;       // activations [B, K] in the activation format (plain prologue)
   const void* norm_w;    // [K]
   const void* w;         // [N, K]
   const void* w3;        // [N, K] second matrix of SWIGLU
@@ -63,7 +63,7 @@ struct LinearArgs {
   // RESIDUAL
   float* x_out;          // [B, N]
   // SWIGLU
-  void* h_out;           // fp32 [B, N]
+  void* h_out;           // [B, N] in the activation format
   // LOGITS
   void* logits;          // fp32 [B, V], optional; row offset pos[b]*logits_pos_stride
   long logits_batch_stride;
@@ -114,37 +114,79 @@ __device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
   return v > bv || (v == bv && i < bi);
 }
 
-// B operand of one chunk from 16 bytes' worth of fp32 activations (8 values for
-// bf16, 4 for fp32). bf16 splits each value into hi + lo bf16 parts so the
-// activation enters the product with ~16 mantissa bits; fp32 passes through.
-template <typename T>
-__device__ __forceinline__ f32x4 mfma_act(const uint4& w, const float* f, f32x4 acc);
+// Activation operand format, 4 bytes per element in both cases:
+//   fp32 weights: plain fp32 values;
+//   bf16 weights: each group of 8 consecutive values is stored as 8 "hi" bf16
+//   followed by 8 "lo" bf16 (32 bytes), with hi = x truncated to bf16 and
+//   lo = (x - hi) truncated to bf16, so hi + lo keeps ~16 mantissa bits of x
+//   and one lane's chunk is exactly the two MFMA B operands.
+// Producers (the RMSNorm prologue, the SwiGLU epilogue, the attention merge)
+// write this format once; the GEMV loop then does no conversion.
+template <typename T> struct ActChunk;
+template <> struct ActChunk<float> { uint4 v; };
+template <> struct ActChunk<bf16_t> { uint4 hi, lo; };
 
+template <typename T>
+__device__ __forceinline__ ActChunk<T> load_act(const unsigned char* p);
 template <>
-__device__ __forceinline__ f32x4 mfma_act<bf16_t>(const uint4& w, const float* f, f32x4 acc) {
-  uint32_t hi[4], lo[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const uint16_t h0 = f32_to_bf16_bits(f[2 * j]), h1 = f32_to_bf16_bits(f[2 * j + 1]);
-    const uint16_t l0 = f32_to_bf16_bits(f[2 * j] - __uint_as_float(uint32_t(h0) << 16));
-    const uint16_t l1 = f32_to_bf16_bits(f[2 * j + 1] - __uint_as_float(uint32_t(h1) << 16));
-    hi[j] = uint32_t(h0) | (uint32_t(h1) << 16);
-    lo[j] = uint32_t(l0) | (uint32_t(l1) << 16);
-  }
-  const u32x4 bh = {hi[0], hi[1], hi[2], hi[3]};
-  const u32x4 bl = {lo[0], lo[1], lo[2], lo[3]};
+__device__ __forceinline__ ActChunk<float> load_act<float>(const unsigned char* p) {
+  return {load16(p)};
+}
+template <>
+__device__ __forceinline__ ActChunk<bf16_t> load_act<bf16_t>(const unsigned char* p) {
+  return {load16(p), load16(p + 16)};
+}
+
+template <typename T>
+__device__ __forceinline__ f32x4 mfma_act(const uint4& w, const ActChunk<T>& x, bool live, f32x4 acc);
+template <>
+__device__ __forceinline__ f32x4 mfma_act<bf16_t>(const uint4& w, const ActChunk<bf16_t>& x, bool live, f32x4 acc) {
+  const u32x4 bh = {live ? x.hi.x : 0u, live ? x.hi.y : 0u, live ? x.hi.z : 0u, live ? x.hi.w : 0u};
+  const u32x4 bl = {live ? x.lo.x : 0u, live ? x.lo.y : 0u, live ? x.lo.z : 0u, live ? x.lo.w : 0u};
   acc = mfma_chunk<bf16_t>(w, bh, acc);
   return mfma_chunk<bf16_t>(w, bl, acc);
 }
-
 template <>
-__device__ __forceinline__ f32x4 mfma_act<float>(const uint4& w, const float* f, f32x4 acc) {
-  const u32x4 b = {__float_as_uint(f[0]), __float_as_uint(f[1]), __float_as_uint(f[2]), __float_as_uint(f[3])};
+__device__ __forceinline__ f32x4 mfma_act<float>(const uint4& w, const ActChunk<float>& x, bool live, f32x4 acc) {
+  const u32x4 b = {live ? x.v.x : 0u, live ? x.v.y : 0u, live ? x.v.z : 0u, live ? x.v.w : 0u};
   return mfma_chunk<float>(w, b, acc);
 }
 
-template <typename T, int E, bool NORM>
+// Four consecutive RMSNorm gains as fp32 (one 8- or 16-byte load).
+template <typename T> __device__ __forceinline__ float4 load_gain4(const T* p);
+template <> __device__ __forceinline__ float4 load_gain4<float>(const float* p) {
+  return *reinterpret_cast<const float4*>(p);
+}
+template <> __device__ __forceinline__ float4 load_gain4<bf16_t>(const bf16_t* p) {
+  const uint2 w = *reinterpret_cast<const uint2*>(p);
+  return make_float4(bf16_lo(w.x), bf16_hi(w.x), bf16_lo(w.y), bf16_hi(w.y));
+}
+
+// Store 4 consecutive activation values (element index e, e % 4 == 0) of a row.
+template <typename T>
+__device__ __forceinline__ void store_act4(unsigned char* row, int e, const float* v);
+template <>
+__device__ __forceinline__ void store_act4<float>(unsigned char* row, int e, const float* v) {
+  *reinterpret_cast<float4*>(row + size_t(e) * 4) = make_float4(v[0], v[1], v[2], v[3]);
+}
+template <>
+__device__ __forceinline__ void store_act4<bf16_t>(unsigned char* row, int e, const float* v) {
+  uint32_t hb[4], lb[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    hb[i] = __float_as_uint(v[i]) & 0xffff0000u;
+    lb[i] = __float_as_uint(v[i] - __uint_as_float(hb[i])) & 0xffff0000u;
+  }
+  unsigned char* g = row + size_t(e / 8) * 32 + (e % 8) * 2;
+  *reinterpret_cast<uint2*>(g) = make_uint2((hb[0] >> 16) | hb[1], (hb[2] >> 16) | hb[3]);
+  *reinterpret_cast<uint2*>(g + 16) = make_uint2((lb[0] >> 16) | lb[1], (lb[2] >> 16) | lb[3]);
+}
+
+// CPW: weight chunks each wave loads per round (one round when K/chunk_k <= kWaves*CPW);
+// chosen on the host from K so no wave issues more loads than it needs.
+template <typename T, int E, bool NORM, int CPW>
 __global__ __launch_bounds__(kWaves * kWave) void linear_kernel(LinearArgs a) {
+  constexpr int kChunkGroup = CPW;
   extern __shared__ __align__(16) unsigned char smem[];
   constexpr int EPL = vec_elems<T>();  // k values per lane per chunk
   constexpr int KC = chunk_k<T>();
@@ -153,9 +195,9 @@ __global__ __launch_bounds__(kWaves * kWave) void linear_kernel(LinearArgs a) {
   const int wave = tid / kWave;
   const int lane = tid % kWave;
   const int K = a.k;
-  const int ldk = K + kPadF;
-  float* act_s = reinterpret_cast<float*>(smem);
-  float* red = act_s + (NORM ? kMaxRows * ldk : 0);
+  const int ld = K * 4 + kPadBytes;  // LDS row stride in bytes (activation format)
+  unsigned char* act_s = smem;
+  float* red = reinterpret_cast<float*>(smem + (NORM ? size_t(kMaxRows) * ld : 0));
 
   const int n0 = blockIdx.x * kTileN;
   const int row = min(n0 + lane % 16, a.n - 1);
@@ -163,46 +205,91 @@ __global__ __launch_bounds__(kWaves * kWave) void linear_kernel(LinearArgs a) {
   const int b = lane % 16;
   const T* wrow = static_cast<const T*>(a.w) + long(row) * K + grp * EPL;
   const T* w3row = kTwo ? static_cast<const T*>(a.w3) + long(row) * K + grp * EPL : nullptr;
-  // Plain prologue: this lane's fp32 activation row, read straight from global memory.
-  const float* arow = static_cast<const float*>(a.act) + long(min(b, a.batch - 1)) * K + grp * EPL;
+  // Plain prologue: this lane's activation row, read straight from global memory.
+  const unsigned char* arow = static_cast<const unsigned char*>(a.act) +
+                              (long(min(b, a.batch - 1)) * K + grp * EPL) * 4;
   const bool live = b < a.batch;
   const int nchunks = K / KC;
 
   // Issue the first group of weight (and plain activation) loads up front.
+  // Loads are unconditional, from clamped addresses, and masked where they are
+  // used: a load whose value is consumed inside its own guard makes the
+  // compiler wait for it on the spot, serialising the memory round trips.
   uint4 wa[kChunkGroup], wb[kTwo ? kChunkGroup : 1];
-  float af[NORM ? 1 : kChunkGroup][NORM ? 1 : EPL];
+  ActChunk<T> af[NORM ? 1 : kChunkGroup];
   int c0 = wave;
+  const int last = nchunks - 1;
 #pragma unroll
   for (int j = 0; j < kChunkGroup; ++j) {
-    const int c = c0 + j * kWaves;
-    if (c < nchunks) {
-      wa[j] = load16(wrow + long(c) * KC);
-      if constexpr (kTwo) wb[j] = load16(w3row + long(c) * KC);
-      if constexpr (!NORM) {
-#pragma unroll
-        for (int e = 0; e < EPL; e += 4) {
-          const float4 v = *reinterpret_cast<const float4*>(arow + long(c) * KC + e);
-          af[j][e] = live ? v.x : 0.f; af[j][e + 1] = live ? v.y : 0.f;
-          af[j][e + 2] = live ? v.z : 0.f; af[j][e + 3] = live ? v.w : 0.f;
-        }
+    const long c = min(c0 + j * kWaves, last);
+    wa[j] = load16(wrow + c * KC);
+    if constexpr (kTwo) wb[j] = load16(w3row + c * KC);
+    if constexpr (!NORM) af[j] = load_act<T>(arow + c * KC * 4);
+  }
+
+  // Prefetch what wave 0's epilogue reads, so it overlaps the weight loads.
+  const int n = n0 + 4 * grp;  // this lane's features n .. n+3 of batch row b
+  float4 pre_x = make_float4(0.f, 0.f, 0.f, 0.f);
+  float2 pre_c = make_float2(0.f, 0.f), pre_s = make_float2(0.f, 0.f);
+  int pre_p = 0;
+  if (wave == 0 && live && n < a.n) {
+    if constexpr (E == EPI_RESIDUAL) {
+      pre_x = *reinterpret_cast<const float4*>(a.x + long(b) * a.n + n);
+    } else if constexpr (E == EPI_QKV) {
+      pre_p = a.pos[b];
+      if (n < 2 * a.d_model) {
+        const int half = a.head_dim / 2;
+        const long at = long(pre_p) * half + (n % a.d_model % a.head_dim) / 2;
+        pre_c = *reinterpret_cast<const float2*>(a.cos_t + at);
+        pre_s = *reinterpret_cast<const float2*>(a.sin_t + at);
       }
     }
   }
 
   if constexpr (NORM) {
-    // RMSNorm rows in fp32 into LDS (layers.py:133-141); pad rows are zero.
+    // RMSNorm rows into LDS in the activation format (layers.py:133-141:
+    // x / sqrt(mean(x^2) + eps) * w, here x * (1 / sqrt(...)) * w); pad rows
+    // are zero. Each wave owns kMaxRows/kWaves rows and issues every load of
+    // its rows and of the gain before the first use: one memory round trip.
+    constexpr int R = kMaxRows / kWaves;
     const T* nw = static_cast<const T*>(a.norm_w);
-    for (int r = wave; r < kMaxRows; r += kWaves) {
-      float* dst = act_s + r * ldk;
-      if (r < a.batch) {
-        const float* xr = a.x + long(r) * K;
-        float ss = 0.f;
-        for (int i = lane; i < K; i += kWave) ss = fmaf(xr[i], xr[i], ss);
-        ss = wave_sum(ss);
-        const float rms = sqrtf(ss / float(K) + kEps);
-        for (int i = lane; i < K; i += kWave) dst[i] = (xr[i] / rms) * load_scalar<T>(nw + i);
-      } else {
-        for (int i = lane; i < K; i += kWave) dst[i] = 0.f;
+    float4 xv[R][kNormVecs];
+    float4 gv[kNormVecs];
+#pragma unroll
+    for (int j = 0; j < kNormVecs; ++j) {
+      const int col = min((lane + j * kWave) * 4, K - 4);
+      gv[j] = load_gain4<T>(nw + col);
+    }
+#pragma unroll
+    for (int rr = 0; rr < R; ++rr) {
+      const float* xr = a.x + long(min(wave + rr * kWaves, a.batch - 1)) * K;
+#pragma unroll
+      for (int j = 0; j < kNormVecs; ++j) {
+        const int col = min((lane + j * kWave) * 4, K - 4);
+        xv[rr][j] = *reinterpret_cast<const float4*>(xr + col);
+      }
+    }
+#pragma unroll
+    for (int rr = 0; rr < R; ++rr) {
+      const int r = wave + rr * kWaves;
+      float ss = 0.f;
+#pragma unroll
+      for (int j = 0; j < kNormVecs; ++j) {
+        const float4 v = xv[rr][j];
+        if ((lane + j * kWave) * 4 < K) ss = fmaf(v.x, v.x, fmaf(v.y, v.y, fmaf(v.z, v.z, fmaf(v.w, v.w, ss))));
+      }
+      ss = wave_sum(ss);
+      const float inv = r < a.batch ? 1.f / sqrtf(ss / float(K) + kEps) : 0.f;
+      unsigned char* dst = act_s + size_t(r) * ld;
+#pragma unroll
+      for (int j = 0; j < kNormVecs; ++j) {
+        const int col = (lane + j * kWave) * 4;
+        if (col < K) {
+          const float4 v = xv[rr][j];
+          const float4 g = gv[j];
+          const float h[4] = {(v.x * inv) * g.x, (v.y * inv) * g.y, (v.z * inv) * g.z, (v.w * inv) * g.w};
+          store_act4<T>(dst, col, h);
+        }
       }
     }
     __syncthreads();
@@ -210,44 +297,25 @@ __global__ __launch_bounds__(kWaves * kWave) void linear_kernel(LinearArgs a) {
 
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   f32x4 acc3 = {0.f, 0.f, 0.f, 0.f};
-  const float* bsrc = act_s + b * ldk + grp * EPL;
+  const unsigned char* bsrc = act_s + size_t(b) * ld + grp * EPL * 4;
   for (;;) {
 #pragma unroll
     for (int j = 0; j < kChunkGroup; ++j) {
       const int c = c0 + j * kWaves;
       if (c < nchunks) {
-        float f[EPL];
-        if constexpr (NORM) {
-#pragma unroll
-          for (int e = 0; e < EPL; e += 4) {
-            const float4 v = *reinterpret_cast<const float4*>(bsrc + c * KC + e);
-            f[e] = v.x; f[e + 1] = v.y; f[e + 2] = v.z; f[e + 3] = v.w;
-          }
-        } else {
-#pragma unroll
-          for (int e = 0; e < EPL; ++e) f[e] = af[j][e];
-        }
-        acc = mfma_act<T>(wa[j], f, acc);
-        if constexpr (kTwo) acc3 = mfma_act<T>(wb[j], f, acc3);
+        const ActChunk<T> x = NORM ? load_act<T>(bsrc + size_t(c) * KC * 4) : af[j];
+        acc = mfma_act<T>(wa[j], x, live || NORM, acc);
+        if constexpr (kTwo) acc3 = mfma_act<T>(wb[j], x, live || NORM, acc3);
       }
     }
     c0 += kChunkGroup * kWaves;
     if (c0 >= nchunks) break;
 #pragma unroll
     for (int j = 0; j < kChunkGroup; ++j) {
-      const int c = c0 + j * kWaves;
-      if (c < nchunks) {
-        wa[j] = load16(wrow + long(c) * KC);
-        if constexpr (kTwo) wb[j] = load16(w3row + long(c) * KC);
-        if constexpr (!NORM) {
-#pragma unroll
-          for (int e = 0; e < EPL; e += 4) {
-            const float4 v = *reinterpret_cast<const float4*>(arow + long(c) * KC + e);
-            af[j][e] = live ? v.x : 0.f; af[j][e + 1] = live ? v.y : 0.f;
-            af[j][e + 2] = live ? v.z : 0.f; af[j][e + 3] = live ? v.w : 0.f;
-          }
-        }
-      }
+      const long c = min(c0 + j * kWaves, last);
+      wa[j] = load16(wrow + c * KC);
+      if constexpr (kTwo) wb[j] = load16(w3row + c * KC);
+      if constexpr (!NORM) af[j] = load_act<T>(arow + c * KC * 4);
     }
   }
 
@@ -270,7 +338,6 @@ __global__ __launch_bounds__(kWaves * kWave) void linear_kernel(LinearArgs a) {
     }
   }
 
-  const int n = n0 + 4 * grp;  // this lane's features n .. n+3 of batch row b
   if constexpr (E == EPI_LOGITS) {
     // Start from a valid index so a row of NaN logits still yields an in-range token.
     float bv = -INFINITY;
@@ -302,33 +369,28 @@ __global__ __launch_bounds__(kWaves * kWave) void linear_kernel(LinearArgs a) {
   }
   if (!live || n >= a.n) return;
   if constexpr (E == EPI_RESIDUAL) {
-    const float* xr = a.x + long(b) * a.n + n;
-    float* xo = a.x_out + long(b) * a.n + n;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) xo[i] = xr[i] + v1[i];
+    *reinterpret_cast<float4*>(a.x_out + long(b) * a.n + n) =
+        make_float4(pre_x.x + v1[0], pre_x.y + v1[1], pre_x.z + v1[2], pre_x.w + v1[3]);
   } else if constexpr (E == EPI_SWIGLU) {
     float h[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) h[i] = v1[i] / (1.f + expf(-v1[i])) * v3[i];
-    float* dst = static_cast<float*>(a.h_out) + long(b) * a.n + n;
-    *reinterpret_cast<float4*>(dst) = make_float4(h[0], h[1], h[2], h[3]);
+    store_act4<T>(static_cast<unsigned char*>(a.h_out) + size_t(b) * a.n * 4, n, h);
   } else {  // EPI_QKV
     const int section = n / a.d_model;  // 0 q, 1 k, 2 v
     const int f = n % a.d_model;
     const int head = f / a.head_dim;
     const int dim = f % a.head_dim;
-    const int p = a.pos[b];
+    const int p = pre_p;
     float y[4] = {v1[0], v1[1], v1[2], v1[3]};
     if (section < 2) {
-      const int half = a.head_dim / 2;
+      // Pairs (dim, dim+1) and (dim+2, dim+3) use table columns dim/2 and dim/2+1.
+      const float c[2] = {pre_c.x, pre_c.y}, sn[2] = {pre_s.x, pre_s.y};
 #pragma unroll
       for (int i = 0; i < 4; i += 2) {
-        const int pair = (dim + i) / 2;
-        const float c = a.cos_t[long(p) * half + pair];
-        const float s = a.sin_t[long(p) * half + pair];
         const float e = y[i], o = y[i + 1];
-        y[i] = e * c - o * s;
-        y[i + 1] = e * s + o * c;
+        y[i] = e * c[i / 2] - o * sn[i / 2];
+        y[i + 1] = e * sn[i / 2] + o * c[i / 2];
       }
     }
     if (section == 0) {
@@ -341,21 +403,34 @@ __global__ __launch_bounds__(kWaves * kWave) void linear_kernel(LinearArgs a) {
   }
 }
 
-template <typename T, int E, bool NORM>
-int launch_linear(const LinearArgs& a, hipStream_t stream, const char* what) {
-  const size_t lds = (NORM ? size_t(kMaxRows) * (a.k + kPadF) * sizeof(float) : 0) +
+template <typename T, int E, bool NORM, int CPW>
+int launch_linear_cpw(const LinearArgs& a, hipStream_t stream, const char* what) {
+  const size_t lds = (NORM ? size_t(kMaxRows) * (size_t(a.k) * 4 + kPadBytes) : 0) +
                      size_t(kWaves) * kWave * (E == EPI_SWIGLU ? 8 : 4) * sizeof(float);
   if (lds > 160 * 1024)
     return set_error(SFL_ERR_UNSUPPORTED, "%s: K=%d needs %zu bytes of LDS (max 163840)", what, a.k, lds);
+  if (NORM && a.k > kNormVecs * kWave * 4)
+    return set_error(SFL_ERR_UNSUPPORTED, "%s: RMSNorm prologue supports d_model <= %d", what, kNormVecs * kWave * 4);
   static bool attr_set = false;
   if (!attr_set) {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&linear_kernel<T, E, NORM>),
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&linear_kernel<T, E, NORM, CPW>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
     attr_set = true;
   }
   const unsigned tiles = unsigned((a.n + kTileN - 1) / kTileN);
-  hipLaunchKernelGGL((linear_kernel<T, E, NORM>), dim3(tiles), dim3(kWaves * kWave), lds, stream, a);
+  hipLaunchKernelGGL((linear_kernel<T, E, NORM, CPW>), dim3(tiles), dim3(kWaves * kWave), lds, stream, a);
   return check_launch(what);
+}
+
+template <typename T, int E, bool NORM>
+int launch_linear(const LinearArgs& a, hipStream_t stream, const char* what) {
+  const int per_wave = (a.k / chunk_k<T>() + kWaves - 1) / kWaves;
+  if (per_wave <= 1) return launch_linear_cpw<T, E, NORM, 1>(a, stream, what);
+  if (per_wave <= 2) return launch_linear_cpw<T, E, NORM, 2>(a, stream, what);
+  if (per_wave <= 4) return launch_linear_cpw<T, E, NORM, 4>(a, stream, what);
+  if (per_wave <= 6) return launch_linear_cpw<T, E, NORM, 6>(a, stream, what);
+  if (per_wave <= 8) return launch_linear_cpw<T, E, NORM, 8>(a, stream, what);
+  return launch_linear_cpw<T, E, NORM, 11>(a, stream, what);  // larger K loops in rounds of 11
 }
 
 int check_common(const char* what, int batch, int n, int k, int dtype) {

@@ -39,12 +39,26 @@ __global__ __launch_bounds__(64) void next_token_kernel(
     const T* __restrict__ emb, float* __restrict__ x, int d, int cap) {
   const int b = blockIdx.x;
   const int lane = threadIdx.x;
+  const int p = pos[b];
+  const int plen = prompt_len[b];
+  const int np = p + 1;
+  const long given = np < cap ? tokens[b * stride + np] : 0;
   float bv = -INFINITY;
   int bi = 0x7fffffff;
-  for (int t = lane; t < tiles; t += kWave) {
-    const float v = best_val[long(t) * batch + b];
-    const int i = best_idx[long(t) * batch + b];
-    if (better(v, i, bv, bi)) { bv = v; bi = i; }
+  // Issue kScan independent loads per lane per round (tiles <= 1024 in one round).
+  constexpr int kScan = 16;
+  for (int t0 = 0; t0 < tiles; t0 += kScan * kWave) {
+    float v[kScan];
+    int ix[kScan];
+#pragma unroll
+    for (int j = 0; j < kScan; ++j) {  // unconditional loads from clamped tiles
+      const long t = min(t0 + lane + j * kWave, tiles - 1);
+      v[j] = best_val[t * batch + b];
+      ix[j] = best_idx[t * batch + b];
+    }
+#pragma unroll
+    for (int j = 0; j < kScan; ++j)
+      if (t0 + lane + j * kWave < tiles && better(v[j], ix[j], bv, bi)) { bv = v[j]; bi = ix[j]; }
   }
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) {
@@ -52,13 +66,32 @@ __global__ __launch_bounds__(64) void next_token_kernel(
     const int oi = __shfl_xor(bi, m, kWave);
     if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
   }
-  const int p = pos[b];
-  const int np = p + 1;
   if (np >= cap) return;  // context full: the host never steps past capacity
-  const bool forced = np < prompt_len[b];
-  const long tok = forced ? tokens[b * stride + np] : long(bi);
+  const bool forced = np < plen;
+  const long tok = forced ? given : long(bi);
   const T* src = emb + tok * d;
-  for (int i = lane; i < d; i += kWave) x[long(b) * d + i] = load_scalar<T>(src + i);
+  float* dst = x + long(b) * d;
+  constexpr int V = vec_elems<T>();
+  if (d % V == 0) {
+    for (int i0 = 0; i0 < d; i0 += 4 * kWave * V) {
+      uint4 r[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) r[j] = load16(src + min(i0 + (lane + j * kWave) * V, d - V));
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int i = i0 + (lane + j * kWave) * V;
+        if (i < d) {
+          float f[V];
+          unpack16<T>(r[j], f);
+#pragma unroll
+          for (int e = 0; e < V; e += 4)
+            *reinterpret_cast<float4*>(dst + i + e) = make_float4(f[e], f[e + 1], f[e + 2], f[e + 3]);
+        }
+      }
+    }
+  } else {
+    for (int i = lane; i < d; i += kWave) dst[i] = load_scalar<T>(src + i);
+  }
   if (lane == 0) {
     predicted[b * stride + np] = bi;
     if (!forced) tokens[b * stride + np] = bi;

@@ -60,15 +60,16 @@ def _validate(q, k, v, lengths, splits):
     return batch, query_heads, dim
 
 
-def auto_splits(batch: int, kv_heads: int, capacity: int, target_items: int = 2048,
-                keys_per_item: int = 256, min_keys: int = 64) -> int:
-    """Split count giving about ``target_items`` wave work items of >= ``min_keys`` keys.
+def auto_splits(batch: int, kv_heads: int, capacity: int, target_groups: int = 256,
+                min_keys: int = 1024) -> int:
+    """Split count giving about ``target_groups`` workgroups of >= ``min_keys`` keys.
 
-    One wave streams one chunk of ceil(capacity/splits) keys; 256 keys per wave
-    is 64 KB of bf16 K+V at D=64, enough to keep its loads in flight, and a few
-    thousand items fill the 256 CUs several times over.
+    One workgroup (up to 16 waves) owns one (batch, kv head, split) chunk and
+    merges its waves through LDS; with a single split it writes the output
+    directly and no merge kernel runs. A few hundred workgroups cover the 256
+    CUs, so splitting further only adds partials and a merge launch.
     """
-    splits = max(math.ceil(capacity / keys_per_item), math.ceil(target_items / (batch * kv_heads)))
+    splits = math.ceil(target_groups / (batch * kv_heads))
     return max(1, min(MAX_SPLITS, splits, math.ceil(capacity / min_keys)))
 
 
@@ -93,7 +94,8 @@ class PreparedDecode:
                   self.lengths.data_ptr(), self.partial_max.data_ptr(), self.partial_sum.data_ptr(),
                   self.partial_output.data_ptr(), self.output.data_ptr(), batch, heads, kv_heads,
                   capacity, dim, self.splits, self.scale, _lib.dtype_code(self.q.dtype),
-                  _lib.dtype_code(self.q.dtype), _lib.stream_handle(self.q.device))
+                  _lib.dtype_code(self.q.dtype), _lib.dtype_code(self.q.dtype),
+                  _lib.stream_handle(self.q.device))
         return self.output
 
     @property

@@ -59,10 +59,13 @@ class DecodeSession:
         self.k_cache = torch.zeros((n, batch, h, cap, self.dk), device=dev, dtype=dt)
         self.v_cache = torch.zeros_like(self.k_cache)
         self.x = torch.zeros((batch, d), device=dev, dtype=torch.float32)
-        # Activations stay fp32; only weights and the KV cache use the model dtype.
+        # Only weights and the KV cache use the model dtype. x and q are fp32; the
+        # GEMV inputs (attention output, SwiGLU hidden) are 4 bytes per value:
+        # fp32 for fp32 models, the split-bf16 (hi, lo) format for bf16 models.
         self.q = torch.zeros((batch, h, self.dk), device=dev, dtype=torch.float32)
         self.attn = torch.zeros((batch, h, self.dk), device=dev, dtype=torch.float32)
         self.hidden = torch.zeros((batch, f), device=dev, dtype=torch.float32)
+        self.act_code = _lib.DTYPE_BF16X2 if dt == torch.bfloat16 else _lib.DTYPE_CODES[torch.float32]
         self.splits = splits or auto_splits(batch, h, cap)
         self.pmax = torch.empty((batch, h, self.splits), device=dev, dtype=torch.float32)
         self.psum = torch.empty_like(self.pmax)
@@ -99,7 +102,8 @@ class DecodeSession:
             calls.append((lib.sfl_decode_attention, (
                 self.q.data_ptr(), kc.data_ptr(), vc.data_ptr(), self.lengths.data_ptr(),
                 self.pmax.data_ptr(), self.psum.data_ptr(), self.pout.data_ptr(), self.attn.data_ptr(),
-                self.batch, h, h, cap, dk, self.splits, scale, code, _lib.DTYPE_CODES[torch.float32])))
+                self.batch, h, h, cap, dk, self.splits, scale, code, _lib.DTYPE_CODES[torch.float32],
+                self.act_code)))
             for r, rows in row_chunks:
                 calls.append((lib.sfl_linear_residual, (
                     self.attn[r].data_ptr(), blk.attn.output_proj.weight.data_ptr(), self.x[r].data_ptr(),

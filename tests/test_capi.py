@@ -39,10 +39,10 @@ def test_argument_errors_are_reported_without_a_launch():
         pytest.skip("libsfl.so not built")
     with pytest.raises(RuntimeError, match="null pointer"):
         _lib.call("sfl_decode_attention", None, None, None, None, None, None, None, None,
-                  1, 1, 1, 1, 64, 1, 0.125, 1, 1, None)
+                  1, 1, 1, 1, 64, 1, 0.125, 1, 1, 1, None)
     buf = ctypes.create_string_buffer(64)
     p = ctypes.addressof(buf)
     with pytest.raises(RuntimeError, match="divisible"):
-        _lib.call("sfl_decode_attention", p, p, p, p, p, p, p, p, 1, 3, 2, 16, 64, 1, 0.125, 1, 1, None)
+        _lib.call("sfl_decode_attention", p, p, p, p, p, p, p, p, 1, 3, 2, 16, 64, 1, 0.125, 1, 1, 1, None)
     with pytest.raises(RuntimeError, match="head dim"):
-        _lib.call("sfl_decode_attention", p, p, p, p, p, p, p, p, 1, 2, 2, 16, 48, 1, 0.125, 1, 1, None)
+        _lib.call("sfl_decode_attention", p, p, p, p, p, p, p, p, 1, 2, 2, 16, 48, 1, 0.125, 1, 1, 1, None)

@@ -34,9 +34,10 @@ def test_unknown_variant_and_bad_ratio_rejected():
 
 
 def test_auto_splits_bounds():
-    assert auto_splits(64, 16, 16384) == 64
-    assert auto_splits(16, 16, 4096) == 16
-    assert auto_splits(1, 4, 1024) == 16
+    assert auto_splits(64, 16, 16384) == 1   # config 4: 1024 workgroups already
+    assert auto_splits(16, 16, 4096) == 1    # 324M decode: one workgroup per (batch, head)
+    assert auto_splits(1, 16, 4096) == 4     # single sequence: split the context
+    assert auto_splits(1, 4, 1024) == 1
     assert auto_splits(1, 1, 10) == 1
     for b, h, n in ((1, 1, 1), (3, 5, 999), (128, 32, 65536)):
         s = auto_splits(b, h, n)
