@@ -146,6 +146,38 @@ int sfl_next_token(const float* best_val, const int32_t* best_idx, int tiles, in
                    int32_t* lengths, const void* emb, float* x, int batch, int d_model,
                    int capacity, int dtype, void* stream);
 
+/* ---- masked prefill attention ----------------------------------------------
+ * Replaces attention_lab/triton_attention.py `attention` (:326-438) and its
+ * kernels interval_attention_forward (:209-321) and csr_attention_forward
+ * (:126-197), bound by the Python wrapper at :389-435.
+ *
+ *   q, k, v, o   [B, H, N, D] bf16/fp16 addressed by per-tensor strides
+ *                {batch, head, sequence} in elements (D contiguous; row
+ *                strides multiple of 8 for q/k/v, of 4 for o)
+ *   lse          optional fp32 [B, H, N]: natural-log row normalizers,
+ *                -inf (with a zero output row) where no key is admissible
+ *   scale        score scale (the reference uses D^-0.5)
+ *   mask         causal; window_left / window_right (< 0: unbounded);
+ *                global_prefix: keys k < prefix pass the windows (not
+ *                causality or documents); document_ids int64 [N] or NULL
+ *   schedule     mode 0: interval bounds derived on the device (no
+ *                documents); mode 1: CSR over 64-row query tiles of 64-key
+ *                tiles, row_ptr int32 [ceil(N/64)+1], col_idx int32, full
+ *                uint8 (1 = no elementwise mask needed)
+ *   use_full_blocks 0 applies the elementwise mask to every tile
+ * Tiles are 64 x 64 (sfl_masked_attention_block()). D in {32, 64, 128}.
+ */
+int sfl_masked_attention(const void* q, const void* k, const void* v, void* o, float* lse,
+                         int batch, int heads, int n, int head_dim, const long* q_strides,
+                         const long* k_strides, const long* v_strides, const long* o_strides,
+                         float scale, int causal, int window_left, int window_right,
+                         int global_prefix, const int64_t* document_ids, int schedule_mode,
+                         const int32_t* row_ptr, const int32_t* col_idx,
+                         const uint8_t* full_blocks, int use_full_blocks, int dtype, void* stream);
+
+/* Query/key tile size of sfl_masked_attention (64). */
+int sfl_masked_attention_block(void);
+
 #ifdef __cplusplus
 }
 #endif

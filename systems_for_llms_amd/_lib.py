@@ -8,7 +8,7 @@ is missing every GPU entry point raises, naming the build command.
 from __future__ import annotations
 
 import ctypes
-from ctypes import c_char_p, c_float, c_int, c_long, c_void_p
+from ctypes import POINTER, c_char_p, c_float, c_int, c_long, c_void_p
 from pathlib import Path
 
 import torch
@@ -29,6 +29,10 @@ SIGNATURES: dict[str, list] = {
     "sfl_lm_head_tiles": [c_int],
     "sfl_embedding_gather": [P, c_long, P, P, P, c_int, c_int, c_int, P],
     "sfl_next_token": [P, P, c_int, P, P, c_long, P, P, P, P, P, c_int, c_int, c_int, c_int, P],
+    "sfl_masked_attention": [P, P, P, P, P, c_int, c_int, c_int, c_int, POINTER(c_long), POINTER(c_long),
+                             POINTER(c_long), POINTER(c_long), c_float, c_int, c_int, c_int, c_int, P,
+                             c_int, P, P, P, c_int, c_int, P],
+    "sfl_masked_attention_block": [],
 }
 
 _LIB = None

@@ -1,0 +1,344 @@
+// Masked softmax attention over a block schedule (prefill), bf16/fp16 MFMA.
+//
+// Semantics follow attention_lab/triton_attention.py: a query tile visits the
+// key tiles of its schedule row -- analytic interval bounds
+// (interval_attention_forward, :209-321) or a CSR list with full/partial flags
+// (csr_attention_forward, :126-197) -- with an online softmax in fp32 whose
+// rescale is safe for fully masked rows (:176-183); rows with no admissible
+// key produce zeros and LSE -inf (:191-197); LSE is the natural log; full
+// tiles skip the elementwise mask except at the sequence tail (:225-234).
+// The mask language is attention_lab/masks.py:84-106 plus this build's
+// global key prefix: allowed = causal_ok & doc_ok & (window_ok | k < prefix).
+//
+// gfx950 design: a workgroup of 4 waves owns 64 query rows of one (batch,
+// head); each wave owns 16 rows. Key tiles of 64 rows are staged in LDS (K
+// row-major, V transposed). Scores are computed transposed, S^T = K Q^T, with
+// 16x16x32 MFMAs so each lane holds 16 scores of ONE query: the row max and
+// row sum need only two cross-lane steps and the rescale factor is per lane.
+// The P V product is O^T = V^T P^T; its key order is chosen so that the B
+// operand is exactly the probabilities the lane already holds (the product is
+// a sum over keys, so any order both operands share is exact), and V^T rows
+// come from LDS as 8-byte runs.
+#include "common.hpp"
+
+namespace sfl {
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int BQ = 64;        // query rows per workgroup
+constexpr int BK = 64;        // key rows per tile
+constexpr int kThreads = 256;
+constexpr int kPadK = 8;      // LDS padding (elements) of K rows and V^T rows
+
+template <typename T>
+__device__ __forceinline__ f32x4 mfma16(const u32x4& a, const u32x4& b, f32x4 c);
+template <>
+__device__ __forceinline__ f32x4 mfma16<bf16_t>(const u32x4& a, const u32x4& b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+template <>
+__device__ __forceinline__ f32x4 mfma16<f16_t>(const u32x4& a, const u32x4& b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+
+template <typename T> __device__ __forceinline__ uint16_t to_bits(float v);
+template <> __device__ __forceinline__ uint16_t to_bits<bf16_t>(float v) { return f32_to_bf16_bits(v); }
+template <> __device__ __forceinline__ uint16_t to_bits<f16_t>(float v) { return f32_to_f16_bits(v); }
+
+struct MaskArgs {
+  int causal;
+  int left, right;      // < 0: unbounded
+  int prefix;           // global key prefix (0: none)
+  const int64_t* docs;  // same-document labels (nullptr: none)
+};
+
+struct Sched {
+  int mode;             // 0 interval, 1 csr
+  int use_full;
+  const int32_t* row_ptr;
+  const int32_t* col_idx;
+  const uint8_t* full;
+};
+
+struct AttnArgs {
+  const void *q, *k, *v;
+  void* o;
+  float* lse;
+  long qs[3], ks[3], vs[3], os[3];  // strides (elements) of batch, head, sequence
+  int heads, n;
+  float scale_log2;
+  MaskArgs m;
+  Sched s;
+};
+
+__device__ __forceinline__ bool allowed(const MaskArgs& m, int q, int k, int n) {
+  if (k >= n || q >= n) return false;
+  if (m.causal && k > q) return false;
+  if (m.docs && m.docs[q] != m.docs[k]) return false;
+  if (k < m.prefix) return true;
+  if (m.left >= 0 && q - k > m.left) return false;
+  if (m.right >= 0 && k - q > m.right) return false;
+  return true;
+}
+
+// Tile geometry of one query tile, as masks.py/_tile_geometry derives it.
+struct TileBounds {
+  int begin, end, gend;  // window blocks [begin, end), global blocks [0, gend)
+  int f_lo, f_hi, gf_hi; // keys admissible for every row: [f_lo, f_hi] U [0, gf_hi]
+};
+
+__device__ __forceinline__ TileBounds tile_bounds(const MaskArgs& m, int n, int q0, int q1) {
+  const int right = m.causal ? (m.right < 0 ? 0 : min(0, m.right)) : m.right;  // < 0 unbounded when !causal
+  const bool has_right = m.causal || m.right >= 0;
+  const int w_lo = m.left < 0 ? 0 : max(0, q0 - m.left);
+  const int w_hi = has_right ? min(n - 1, q1 + right) : n - 1;
+  TileBounds t;
+  t.begin = w_lo / BK;
+  t.end = w_hi / BK + 1;
+  t.f_lo = m.left < 0 ? 0 : max(0, q1 - m.left);
+  t.f_hi = has_right ? min(n - 1, q0 + right) : n - 1;
+  const int g = min(m.prefix, n);
+  const int g_hi = m.causal ? min(g - 1, q1) : g - 1;
+  t.gf_hi = m.causal ? min(g - 1, q0) : g - 1;
+  t.gend = g_hi >= 0 ? g_hi / BK + 1 : 0;
+  return t;
+}
+
+// Whether every key of [k0, k1] is admissible for every row of the tile
+// (without documents): [k0, k1] inside [0, gf_hi] U [f_lo, f_hi].
+__device__ __forceinline__ bool covered(const TileBounds& t, int k0, int k1) {
+  int pos = k0;
+  if (t.gf_hi >= 0 && pos <= t.gf_hi) pos = t.gf_hi + 1;
+  if (pos > k1) return true;
+  if (t.f_lo <= pos && pos <= t.f_hi) pos = t.f_hi + 1;
+  if (pos > k1) return true;
+  // [0, gf_hi] may also cover the tail if f-range came first
+  if (t.gf_hi >= 0 && pos <= t.gf_hi) pos = t.gf_hi + 1;
+  return pos > k1;
+}
+
+template <typename T, int D>
+__global__ __launch_bounds__(kThreads) void masked_attention_kernel(AttnArgs a) {
+  constexpr int KSTEPS = D / 32;   // MFMA k-steps over the head dim
+  constexpr int DT = D / 16;       // 16-wide d tiles of O^T
+  constexpr int LDK = D + kPadK;   // K row stride (elements)
+  constexpr int LDV = BK + kPadK;  // V^T row stride (elements)
+  __shared__ __align__(16) uint16_t k_s[BK * LDK];
+  __shared__ __align__(16) uint16_t vt_s[D * LDV];
+
+  const int tid = threadIdx.x;
+  const int wave = tid / kWave, lane = tid % kWave;
+  const int col = lane % 16, grp = lane / 16;
+  const int qt = blockIdx.x;
+  const int bh = blockIdx.y;
+  const int b = bh / a.heads, h = bh % a.heads;
+  const int n = a.n;
+  const int q0 = qt * BQ;
+  const int q1 = min(q0 + BQ, n) - 1;
+  const int qrow = q0 + wave * 16 + col;  // this lane's query row
+
+  const uint16_t* qp = static_cast<const uint16_t*>(a.q) + b * a.qs[0] + h * a.qs[1];
+  const uint16_t* kp = static_cast<const uint16_t*>(a.k) + b * a.ks[0] + h * a.ks[1];
+  const uint16_t* vp = static_cast<const uint16_t*>(a.v) + b * a.vs[0] + h * a.vs[1];
+
+  // Q^T operand: lane holds Q[qrow][32*ks + 8*grp .. +8] for every k-step.
+  u32x4 qreg[KSTEPS];
+  {
+    const uint16_t* qr = qp + long(min(qrow, n - 1)) * a.qs[2];
+#pragma unroll
+    for (int ks = 0; ks < KSTEPS; ++ks) {
+      const uint4 r = load16(qr + 32 * ks + 8 * grp);
+      qreg[ks] = u32x4{r.x, r.y, r.z, r.w};
+    }
+  }
+
+  float m_run = -INFINITY, l_run = 0.f;
+  f32x4 oacc[DT];
+#pragma unroll
+  for (int t = 0; t < DT; ++t) oacc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const TileBounds tb = tile_bounds(a.m, n, q0, q1);
+  int count, base = 0;
+  if (a.s.mode == 1) {
+    base = a.s.row_ptr[qt];
+    count = a.s.row_ptr[qt + 1] - base;
+  } else {
+    const int lowg = min(tb.gend, tb.begin);
+    count = lowg + max(0, max(tb.end, tb.gend) - tb.begin);
+  }
+  const int lowg = min(tb.gend, tb.begin);
+
+  for (int it = 0; it < count; ++it) {
+    int kb;
+    bool full;
+    if (a.s.mode == 1) {
+      kb = a.s.col_idx[base + it];
+      full = a.s.full[base + it] != 0;
+    } else {
+      kb = it < lowg ? it : tb.begin + (it - lowg);
+      full = !a.m.docs && covered(tb, kb * BK, min(kb * BK + BK, n) - 1);
+    }
+    full = full && a.s.use_full;
+    const int k0 = kb * BK;
+
+    // Stage the key tile: K row-major, V transposed.
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < (BK * D / 8) / kThreads; ++r) {
+      const int idx = tid + r * kThreads;
+      const int key = idx / (D / 8), dg = idx % (D / 8);
+      const int kr = min(k0 + key, n - 1);
+      const uint4 kv = load16(kp + long(kr) * a.ks[2] + dg * 8);
+      const uint4 vv = load16(vp + long(kr) * a.vs[2] + dg * 8);
+      *reinterpret_cast<uint4*>(k_s + key * LDK + dg * 8) = kv;
+      const uint32_t w[4] = {vv.x, vv.y, vv.z, vv.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        vt_s[(dg * 8 + 2 * e) * LDV + key] = uint16_t(w[e] & 0xffffu);
+        vt_s[(dg * 8 + 2 * e + 1) * LDV + key] = uint16_t(w[e] >> 16);
+      }
+    }
+    __syncthreads();
+
+    // S^T = K Q^T: subtile j covers keys 16j .. 16j+15; lane holds keys 16j + 4*grp + i.
+    f32x4 sacc[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      sacc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < KSTEPS; ++ks) {
+        const u32x4 ka = *reinterpret_cast<const u32x4*>(k_s + (16 * j + col) * LDK + 32 * ks + 8 * grp);
+        sacc[j] = mfma16<T>(ka, qreg[ks], sacc[j]);
+      }
+    }
+    const bool tail = k0 + BK > n || qrow >= n;
+    float sv[16];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int key = k0 + 16 * j + 4 * grp + i;
+        const bool ok = (full && !tail) ? true : (full ? (key < n && qrow < n) : allowed(a.m, qrow, key, n));
+        sv[4 * j + i] = ok ? sacc[j][i] * a.scale_log2 : -INFINITY;
+      }
+    }
+    float mx = sv[0];
+#pragma unroll
+    for (int e = 1; e < 16; ++e) mx = fmaxf(mx, sv[e]);
+    mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+    const float m_new = fmaxf(m_run, mx);
+    const float ms = m_new == -INFINITY ? 0.f : m_new;
+    const float alpha = exp2f(m_run - ms);
+    float psum = 0.f;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      sv[e] = exp2f(sv[e] - ms);
+      psum += sv[e];
+    }
+    psum += __shfl_xor(psum, 16, kWave);
+    psum += __shfl_xor(psum, 32, kWave);
+    l_run = l_run * alpha + psum;
+    m_run = m_new;
+#pragma unroll
+    for (int t = 0; t < DT; ++t) oacc[t] *= alpha;
+
+    // O^T += V^T P^T. Step s covers subtiles 2s and 2s+1; element e of the
+    // lane's operands is key 16*(2s + e/4) + 4*grp + e%4 for both operands.
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2) {
+      uint32_t pb[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float lo = sv[4 * (2 * s2 + e / 2) + (2 * e) % 4];
+        const float hi = sv[4 * (2 * s2 + e / 2) + (2 * e) % 4 + 1];
+        pb[e] = uint32_t(to_bits<T>(lo)) | (uint32_t(to_bits<T>(hi)) << 16);
+      }
+      const u32x4 pop = {pb[0], pb[1], pb[2], pb[3]};
+#pragma unroll
+      for (int t = 0; t < DT; ++t) {
+        const uint16_t* vrow = vt_s + (16 * t + col) * LDV;
+        const uint2 a0 = *reinterpret_cast<const uint2*>(vrow + 16 * (2 * s2) + 4 * grp);
+        const uint2 a1 = *reinterpret_cast<const uint2*>(vrow + 16 * (2 * s2 + 1) + 4 * grp);
+        const u32x4 vop = {a0.x, a0.y, a1.x, a1.y};
+        oacc[t] = mfma16<T>(vop, pop, oacc[t]);
+      }
+    }
+  }
+
+  if (qrow >= n) return;
+  const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
+  uint16_t* op = static_cast<uint16_t*>(a.o) + b * a.os[0] + h * a.os[1] + long(qrow) * a.os[2];
+#pragma unroll
+  for (int t = 0; t < DT; ++t) {
+    const uint32_t lo = uint32_t(to_bits<T>(oacc[t][0] * inv)) | (uint32_t(to_bits<T>(oacc[t][1] * inv)) << 16);
+    const uint32_t hi = uint32_t(to_bits<T>(oacc[t][2] * inv)) | (uint32_t(to_bits<T>(oacc[t][3] * inv)) << 16);
+    *reinterpret_cast<uint2*>(op + 16 * t + 4 * grp) = make_uint2(lo, hi);
+  }
+  if (a.lse && grp == 0) {
+    const float lse = l_run > 0.f ? (m_run + log2f(l_run)) * 0.6931471805599453f : -INFINITY;
+    a.lse[(long(b) * a.heads + h) * n + qrow] = lse;
+  }
+}
+
+template <typename T>
+int launch_masked(const AttnArgs& a, int batch, int dim, hipStream_t stream) {
+  dim3 grid((a.n + BQ - 1) / BQ, batch * a.heads);
+  switch (dim) {
+    case 32: hipLaunchKernelGGL((masked_attention_kernel<T, 32>), grid, dim3(kThreads), 0, stream, a); break;
+    case 64: hipLaunchKernelGGL((masked_attention_kernel<T, 64>), grid, dim3(kThreads), 0, stream, a); break;
+    case 128: hipLaunchKernelGGL((masked_attention_kernel<T, 128>), grid, dim3(kThreads), 0, stream, a); break;
+    default: return set_error(SFL_ERR_UNSUPPORTED, "masked_attention: head dim must be 32, 64 or 128");
+  }
+  return check_launch("masked_attention");
+}
+
+}  // namespace
+}  // namespace sfl
+
+using namespace sfl;
+
+extern "C" int sfl_masked_attention(const void* q, const void* k, const void* v, void* o, float* lse,
+                                    int batch, int heads, int n, int head_dim,
+                                    const long* q_strides, const long* k_strides,
+                                    const long* v_strides, const long* o_strides, float scale,
+                                    int causal, int window_left, int window_right, int global_prefix,
+                                    const int64_t* document_ids, int schedule_mode,
+                                    const int32_t* row_ptr, const int32_t* col_idx,
+                                    const uint8_t* full_blocks, int use_full_blocks, int dtype,
+                                    void* stream) {
+  const char* what = "masked_attention";
+  if (!q || !k || !v || !o || !q_strides || !k_strides || !v_strides || !o_strides)
+    return set_error(SFL_ERR_INVALID, "%s: null pointer argument", what);
+  if (batch < 1 || heads < 1 || n < 1) return set_error(SFL_ERR_INVALID, "%s: sizes must be positive", what);
+  if (!(scale > 0.f) || !__builtin_isfinite(scale)) return set_error(SFL_ERR_INVALID, "%s: scale must be finite and positive", what);
+  if (schedule_mode != 0 && schedule_mode != 1) return set_error(SFL_ERR_INVALID, "%s: schedule_mode must be 0 (interval) or 1 (csr)", what);
+  if (schedule_mode == 1 && (!row_ptr || !col_idx || !full_blocks))
+    return set_error(SFL_ERR_INVALID, "%s: csr schedule arrays are required", what);
+  if (schedule_mode == 0 && document_ids)
+    return set_error(SFL_ERR_INVALID, "%s: interval schedules do not support document constraints", what);
+  if (global_prefix < 0) return set_error(SFL_ERR_INVALID, "%s: global_prefix must be >= 0", what);
+  for (int i = 0; i < 3; ++i) {
+    if (q_strides[i] < 0 || k_strides[i] < 0 || v_strides[i] < 0 || o_strides[i] < 0)
+      return set_error(SFL_ERR_INVALID, "%s: strides must be non-negative", what);
+  }
+  if (q_strides[2] % 8 || k_strides[2] % 8 || v_strides[2] % 8 || o_strides[2] % 4)
+    return set_error(SFL_ERR_INVALID, "%s: row strides must keep 16-byte alignment", what);
+  AttnArgs a{};
+  a.q = q; a.k = k; a.v = v; a.o = o; a.lse = lse;
+  for (int i = 0; i < 3; ++i) {
+    a.qs[i] = q_strides[i]; a.ks[i] = k_strides[i]; a.vs[i] = v_strides[i]; a.os[i] = o_strides[i];
+  }
+  a.heads = heads; a.n = n; a.scale_log2 = scale * kLog2e;
+  a.m = MaskArgs{causal, window_left, window_right, global_prefix, document_ids};
+  a.s = Sched{schedule_mode, use_full_blocks, row_ptr, col_idx, full_blocks};
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == SFL_DTYPE_BF16) return launch_masked<bf16_t>(a, batch, head_dim, s);
+  if (dtype == SFL_DTYPE_F16) return launch_masked<f16_t>(a, batch, head_dim, s);
+  return set_error(SFL_ERR_UNSUPPORTED, "%s: dtype must be BF16 or F16", what);
+}
+
+extern "C" int sfl_masked_attention_block(void) { return BQ; }
