@@ -3,10 +3,12 @@
 Workload: d_model 1024, 24 layers, 16 heads of 64, SwiGLU d_ff 2752, vocab
 10000, bf16 weights N(0, 0.02) from seed 1337; batch 16; 3072 uniform random
 prompt tokens (seed 2027) are prefilled, then greedy decode runs to context
-4096. One step = one decode position for all 16 sequences (16 tokens), replayed
-from a captured HIP graph. W warmup steps run first and the state is rewound
-to the first decode position, so the K timed steps always cover positions
-3071 .. 3071+K-1 (attention lengths 3072 .. 3071+K).
+4096. The prompt is prefilled in one pass (MFMA GEMMs + masked attention),
+which also picks token 3072. One step = one decode position for all 16
+sequences (16 tokens), replayed from a captured HIP graph. W warmup steps run
+first and the state is rewound to the first decode position, so the K timed
+steps always cover positions 3072 .. 3072+K-1 (attention lengths 3073 ..
+3072+K); the default K = 1023 generates tokens 3073 .. 4095.
 
 Printed JSON (one line): decode tok/s; ``roofline`` for the dominant kernel,
 split-KV decode attention, timed with HIP events on its launch stream at the
@@ -97,7 +99,7 @@ def cpu_baseline(cfg, seconds=12.0, max_steps=32):
 def main() -> int:
     parser = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     parser.add_argument("--gpus", type=int, default=1)
-    parser.add_argument("--steps", type=int, default=CONTEXT - PROMPT)
+    parser.add_argument("--steps", type=int, default=CONTEXT - PROMPT - 1)
     parser.add_argument("--warmup", type=int, default=8)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--attention-reps", type=int, default=50)
@@ -106,8 +108,8 @@ def main() -> int:
         print("bench.py measures one GPU: every box in this build has a single MI355X and the decode "
               "path is not sharded across GPUs (see DESIGN.md for how it would shard)", file=sys.stderr)
         return 2
-    if not 1 <= args.steps <= CONTEXT - PROMPT or not 0 <= args.warmup <= CONTEXT - PROMPT:
-        print(f"--steps and --warmup must be in [1, {CONTEXT - PROMPT}]", file=sys.stderr)
+    if not 1 <= args.steps <= CONTEXT - PROMPT - 1 or not 0 <= args.warmup <= CONTEXT - PROMPT - 1:
+        print(f"--steps and --warmup must be in [1, {CONTEXT - PROMPT - 1}]", file=sys.stderr)
         return 2
 
     import torch
@@ -127,18 +129,18 @@ def main() -> int:
     log(f"model ready in {time.perf_counter() - t0:.1f}s")
 
     session = DecodeSession(model, BATCH, CONTEXT)
-    session.start(prompt)
+    session.prefill(prompt)  # warm-up: first-call kernel attributes and allocations
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    session.step()  # eager warm-up of every kernel before capture
-    session.capture(1)
-    for _ in range(PROMPT - 2):
-        session.graph.replay()
+    session.prefill(prompt)
     torch.cuda.synchronize()
     prefill_s = time.perf_counter() - t0
-    log(f"prefill of {PROMPT} positions in {prefill_s:.2f}s (decode-step kernels)")
-    first = PROMPT - 1
+    log(f"prefill of {BATCH}x{PROMPT} tokens in {prefill_s * 1000:.1f} ms "
+        f"({BATCH * PROMPT / prefill_s:.0f} tok/s, MFMA GEMMs + masked attention)")
+    first = PROMPT  # prefill chose token PROMPT; decode steps run at positions PROMPT ..
     assert int(session.pos[0]) == first
+    session.step()  # eager warm-up of every decode kernel before capture
+    session.capture(1)
 
     for _ in range(args.warmup):
         session.graph.replay()
@@ -148,7 +150,7 @@ def main() -> int:
     ms = time_events(session.graph.replay, args.steps)
     ms_per_step = ms
     tokens_per_s = BATCH * 1000.0 / ms_per_step
-    generated = session.tokens[:, PROMPT:PROMPT + args.steps]
+    generated = session.tokens[:, PROMPT:PROMPT + args.steps + 1]
     assert int(session.pos[0]) == first + args.steps
     assert bool((generated >= 0).all()) and bool((generated < cfg.vocab_size).all())
     log(f"decode {args.steps} steps: {ms_per_step:.3f} ms/step, {tokens_per_s:.0f} tok/s")
@@ -221,7 +223,7 @@ def main() -> int:
                    "d_model": cfg.d_model, "num_layers": cfg.num_layers, "num_heads": cfg.num_heads,
                    "d_ff": cfg.d_ff, "vocab_size": cfg.vocab_size, "global_batch": BATCH,
                    "prompt": PROMPT, "context": CONTEXT, "parallelism": "single GPU"},
-        "roofline": {"bound": "hbm", "kernel": "decode_partial_kernel + decode_merge_kernel",
+        "roofline": {"bound": "hbm", "kernel": "decode_attn_kernel (split-KV decode attention, one launch)",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
                      "bytes_per_launch": attn_bytes, "us_per_launch": round(attn_ms * 1000, 2),
@@ -229,7 +231,8 @@ def main() -> int:
         "e2e": {"bytes_per_step": int(e2e_bytes), "achieved_gbs": round(e2e_gbs, 1),
                 "frac_of_hbm_peak": round(e2e_gbs / HBM_PEAK_GBS, 4),
                 "roofline_tok_s": round(BATCH / (e2e_bytes / (HBM_PEAK_GBS * 1e9)), 1),
-                "prefill_s": round(prefill_s, 3), "prefill_path": "decode-step kernels, one position per step"},
+                "prefill_s": round(prefill_s, 4), "prefill_tok_s": round(BATCH * PROMPT / prefill_s, 1),
+                "prefill_path": "MFMA GEMMs (QKV+RoPE+append, O, SwiGLU, W2) + MFMA causal attention"},
         "decode_attention_config4": {"us": round(c4_ms * 1000, 1), "achieved_gbs": round(c4_gbs, 1),
                                      "frac": round(c4_gbs / HBM_PEAK_GBS, 4), "bytes": c4_bytes,
                                      "shape": "B=64 H=16 D=64 bf16 ragged lengths U[1024,16384] seed 4"},

@@ -178,6 +178,38 @@ int sfl_masked_attention(const void* q, const void* k, const void* v, void* o, f
 /* Query/key tile size of sfl_masked_attention (64). */
 int sfl_masked_attention_block(void);
 
+/* ---- prefill (bf16 weights) -------------------------------------------------
+ * C^T = W A^T on MFMA 16x16x32 bf16 tiles of 128 features x 128 tokens;
+ * A [M, K] bf16 row-major (one row per token), W [N, K] bf16; K % 8 == 0.
+ * Replace, for a whole prompt, the Linear layers of one TransformerBlock and
+ * the lm_head (src/llmlab/model/layers.py:34-35, attention.py:160-162,199-203,
+ * layers.py:114-115, transformer.py:137-138).
+ */
+
+/* C = A W^T as fp32 (accumulate = 1 adds into C: the residual update) or bf16. */
+int sfl_gemm_bf16(const void* a, const void* w, void* c, int m, int n, int k, int c_dtype,
+                  int accumulate, void* stream);
+
+/* q/k/v = A W_qkv^T with RoPE at position (row % seq) from the fp32 table;
+ * q to [m/seq, heads, seq, head_dim] bf16, k/v written at positions 0..seq-1
+ * of the [m/seq, heads, capacity, head_dim] bf16 cache. */
+int sfl_gemm_qkv_rope(const void* a, const void* w_qkv, int m, int seq, int d_model, int heads,
+                      const float* cos_t, const float* sin_t, void* q_out, void* k_cache,
+                      void* v_cache, int capacity, void* stream);
+
+/* h = silu(A W1^T) * (A W3^T) as bf16 [m, d_ff]; w13_interleaved [2*d_ff, k]
+ * holds 8 rows of W1 then the same 8 rows of W3, repeatedly. */
+int sfl_gemm_swiglu(const void* a, const void* w13_interleaved, void* h_out, int m, int d_ff, int k,
+                    void* stream);
+
+/* x[r] = emb[ids[r]] in fp32 for r < m (Embedding.forward, layers.py:68-70). */
+int sfl_embed_rows(const int64_t* ids, const void* emb, float* x, int m, int d_model, int dtype,
+                   void* stream);
+
+/* out[r] = bf16(RMSNorm(x[r]) * w) for r < m (layers.py:133-141); dtype is w's. */
+int sfl_rmsnorm_rows(const float* x, const void* w, void* out_bf16, int m, int d_model, int dtype,
+                     void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -33,6 +33,11 @@ SIGNATURES: dict[str, list] = {
                              POINTER(c_long), POINTER(c_long), c_float, c_int, c_int, c_int, c_int, P,
                              c_int, P, P, P, c_int, c_int, P],
     "sfl_masked_attention_block": [],
+    "sfl_gemm_bf16": [P, P, P, c_int, c_int, c_int, c_int, c_int, P],
+    "sfl_gemm_qkv_rope": [P, P, c_int, c_int, c_int, c_int, P, P, P, P, P, c_int, P],
+    "sfl_gemm_swiglu": [P, P, P, c_int, c_int, c_int, P],
+    "sfl_embed_rows": [P, P, P, c_int, c_int, c_int, P],
+    "sfl_rmsnorm_rows": [P, P, P, c_int, c_int, c_int, P],
 }
 
 _LIB = None

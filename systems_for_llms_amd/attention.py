@@ -183,3 +183,18 @@ def attention(q, k, v, schedule, spec, document_ids=None, num_warps=4, num_stage
                                 "threads": 256, "implementation": implementation,
                                 "source": "libsfl.so gfx950 HIP kernel; not a profiler measurement"})
     return (out, lse) if return_lse else out
+
+
+def causal_prefill(q, k, v, out):
+    """Causal attention of a prompt for the model's prefill (interval schedule, no LSE).
+
+    ``q``, ``k``, ``v`` and ``out`` are ``[B, H, T, D]`` bf16 views with a
+    contiguous last dimension (``k``/``v`` straight out of the KV cache);
+    launches on the current stream without any host synchronisation.
+    """
+    b, h, t, d = q.shape
+    _lib.call("sfl_masked_attention", q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), None,
+              b, h, t, d, _strides(q), _strides(k), _strides(v), _strides(out), float(d ** -0.5),
+              1, -1, -1, 0, None, 0, None, None, None, 1, _lib.dtype_code(q.dtype),
+              _lib.stream_handle(q.device))
+    return out

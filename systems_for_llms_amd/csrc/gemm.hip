@@ -1,0 +1,313 @@
+// Prefill projections as bf16 MFMA GEMMs with fused epilogues, plus the
+// row-wise prefill helpers (embedding gather, RMSNorm).
+//
+// Every GEMM computes C^T[n][m] = sum_k W[n][k] * A[m][k] for A [M, K] bf16
+// activations (one row per token) and W [N, K] bf16 weights, both K-contiguous
+// as the reference's Linear stores them (src/llmlab/model/layers.py:34-35).
+// Features are the MFMA rows, so each lane ends with 4 consecutive features
+// of one token: RoPE pairs and SwiGLU pairs are in-lane or one shuffle away
+// and stores are 8/16-byte vectors.
+//
+// Tiling: a workgroup of 4 waves computes a 128-feature x 128-token tile;
+// wave (wn, wm) owns 64 x 64 = 4 x 4 MFMA tiles of 16x16x32. K advances in
+// steps of 64 through double-buffered LDS tiles (rows padded by 8 elements);
+// the next step's global loads are in registers while the current step runs.
+// Epilogues:
+//   PLAIN     C[m][n] stored as fp32 or bf16 (optionally accumulated into fp32).
+//   QKV       RoPE on q and k (attention.py:44-58) from the host fp32 table at
+//             position m % T, q to [B, H, T, dk] bf16, k/v to the KV cache.
+//   SWIGLU    W is W1/W3 interleaved in blocks of 8 rows; h = silu(a) * c
+//             (layers.py:114-115) as bf16 [M, d_ff].
+#include "common.hpp"
+
+namespace sfl {
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int TN = 128, TM = 128, TK = 64;
+constexpr int LDT = TK + 8;      // LDS row stride (elements)
+constexpr int kThreads = 256;
+
+enum GemmEpi { G_PLAIN = 0, G_QKV = 1, G_SWIGLU = 2 };
+
+struct GemmArgs {
+  const uint16_t* a;   // [M, K]
+  const uint16_t* w;   // [N, K]
+  int m, n, k;
+  // PLAIN
+  void* c;             // [M, N] (ldc = N)
+  int c_f32, accumulate;
+  // QKV
+  const float* cos_t;
+  const float* sin_t;
+  int seq, heads, head_dim, d_model, cap;
+  uint16_t* q_out;     // [B, H, T, dk]
+  uint16_t* k_cache;   // [B, H, cap, dk]
+  uint16_t* v_cache;
+  // SWIGLU
+  uint16_t* h_out;     // [M, N/2]
+};
+
+__device__ __forceinline__ f32x4 mfma_bf16(const u32x4& a, const u32x4& b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+
+__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
+  return uint32_t(f32_to_bf16_bits(lo)) | (uint32_t(f32_to_bf16_bits(hi)) << 16);
+}
+
+template <int E>
+__global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
+  __shared__ __align__(16) uint16_t ws[2][TN * LDT];
+  __shared__ __align__(16) uint16_t as[2][TM * LDT];
+  const int tid = threadIdx.x;
+  const int wave = tid / kWave, lane = tid % kWave;
+  const int wn = wave / 2, wm = wave % 2;
+  const int col = lane % 16, grp = lane / 16;
+  const int n0 = blockIdx.x * TN;
+  const int m0 = blockIdx.y * TM;
+  const int ksteps = (g.k + TK - 1) / TK;
+
+  // Each thread moves 4 x 16 bytes of W and of A per K step: row r, 8-element
+  // group cg. Loads are unconditional from clamped addresses; the K tail is
+  // zeroed when the registers go to LDS, so no load waits inside its guard.
+  uint4 wr[4], ar[4];
+  bool kin[4];
+  auto gload = [&](int kt) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int idx = tid + i * kThreads;  // 0 .. 1023
+      const int r = idx / (TK / 8), cg = idx % (TK / 8);
+      const int kk = kt * TK + cg * 8;
+      kin[i] = kk < g.k;
+      const int kc = kin[i] ? kk : 0;
+      wr[i] = load16(g.w + long(min(n0 + r, g.n - 1)) * g.k + kc);
+      ar[i] = load16(g.a + long(min(m0 + r, g.m - 1)) * g.k + kc);
+    }
+  };
+  auto sstore = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int idx = tid + i * kThreads;
+      const int r = idx / (TK / 8), cg = idx % (TK / 8);
+      const uint4 z = make_uint4(0, 0, 0, 0);
+      *reinterpret_cast<uint4*>(&ws[buf][r * LDT + cg * 8]) = kin[i] ? wr[i] : z;
+      *reinterpret_cast<uint4*>(&as[buf][r * LDT + cg * 8]) = kin[i] ? ar[i] : z;
+    }
+  };
+
+  f32x4 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  gload(0);
+  sstore(0);
+  __syncthreads();
+  for (int kt = 0; kt < ksteps; ++kt) {
+    const int buf = kt & 1;
+    if (kt + 1 < ksteps) gload(kt + 1);
+#pragma unroll
+    for (int ks = 0; ks < TK / 32; ++ks) {
+      u32x4 af[4], bfr[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        af[i] = *reinterpret_cast<const u32x4*>(&ws[buf][(wn * 64 + i * 16 + col) * LDT + ks * 32 + grp * 8]);
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        bfr[j] = *reinterpret_cast<const u32x4*>(&as[buf][(wm * 64 + j * 16 + col) * LDT + ks * 32 + grp * 8]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = mfma_bf16(af[i], bfr[j], acc[i][j]);
+    }
+    if (kt + 1 < ksteps) {
+      sstore(buf ^ 1);
+      __syncthreads();
+    }
+  }
+
+  // Epilogue: acc[i][j] holds features n0 + wn*64 + 16i + 4grp + (0..3) of token m0 + wm*64 + 16j + col.
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int m = m0 + wm * 64 + j * 16 + col;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int n = n0 + wn * 64 + i * 16 + 4 * grp;
+      float y[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
+      if constexpr (E == G_SWIGLU) {
+        // Rows 16i + 0..7 of the tile are W1 features, rows 16i + 8..15 the
+        // matching W3 features: lane groups 0,1 pair with groups 2,3.
+        float c3[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) c3[e] = __shfl_xor(y[e], 32, kWave);
+        if (grp >= 2 || m >= g.m) continue;
+        const int f = (n0 + wn * 64 + i * 16) / 2 + 4 * grp;  // hidden feature index
+        if (f >= g.n / 2) continue;
+        float h[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) h[e] = y[e] / (1.f + expf(-y[e])) * c3[e];
+        *reinterpret_cast<uint2*>(g.h_out + long(m) * (g.n / 2) + f) = make_uint2(pack_bf16(h[0], h[1]), pack_bf16(h[2], h[3]));
+      } else {
+        if (m >= g.m || n >= g.n) continue;
+        if constexpr (E == G_PLAIN) {
+          if (g.c_f32) {
+            float* c = static_cast<float*>(g.c) + long(m) * g.n + n;
+            if (n + 3 < g.n && (g.n & 3) == 0) {
+              float4 old = g.accumulate ? *reinterpret_cast<const float4*>(c) : make_float4(0.f, 0.f, 0.f, 0.f);
+              *reinterpret_cast<float4*>(c) = make_float4(old.x + y[0], old.y + y[1], old.z + y[2], old.w + y[3]);
+            } else {
+              for (int e = 0; e < 4 && n + e < g.n; ++e) c[e] = (g.accumulate ? c[e] : 0.f) + y[e];
+            }
+          } else {
+            uint16_t* c = static_cast<uint16_t*>(g.c) + long(m) * g.n + n;
+            if (n + 3 < g.n && (g.n & 3) == 0) {
+              *reinterpret_cast<uint2*>(c) = make_uint2(pack_bf16(y[0], y[1]), pack_bf16(y[2], y[3]));
+            } else {
+              for (int e = 0; e < 4 && n + e < g.n; ++e) c[e] = f32_to_bf16_bits(y[e]);
+            }
+          }
+        } else {  // G_QKV
+          const int section = n / g.d_model;
+          const int f = n % g.d_model;
+          const int head = f / g.head_dim, dim = f % g.head_dim;
+          const int b = m / g.seq, t = m % g.seq;
+          if (section < 2) {
+            const int half = g.head_dim / 2;
+            const float2 c = *reinterpret_cast<const float2*>(g.cos_t + long(t) * half + dim / 2);
+            const float2 s = *reinterpret_cast<const float2*>(g.sin_t + long(t) * half + dim / 2);
+            const float e0 = y[0], o0 = y[1], e1 = y[2], o1 = y[3];
+            y[0] = e0 * c.x - o0 * s.x;
+            y[1] = e0 * s.x + o0 * c.x;
+            y[2] = e1 * c.y - o1 * s.y;
+            y[3] = e1 * s.y + o1 * c.y;
+          }
+          uint16_t* dst;
+          if (section == 0) {
+            dst = g.q_out + ((long(b) * g.heads + head) * g.seq + t) * g.head_dim + dim;
+          } else {
+            uint16_t* cache = section == 1 ? g.k_cache : g.v_cache;
+            dst = cache + ((long(b) * g.heads + head) * g.cap + t) * g.head_dim + dim;
+          }
+          *reinterpret_cast<uint2*>(dst) = make_uint2(pack_bf16(y[0], y[1]), pack_bf16(y[2], y[3]));
+        }
+      }
+    }
+  }
+}
+
+template <int E>
+int launch_gemm(const GemmArgs& g, hipStream_t s, const char* what) {
+  if (g.m < 1 || g.n < 1 || g.k < 1) return set_error(SFL_ERR_INVALID, "%s: sizes must be positive", what);
+  if (g.k % 8) return set_error(SFL_ERR_UNSUPPORTED, "%s: K must be a multiple of 8", what);
+  dim3 grid((g.n + TN - 1) / TN, (g.m + TM - 1) / TM);
+  if (grid.y > 65535) return set_error(SFL_ERR_UNSUPPORTED, "%s: M too large", what);
+  hipLaunchKernelGGL((gemm_kernel<E>), grid, dim3(kThreads), 0, s, g);
+  return check_launch(what);
+}
+
+// Prefill embedding gather: x[m] = emb[ids[m]] in fp32.
+template <typename T>
+__global__ __launch_bounds__(256) void embed_rows_kernel(const int64_t* ids, const T* emb, float* x, int d) {
+  const long m = blockIdx.x;
+  const T* src = emb + ids[m] * d;
+  for (int i = threadIdx.x; i < d; i += blockDim.x) x[m * d + i] = load_scalar<T>(src + i);
+}
+
+// Prefill RMSNorm: out[m] = bf16(x[m] / sqrt(mean(x[m]^2) + eps) * w) (layers.py:133-141).
+template <typename T>
+__global__ __launch_bounds__(256) void rmsnorm_rows_kernel(const float* x, const T* w, uint16_t* out, int d) {
+  __shared__ float part[4];
+  const long m = blockIdx.x;
+  const float* xr = x + m * d;
+  float ss = 0.f;
+  for (int i = threadIdx.x; i < d; i += 256) ss = fmaf(xr[i], xr[i], ss);
+  ss = wave_sum(ss);
+  if (threadIdx.x % kWave == 0) part[threadIdx.x / kWave] = ss;
+  __syncthreads();
+  const float total = part[0] + part[1] + part[2] + part[3];
+  const float inv = 1.f / sqrtf(total / float(d) + 1e-5f);
+  for (int i = threadIdx.x; i < d; i += 256) out[m * d + i] = f32_to_bf16_bits((xr[i] * inv) * load_scalar<T>(w + i));
+}
+
+}  // namespace
+}  // namespace sfl
+
+using namespace sfl;
+
+extern "C" int sfl_gemm_bf16(const void* a, const void* w, void* c, int m, int n, int k, int c_dtype,
+                             int accumulate, void* stream) {
+  if (!a || !w || !c) return set_error(SFL_ERR_INVALID, "gemm_bf16: null pointer argument");
+  if (c_dtype != SFL_DTYPE_F32 && c_dtype != SFL_DTYPE_BF16)
+    return set_error(SFL_ERR_UNSUPPORTED, "gemm_bf16: output dtype must be F32 or BF16");
+  if (accumulate && c_dtype != SFL_DTYPE_F32)
+    return set_error(SFL_ERR_UNSUPPORTED, "gemm_bf16: accumulation needs an F32 output");
+  GemmArgs g{};
+  g.a = static_cast<const uint16_t*>(a); g.w = static_cast<const uint16_t*>(w);
+  g.m = m; g.n = n; g.k = k; g.c = c; g.c_f32 = c_dtype == SFL_DTYPE_F32; g.accumulate = accumulate;
+  return launch_gemm<G_PLAIN>(g, static_cast<hipStream_t>(stream), "gemm_bf16");
+}
+
+extern "C" int sfl_gemm_qkv_rope(const void* a, const void* w_qkv, int m, int seq, int d_model, int heads,
+                                 const float* cos_t, const float* sin_t, void* q_out, void* k_cache,
+                                 void* v_cache, int capacity, void* stream) {
+  const char* what = "gemm_qkv_rope";
+  if (!a || !w_qkv || !cos_t || !sin_t || !q_out || !k_cache || !v_cache)
+    return set_error(SFL_ERR_INVALID, "%s: null pointer argument", what);
+  if (seq < 1 || m % seq) return set_error(SFL_ERR_INVALID, "%s: rows must be batch * seq", what);
+  if (heads < 1 || d_model % heads || (d_model / heads) % 16)
+    return set_error(SFL_ERR_UNSUPPORTED, "%s: head dim must be a multiple of 16", what);
+  if (seq > capacity) return set_error(SFL_ERR_INVALID, "%s: seq exceeds the cache capacity", what);
+  GemmArgs g{};
+  g.a = static_cast<const uint16_t*>(a); g.w = static_cast<const uint16_t*>(w_qkv);
+  g.m = m; g.n = 3 * d_model; g.k = d_model;
+  g.cos_t = cos_t; g.sin_t = sin_t; g.seq = seq; g.heads = heads; g.head_dim = d_model / heads;
+  g.d_model = d_model; g.cap = capacity;
+  g.q_out = static_cast<uint16_t*>(q_out); g.k_cache = static_cast<uint16_t*>(k_cache);
+  g.v_cache = static_cast<uint16_t*>(v_cache);
+  return launch_gemm<G_QKV>(g, static_cast<hipStream_t>(stream), what);
+}
+
+extern "C" int sfl_gemm_swiglu(const void* a, const void* w13_interleaved, void* h_out, int m, int d_ff,
+                               int k, void* stream) {
+  const char* what = "gemm_swiglu";
+  if (!a || !w13_interleaved || !h_out) return set_error(SFL_ERR_INVALID, "%s: null pointer argument", what);
+  if (d_ff % 8) return set_error(SFL_ERR_UNSUPPORTED, "%s: d_ff must be a multiple of 8", what);
+  GemmArgs g{};
+  g.a = static_cast<const uint16_t*>(a); g.w = static_cast<const uint16_t*>(w13_interleaved);
+  g.m = m; g.n = 2 * d_ff; g.k = k; g.h_out = static_cast<uint16_t*>(h_out);
+  return launch_gemm<G_SWIGLU>(g, static_cast<hipStream_t>(stream), what);
+}
+
+extern "C" int sfl_embed_rows(const int64_t* ids, const void* emb, float* x, int m, int d_model, int dtype,
+                              void* stream) {
+  if (!ids || !emb || !x) return set_error(SFL_ERR_INVALID, "embed_rows: null pointer argument");
+  if (m < 1 || d_model < 1) return set_error(SFL_ERR_INVALID, "embed_rows: sizes must be positive");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == SFL_DTYPE_BF16)
+    hipLaunchKernelGGL(embed_rows_kernel<bf16_t>, dim3(m), dim3(256), 0, s, ids, static_cast<const bf16_t*>(emb), x, d_model);
+  else if (dtype == SFL_DTYPE_F32)
+    hipLaunchKernelGGL(embed_rows_kernel<float>, dim3(m), dim3(256), 0, s, ids, static_cast<const float*>(emb), x, d_model);
+  else
+    return set_error(SFL_ERR_UNSUPPORTED, "embed_rows: dtype must be F32 or BF16");
+  return check_launch("embed_rows");
+}
+
+extern "C" int sfl_rmsnorm_rows(const float* x, const void* w, void* out_bf16, int m, int d_model, int dtype,
+                                void* stream) {
+  if (!x || !w || !out_bf16) return set_error(SFL_ERR_INVALID, "rmsnorm_rows: null pointer argument");
+  if (m < 1 || d_model < 1) return set_error(SFL_ERR_INVALID, "rmsnorm_rows: sizes must be positive");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == SFL_DTYPE_BF16)
+    hipLaunchKernelGGL(rmsnorm_rows_kernel<bf16_t>, dim3(m), dim3(256), 0, s, x, static_cast<const bf16_t*>(w),
+                       static_cast<uint16_t*>(out_bf16), d_model);
+  else if (dtype == SFL_DTYPE_F32)
+    hipLaunchKernelGGL(rmsnorm_rows_kernel<float>, dim3(m), dim3(256), 0, s, x, static_cast<const float*>(w),
+                       static_cast<uint16_t*>(out_bf16), d_model);
+  else
+    return set_error(SFL_ERR_UNSUPPORTED, "rmsnorm_rows: dtype must be F32 or BF16");
+  return check_launch("rmsnorm_rows");
+}

@@ -92,6 +92,7 @@ class DecodeSession:
         calls = []
         scale = float(dk) ** -0.5
         row_chunks = [(r, min(ROWS_PER_LAUNCH, self.batch - r)) for r in range(0, self.batch, ROWS_PER_LAUNCH)]
+        self._row_chunks = row_chunks
         for layer, blk in enumerate(m.layers):
             kc, vc = self.k_cache[layer], self.v_cache[layer]
             for r, rows in row_chunks:
@@ -150,6 +151,91 @@ class DecodeSession:
         _lib.call("sfl_embedding_gather", self.tokens.data_ptr(), self.cap, self.pos.data_ptr(),
                   self.model.token_embeddings.weight.data_ptr(), self.x.data_ptr(), self.batch,
                   self.d, self.code, stream)
+
+    # -- prefill ------------------------------------------------------------
+    def _prefill_weights(self):
+        """W1/W3 interleaved in blocks of 8 rows, the layout the SwiGLU GEMM pairs in-lane."""
+        if getattr(self, "_w13", None) is None:
+            f, d = self.d_ff, self.d
+            self._w13 = [torch.stack([blk.ffn.w1.weight.view(f // 8, 8, d), blk.ffn.w3.weight.view(f // 8, 8, d)],
+                                     dim=1).reshape(2 * f, d).contiguous() for blk in self.model.layers]
+        return self._w13
+
+    @torch.no_grad()
+    def prefill(self, prompt: torch.Tensor, all_logits: bool = False,
+                forced: torch.Tensor | None = None) -> torch.Tensor | None:
+        """Process ``prompt [B, T]`` with MFMA GEMMs and masked attention, then pick token T.
+
+        Fills the KV cache at positions 0..T-1, computes the logits of position
+        T-1 with the decode head, and leaves every row at position T (the next
+        token written, embedded and ready for ``step``). With ``all_logits`` it
+        also returns fp32 logits ``[B, T, V]`` for every position (the
+        reference's ``forward``). bf16 models only; fp32 models use ``start`` +
+        ``run`` (one position per step). ``forced [B, L]`` (L > T, starting with
+        the prompt) makes the following positions up to L teacher-forced.
+        """
+        if self.dtype != torch.bfloat16:
+            raise TypeError("GEMM prefill needs a bfloat16 model; use start() + run() for float32")
+        b, t = prompt.shape
+        if b != self.batch or not 0 < t <= self.cap:
+            raise ValueError("prompt must be [batch, T] with 0 < T <= capacity")
+        low, high = torch.aminmax(prompt)
+        if low.item() < 0 or high.item() >= self.vocab:
+            raise ValueError("token ids must be in [0, vocab_size)")
+        from .attention import causal_prefill
+
+        d, h, dk, f, v = self.d, self.heads, self.dk, self.d_ff, self.vocab
+        m_rows = b * t
+        dev, code = self.device, self.code
+        w13 = self._prefill_weights()
+        self.tokens.zero_()
+        self.tokens[:, :t] = prompt.to(dev)
+        self.predicted.fill_(-1)
+        self.prompt_len.fill_(t)
+        if forced is not None:
+            if forced.shape[0] != b or not t <= forced.shape[1] <= self.cap:
+                raise ValueError("forced must be [batch, L] with T <= L <= capacity")
+            self.tokens[:, :forced.shape[1]] = forced.to(dev)
+            self.prompt_len.fill_(forced.shape[1])
+        ids = self.tokens[:, :t].contiguous().view(-1)
+        x = torch.empty((m_rows, d), device=dev, dtype=torch.float32)
+        act = torch.empty((m_rows, d), device=dev, dtype=torch.bfloat16)
+        q = torch.empty((b, h, t, dk), device=dev, dtype=torch.bfloat16)
+        attn = torch.empty((b, t, h, dk), device=dev, dtype=torch.bfloat16)
+        hid = torch.empty((m_rows, f), device=dev, dtype=torch.bfloat16)
+        st = _lib.stream_handle(dev)
+        call = _lib.call
+        call("sfl_embed_rows", ids.data_ptr(), self.model.token_embeddings.weight.data_ptr(), x.data_ptr(),
+             m_rows, d, code, st)
+        for layer, blk in enumerate(self.model.layers):
+            kc, vc = self.k_cache[layer], self.v_cache[layer]
+            call("sfl_rmsnorm_rows", x.data_ptr(), blk.attn_norm.weight.data_ptr(), act.data_ptr(), m_rows, d, code, st)
+            call("sfl_gemm_qkv_rope", act.data_ptr(), self.wqkv[layer].data_ptr(), m_rows, t, d, h,
+                 self.cos.data_ptr(), self.sin.data_ptr(), q.data_ptr(), kc.data_ptr(), vc.data_ptr(), self.cap, st)
+            causal_prefill(q, kc[:, :, :t], vc[:, :, :t], attn.transpose(1, 2))
+            call("sfl_gemm_bf16", attn.data_ptr(), blk.attn.output_proj.weight.data_ptr(), x.data_ptr(),
+                 m_rows, d, d, 0, 1, st)
+            call("sfl_rmsnorm_rows", x.data_ptr(), blk.ffn_norm.weight.data_ptr(), act.data_ptr(), m_rows, d, code, st)
+            call("sfl_gemm_swiglu", act.data_ptr(), w13[layer].data_ptr(), hid.data_ptr(), m_rows, f, d, st)
+            call("sfl_gemm_bf16", hid.data_ptr(), blk.ffn.w2.weight.data_ptr(), x.data_ptr(), m_rows, d, f, 0, 1, st)
+        logits = None
+        if all_logits:
+            call("sfl_rmsnorm_rows", x.data_ptr(), self.model.ln_final.weight.data_ptr(), act.data_ptr(),
+                 m_rows, d, code, st)
+            logits = torch.empty((m_rows, v), device=dev, dtype=torch.float32)
+            call("sfl_gemm_bf16", act.data_ptr(), self.model.lm_head.weight.data_ptr(), logits.data_ptr(),
+                 m_rows, v, d, 0, 0, st)
+            logits = logits.view(b, t, v)
+        # Hand the last position to the decode head: pick token T and advance.
+        self.x.copy_(x.view(b, t, d)[:, t - 1])
+        self.pos.fill_(t - 1)
+        self.lengths.fill_(t)
+        for fn, args in self._calls[-(len(self._row_chunks) + 1):]:
+            status = fn(*args, st)
+            if status != 0:
+                raise RuntimeError(f"{fn.__name__} failed ({status}): "
+                                   f"{_lib.lib().sfl_last_error().decode(errors='replace')}")
+        return logits
 
     def set_position(self, position: int) -> None:
         """Rewind/advance every row to ``position`` (the cache below it is kept) and re-embed."""

@@ -166,6 +166,10 @@ class TransformerLM(nn.Module):
     def head_dim(self) -> int:
         return self.d_model // self.num_heads
 
+    def _gemm_prefill(self) -> bool:
+        """bf16 models whose head dim the MFMA prefill attention supports prefill in one pass."""
+        return self.lm_head.weight.dtype == torch.bfloat16 and self.head_dim in (32, 64, 128)
+
     def _check_ids(self, input_ids: torch.Tensor) -> None:
         if input_ids.ndim < 1:
             raise ValueError("input_ids must have a sequence dimension")
@@ -178,6 +182,11 @@ class TransformerLM(nn.Module):
         self._check_ids(input_ids)
         lead = input_ids.shape[:-1]
         ids = input_ids.reshape(-1, input_ids.shape[-1])
+        if self._gemm_prefill():
+            # One pass of MFMA GEMMs and masked attention over the whole prompt.
+            session = _engine.DecodeSession(self, batch=ids.shape[0], capacity=ids.shape[-1])
+            logits = session.prefill(ids, all_logits=True)
+            return logits.to(torch.bfloat16).reshape(*lead, ids.shape[-1], self.vocab_size)
         session = _engine.DecodeSession(self, batch=ids.shape[0], capacity=ids.shape[-1],
                                         record_logits=True)
         session.start(ids)
@@ -196,6 +205,10 @@ class TransformerLM(nn.Module):
         if max_new_tokens < 0 or total > self.context_length:
             raise ValueError("sequence length must be between 1 and context_length")
         session = _engine.DecodeSession(self, batch=input_ids.shape[0], capacity=capacity or total)
-        session.start(input_ids)
-        session.run(total - 1, use_graph=use_graph)
+        if self._gemm_prefill() and max_new_tokens > 0:
+            session.prefill(input_ids)  # positions 0..T-1 at once; token T chosen
+            session.run(max_new_tokens - 1, use_graph=use_graph)
+        else:
+            session.start(input_ids)
+            session.run(total - 1, use_graph=use_graph)
         return session.tokens[:, :total].clone()
