@@ -96,6 +96,42 @@ def cpu_baseline(cfg, seconds=12.0, max_steps=32):
                       f"324M, batch {BATCH}, attention length {PROMPT}..{PROMPT + steps}; os.cpu_count()={threads}"}
 
 
+def profile_target_attention(reps: int = 24) -> int:
+    """Counter-collection target: the roofline's decode-attention launches plus a calibration copy.
+
+    Same shapes as the ``roofline`` measurement (324M cache layout, B=16, H=16,
+    D=64, length 3584, one call per layer cache so nothing is re-read from the
+    last-level cache), with random cache contents, followed by one device copy
+    of 256 MiB whose HBM traffic is known (256 MiB read + 256 MiB written).
+    Run it under ``rocprofv3 --pmc FETCH_SIZE`` and ``--pmc WRITE_SIZE``.
+    """
+    import torch
+
+    from systems_for_llms_amd import _lib
+    from systems_for_llms_amd.decode import auto_splits
+
+    layers, heads, dim, length = 24, 16, 64, PROMPT + 512  # the timed region's mean length, 3584
+    k = torch.randn((layers, BATCH, heads, CONTEXT, dim), device="cuda", dtype=torch.bfloat16)
+    v = torch.randn_like(k)
+    q = torch.randn((BATCH, heads, dim), device="cuda", dtype=torch.float32)
+    out = torch.empty((BATCH, heads, dim), device="cuda", dtype=torch.float32)
+    lengths = torch.full((BATCH,), length, device="cuda", dtype=torch.int32)
+    splits = auto_splits(BATCH, heads, CONTEXT)
+    scratch = torch.empty((BATCH, heads, splits, dim + 2), device="cuda", dtype=torch.float32)
+    for i in range(reps):
+        _lib.call("sfl_decode_attention", q.data_ptr(), k[i % layers].data_ptr(), v[i % layers].data_ptr(),
+                  lengths.data_ptr(), scratch.data_ptr(), scratch.data_ptr(), scratch.data_ptr(), out.data_ptr(),
+                  BATCH, heads, heads, CONTEXT, dim, splits, dim ** -0.5, 1, 0, _lib.DTYPE_BF16X2,
+                  _lib.stream_handle())
+    src = torch.ones(256 << 20, device="cuda", dtype=torch.uint8)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"profile target: {reps} decode-attention launches (length {length}, "
+        f"{attention_bytes([length] * BATCH, heads, dim)} algorithmic bytes each) + one 256 MiB copy")
+    return 0
+
+
 def main() -> int:
     parser = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     parser.add_argument("--gpus", type=int, default=1)
@@ -103,7 +139,11 @@ def main() -> int:
     parser.add_argument("--warmup", type=int, default=8)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--attention-reps", type=int, default=50)
+    parser.add_argument("--profile-target", choices=["attention"], default=None,
+                        help="run only the counter-collection target (see profile_target_attention)")
     args = parser.parse_args()
+    if args.profile_target == "attention":
+        return profile_target_attention()
     if args.gpus != 1:
         print("bench.py measures one GPU: every box in this build has a single MI355X and the decode "
               "path is not sharded across GPUs (see DESIGN.md for how it would shard)", file=sys.stderr)
@@ -197,6 +237,13 @@ def main() -> int:
     del qc, kc, vc
     log(f"config-4 decode attention: {c4_ms * 1000:.1f} us, {c4_gbs:.0f} GB/s")
 
+    # HBM traffic per launch from the committed PMC record of the same launch
+    # shape (FETCH_SIZE + WRITE_SIZE, calibrated on a copy of known size).
+    traffic = None
+    pmc = ROOT / "profiles" / "decode_attention_324m_b16_len3584_pmc.json"
+    if pmc.exists() and length == 3584:
+        traffic = json.loads(pmc.read_text())["traffic_bytes"]
+
     e2e_bytes = step_bytes(cfg, BATCH, mean_len)
     e2e_gbs = e2e_bytes / (ms_per_step * 1e-3) / 1e9
     baseline = None
@@ -225,7 +272,8 @@ def main() -> int:
                    "prompt": PROMPT, "context": CONTEXT, "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "kernel": "decode_attn_kernel (split-KV decode attention, one launch)",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "traffic_source": "profiles/decode_attention_324m_b16_len3584_pmc.json" if traffic else None,
                      "bytes_per_launch": attn_bytes, "us_per_launch": round(attn_ms * 1000, 2),
                      "shape": f"B={BATCH} H={cfg.num_heads} D={cfg.head_dim} length={length} (mean of timed region)"},
         "e2e": {"bytes_per_step": int(e2e_bytes), "achieved_gbs": round(e2e_gbs, 1),

@@ -94,16 +94,19 @@ __global__ __launch_bounds__(W * kWave) void decode_attn_kernel(
   const T* kb = k + row0 * D + dg * EPL;
   const T* vb = v + row0 * D + dg * EPL;
 
+  // Rows past the wave's range are clamped to its last row: the masked lanes
+  // of a partial tile re-read a cached row instead of fetching new HBM lines.
+  const int last = wend - 1;
   for (int t0 = wbegin; t0 < wend; t0 += TILE) {
     uint4 kr[NL], vr[NL];
 #pragma unroll
     for (int i = 0; i < NL; ++i) {
-      const int tc = min(t0 + i * TPL + slot, cap - 1);
+      const int tc = min(t0 + i * TPL + slot, last);
       kr[i] = load16_stream(kb + long(tc) * D);
     }
 #pragma unroll
     for (int i = 0; i < NL; ++i) {
-      const int tc = min(t0 + i * TPL + slot, cap - 1);
+      const int tc = min(t0 + i * TPL + slot, last);
       vr[i] = load16_stream(vb + long(tc) * D);
     }
     float sc[G][NL];
