@@ -80,45 +80,65 @@ int sfl_decode_attention(const void* q, const void* k, const void* v, const int3
  */
 
 /*
+ * Normalized GEMV inputs. RMSNorm(x) @ W^T is computed as
+ * (x * g) @ W^T / sqrt(sum(x^2) / d_model + 1e-5) (layers.py:133-141), so a
+ * normalized consumer takes
+ *   act [batch, d_model]      x * g in the activation format (fp32 for F32
+ *                             weights, BF16X2 for BF16 weights), and
+ *   ss  [batch, d_model / 16] fp32 sums of x^2 over each 16-feature tile,
+ * written by the producer of x (sfl_linear_residual, sfl_next_token or
+ * sfl_norm_act). Normalized consumers need d_model % 64 == 0, d_model <= 2048.
+ */
+
+/* act = x * gain and ss for a fp32 x [batch, d_model] (d_model % 16 == 0). */
+int sfl_norm_act(const float* x, const void* gain, void* act, float* ss, int batch, int d_model,
+                 int dtype, void* stream);
+
+/*
  * q/k/v projections of RMSNorm(x) with RoPE and the KV-cache append.
  * Replaces, for one position, TransformerBlock's attn_norm + q/k/v_proj + RoPE
  * (src/llmlab/model/transformer.py:46, layers.py:133-141,
  * attention.py:160-185); the reference recomputes K/V for every position.
+ *   act, ss  the normalized input (attn_norm gain folded into act)
  *   w_qkv    [3*d_model, d_model]: q_proj, k_proj, v_proj rows stacked
  *   cos_t, sin_t [capacity, head_dim/2] fp32 (the table of attention.py:31-42)
  *   pos      [batch] int32 position of this token; k/v are written at pos[b]
  *   q_out    [batch, heads, head_dim] fp32; k_cache, v_cache [batch, heads, capacity, head_dim]
  */
-int sfl_rmsnorm_qkv_rope_append(const float* x, const void* norm_w, const void* w_qkv,
+int sfl_rmsnorm_qkv_rope_append(const void* act, const float* ss, const void* w_qkv,
                                 const float* cos_t, const float* sin_t, const int32_t* pos,
                                 void* q_out, void* k_cache, void* v_cache, int batch,
                                 int d_model, int heads, int capacity, int dtype, void* stream);
 
 /*
- * x_out = x + act @ w^T (act [batch, k]: fp32 for F32 weights, BF16X2 for
- * BF16 weights; w [n, k]; x/x_out fp32 [batch, n],
- * x_out may alias x). Replaces output_proj + residual and ffn.w2 + residual
- * (transformer.py:46-47, attention.py:199-203, layers.py:114-115).
+ * x_out = x + act @ w^T (act [batch, k] in the activation format; w [n, k];
+ * x/x_out fp32 [batch, n], x_out may alias x). Replaces output_proj + residual
+ * and ffn.w2 + residual (transformer.py:46-47, attention.py:199-203,
+ * layers.py:114-115). With gain_next (the next RMSNorm's weight, n % 16 == 0)
+ * it also writes act_next = x_out * gain_next and ss_next [batch, n/16], the
+ * normalized input of the next consumer; gain_next may be NULL.
  */
-int sfl_linear_residual(const void* act, const void* w, const float* x, float* x_out, int batch,
-                        int n, int k, int dtype, void* stream);
+int sfl_linear_residual(const void* act, const void* w, const float* x, float* x_out,
+                        const void* gain_next, void* act_next, float* ss_next, int batch, int n,
+                        int k, int dtype, void* stream);
 
 /*
  * h = silu(RMSNorm(x) @ w1^T) * (RMSNorm(x) @ w3^T), h [batch, d_ff] in the
- * GEMV activation format (fp32, or BF16X2 for BF16 weights).
+ * activation format. act/ss: the normalized input (ffn_norm gain folded in).
  * Replaces ffn_norm + SwiGLU's w1/w3 half (transformer.py:47, layers.py:73-115).
  */
-int sfl_rmsnorm_swiglu(const float* x, const void* norm_w, const void* w1, const void* w3,
+int sfl_rmsnorm_swiglu(const void* act, const float* ss, const void* w1, const void* w3,
                        void* h_out, int batch, int d_model, int d_ff, int dtype, void* stream);
 
 /*
  * logits = RMSNorm(x) @ w_head^T plus a per-tile argmax (lowest index on ties).
  * Replaces ln_final + lm_head (transformer.py:137-138) for the last position.
+ *   act, ss  the normalized input (ln_final gain folded in)
  *   logits   optional [.., vocab] fp32; row b is written at
  *            logits + b*logits_batch_stride + pos[b]*logits_pos_stride (pos may be NULL)
  *   best_val, best_idx [sfl_lm_head_tiles(vocab), best_stride]: the tile maxima
  */
-int sfl_rmsnorm_lm_head(const float* x, const void* norm_w, const void* w_head, void* logits,
+int sfl_rmsnorm_lm_head(const void* act, const float* ss, const void* w_head, void* logits,
                         long logits_batch_stride, const int32_t* pos, long logits_pos_stride,
                         float* best_val, int32_t* best_idx, int best_stride, int batch,
                         int d_model, int vocab, int dtype, void* stream);
@@ -137,14 +157,15 @@ int sfl_embedding_gather(const int64_t* tokens, long token_stride, const int32_t
  * Greedy step: argmax over the lm_head tiles (first maximal index, as
  * torch.argmax), then, with np = pos[b] + 1: predicted[b, np] = argmax;
  * tokens[b, np] = argmax unless np < prompt_len[b] (the prompt token is kept);
- * x[b] = emb[tokens[b, np]]; pos[b] = np; lengths[b] = np + 1. Nothing changes
- * for a row whose np would reach capacity. The reference has no token loop;
- * its greedy continuation is argmax(TransformerLM.forward(ids)[:, -1]).
+ * x[b] = emb[tokens[b, np]] with act[b] = x[b] * gain0 and ss[b] (the first
+ * layer's normalized input, d_model % 16 == 0); pos[b] = np; lengths[b] = np + 1.
+ * Nothing changes for a row whose np would reach capacity. The reference has
+ * no token loop; its greedy continuation is argmax(TransformerLM.forward(ids)[:, -1]).
  */
 int sfl_next_token(const float* best_val, const int32_t* best_idx, int tiles, int64_t* tokens,
                    int64_t* predicted, long token_stride, const int32_t* prompt_len, int32_t* pos,
-                   int32_t* lengths, const void* emb, float* x, int batch, int d_model,
-                   int capacity, int dtype, void* stream);
+                   int32_t* lengths, const void* emb, float* x, const void* gain0, void* act,
+                   float* ss, int batch, int d_model, int capacity, int dtype, void* stream);
 
 /* ---- masked prefill attention ----------------------------------------------
  * Replaces attention_lab/triton_attention.py `attention` (:326-438) and its

@@ -16,19 +16,23 @@
 // MFMAs (the GEMV is bandwidth-bound, so the second MFMA is free), which keeps
 // ~16 mantissa bits of the activation instead of 8.
 //
-// Prologue NORM: act = RMSNorm(x) from the fp32 residual stream, staged in LDS
-// (layers.py:133-141: x / sqrt(mean(x^2) + eps) * w). Prologue plain: fp32
-// activations read straight from global memory (each wave needs only its own
-// K chunks, so there is nothing to share through LDS).
+// RMSNorm is deferred (layers.py:133-141): RMSNorm(x) W^T = (1/rms(x)) *
+// ((x * g) W^T). The kernel that produces x (a residual epilogue, or the
+// token step) also writes the next consumer's input x * g in the activation
+// format and the per-16-feature partial sums of x^2; the consumer reads its
+// K chunks of x * g straight from global memory (each wave needs only its own
+// chunks, so nothing is staged in LDS) and scales its sums by
+// 1 / sqrt(sum(x^2) / K + eps), adding the partials in a fixed order.
 // Epilogues:
 //   QKV      RoPE on q and k (attention.py:44-58) with the host-built fp32
 //            table; q to an fp32 [B, H, dk] buffer, k/v appended to the
 //            model-dtype [B, H, cap, dk] cache at each row's position.
-//   RESIDUAL x += W act (transformer.py:46-47).
+//   RESIDUAL x += W act (transformer.py:46-47), then x * g_next and the
+//            partial sums of x^2 for the next normalized consumer.
 //   SWIGLU   h = silu(W1 act) * (W3 act) in fp32 (layers.py:114-115).
 //   LOGITS   lm_head rows (transformer.py:137-138) plus a per-tile argmax with
 //            the lowest index winning ties, taken on the fp32 accumulators.
-#include "common.hpp"
+#include "act_format.hpp"
 
 namespace sfl {
 namespace {
@@ -41,14 +45,12 @@ enum Epi { EPI_QKV = 0, EPI_RESIDUAL = 1, EPI_SWIGLU = 2, EPI_LOGITS = 3 };
 constexpr int kWaves = 8;       // waves per workgroup (K split)
 constexpr int kTileN = 16;      // output features per workgroup
 constexpr int kMaxRows = 16;    // batch rows per launch
-constexpr int kPadBytes = 16;   // LDS row padding against bank conflicts
-constexpr int kNormVecs = 8;    // float4 per lane per row in the RMSNorm prologue: K <= 2048
+constexpr int kMaxSsTiles = 128; // 16-feature tiles of a normalized input: d_model <= 2048
 constexpr float kEps = 1e-5f;
 
 struct LinearArgs {
-  const float* x;        // fp32 residual [B, K] (NORM prologue) / residual base (RESIDUAL)
-  const void* act;       // activations [B, K] in the activation format (plain prologue)
-  const void* norm_w;    // [K]
+  const void* act;       // [B, K] activation format (x * g for normalized consumers)
+  const float* ss;       // [B, K/16] partial sums of x^2 (normalized consumers), else nullptr
   const void* w;         // [N, K]
   const void* w3;        // [N, K] second matrix of SWIGLU
   int batch, n, k;
@@ -61,7 +63,11 @@ struct LinearArgs {
   void* v_cache;
   int heads, head_dim, cap, d_model;
   // RESIDUAL
-  float* x_out;          // [B, N]
+  const float* x;        // fp32 residual [B, N]
+  float* x_out;          // [B, N] (may alias x)
+  const void* gain_next; // optional [N] gain of the next normalized consumer
+  void* act_next;        // its input x_out * gain_next, [B, N] activation format
+  float* ss_next;        // its partial sums of x_out^2, [B, N/16]
   // SWIGLU
   void* h_out;           // [B, N] in the activation format
   // LOGITS
@@ -114,14 +120,9 @@ __device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
   return v > bv || (v == bv && i < bi);
 }
 
-// Activation operand format, 4 bytes per element in both cases:
-//   fp32 weights: plain fp32 values;
-//   bf16 weights: each group of 8 consecutive values is stored as 8 "hi" bf16
-//   followed by 8 "lo" bf16 (32 bytes), with hi = x truncated to bf16 and
-//   lo = (x - hi) truncated to bf16, so hi + lo keeps ~16 mantissa bits of x
-//   and one lane's chunk is exactly the two MFMA B operands.
-// Producers (the RMSNorm prologue, the SwiGLU epilogue, the attention merge)
-// write this format once; the GEMV loop then does no conversion.
+// One lane's chunk of the activation format (act_format.hpp). Producers (the
+// residual epilogues, the token step, the SwiGLU epilogue, the attention
+// merge) write the format once; the GEMV loop then does no conversion.
 template <typename T> struct ActChunk;
 template <> struct ActChunk<float> { uint4 v; };
 template <> struct ActChunk<bf16_t> { uint4 hi, lo; };
@@ -152,52 +153,19 @@ __device__ __forceinline__ f32x4 mfma_act<float>(const uint4& w, const ActChunk<
   return mfma_chunk<float>(w, b, acc);
 }
 
-// Four consecutive RMSNorm gains as fp32 (one 8- or 16-byte load).
-template <typename T> __device__ __forceinline__ float4 load_gain4(const T* p);
-template <> __device__ __forceinline__ float4 load_gain4<float>(const float* p) {
-  return *reinterpret_cast<const float4*>(p);
-}
-template <> __device__ __forceinline__ float4 load_gain4<bf16_t>(const bf16_t* p) {
-  const uint2 w = *reinterpret_cast<const uint2*>(p);
-  return make_float4(bf16_lo(w.x), bf16_hi(w.x), bf16_lo(w.y), bf16_hi(w.y));
-}
-
-// Store 4 consecutive activation values (element index e, e % 4 == 0) of a row.
-template <typename T>
-__device__ __forceinline__ void store_act4(unsigned char* row, int e, const float* v);
-template <>
-__device__ __forceinline__ void store_act4<float>(unsigned char* row, int e, const float* v) {
-  *reinterpret_cast<float4*>(row + size_t(e) * 4) = make_float4(v[0], v[1], v[2], v[3]);
-}
-template <>
-__device__ __forceinline__ void store_act4<bf16_t>(unsigned char* row, int e, const float* v) {
-  uint32_t hb[4], lb[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    hb[i] = __float_as_uint(v[i]) & 0xffff0000u;
-    lb[i] = __float_as_uint(v[i] - __uint_as_float(hb[i])) & 0xffff0000u;
-  }
-  unsigned char* g = row + size_t(e / 8) * 32 + (e % 8) * 2;
-  *reinterpret_cast<uint2*>(g) = make_uint2((hb[0] >> 16) | hb[1], (hb[2] >> 16) | hb[3]);
-  *reinterpret_cast<uint2*>(g + 16) = make_uint2((lb[0] >> 16) | lb[1], (lb[2] >> 16) | lb[3]);
-}
-
 // CPW: weight chunks each wave loads per round (one round when K/chunk_k <= kWaves*CPW);
 // chosen on the host from K so no wave issues more loads than it needs.
-template <typename T, int E, bool NORM, int CPW>
+template <typename T, int E, int CPW>
 __global__ __launch_bounds__(kWaves * kWave) void linear_kernel(LinearArgs a) {
   constexpr int kChunkGroup = CPW;
-  extern __shared__ __align__(16) unsigned char smem[];
   constexpr int EPL = vec_elems<T>();  // k values per lane per chunk
   constexpr int KC = chunk_k<T>();
   constexpr bool kTwo = (E == EPI_SWIGLU);
+  __shared__ float red[kWaves * kWave * (kTwo ? 8 : 4)];
   const int tid = threadIdx.x;
   const int wave = tid / kWave;
   const int lane = tid % kWave;
   const int K = a.k;
-  const int ld = K * 4 + kPadBytes;  // LDS row stride in bytes (activation format)
-  unsigned char* act_s = smem;
-  float* red = reinterpret_cast<float*>(smem + (NORM ? size_t(kMaxRows) * ld : 0));
 
   const int n0 = blockIdx.x * kTileN;
   const int row = min(n0 + lane % 16, a.n - 1);
@@ -205,18 +173,17 @@ __global__ __launch_bounds__(kWaves * kWave) void linear_kernel(LinearArgs a) {
   const int b = lane % 16;
   const T* wrow = static_cast<const T*>(a.w) + long(row) * K + grp * EPL;
   const T* w3row = kTwo ? static_cast<const T*>(a.w3) + long(row) * K + grp * EPL : nullptr;
-  // Plain prologue: this lane's activation row, read straight from global memory.
   const unsigned char* arow = static_cast<const unsigned char*>(a.act) +
                               (long(min(b, a.batch - 1)) * K + grp * EPL) * 4;
   const bool live = b < a.batch;
   const int nchunks = K / KC;
 
-  // Issue the first group of weight (and plain activation) loads up front.
-  // Loads are unconditional, from clamped addresses, and masked where they are
-  // used: a load whose value is consumed inside its own guard makes the
-  // compiler wait for it on the spot, serialising the memory round trips.
+  // Issue the first group of weight and activation loads up front. Loads are
+  // unconditional, from clamped addresses, and masked where they are used: a
+  // load whose value is consumed inside its own guard makes the compiler wait
+  // for it on the spot, serialising the memory round trips.
   uint4 wa[kChunkGroup], wb[kTwo ? kChunkGroup : 1];
-  ActChunk<T> af[NORM ? 1 : kChunkGroup];
+  ActChunk<T> af[kChunkGroup];
   int c0 = wave;
   const int last = nchunks - 1;
 #pragma unroll
@@ -224,88 +191,49 @@ __global__ __launch_bounds__(kWaves * kWave) void linear_kernel(LinearArgs a) {
     const long c = min(c0 + j * kWaves, last);
     wa[j] = load16(wrow + c * KC);
     if constexpr (kTwo) wb[j] = load16(w3row + c * KC);
-    if constexpr (!NORM) af[j] = load_act<T>(arow + c * KC * 4);
+    af[j] = load_act<T>(arow + c * KC * 4);
   }
 
   // Prefetch what wave 0's epilogue reads, so it overlaps the weight loads.
   const int n = n0 + 4 * grp;  // this lane's features n .. n+3 of batch row b
-  float4 pre_x = make_float4(0.f, 0.f, 0.f, 0.f);
+  float4 pre_x = make_float4(0.f, 0.f, 0.f, 0.f), pre_g = make_float4(0.f, 0.f, 0.f, 0.f);
   float2 pre_c = make_float2(0.f, 0.f), pre_s = make_float2(0.f, 0.f);
   int pre_p = 0;
-  if (wave == 0 && live && n < a.n) {
+  float ssum = 0.f;  // this lane's share of sum(x^2) of row b (normalized consumers)
+  const int ntiles = K / 16;
+  const int nl = min(n, a.n - 4);
+  if (wave == 0) {
+    if (a.ss) {
+      const float* sr = a.ss + long(min(b, a.batch - 1)) * ntiles;
+      const int per = ntiles / 4;  // tiles summed by each of the 4 lanes of row b
+      float part[kMaxSsTiles / 4];
+#pragma unroll
+      for (int t = 0; t < kMaxSsTiles / 4; ++t) part[t] = sr[grp * per + min(t, per - 1)];
+#pragma unroll
+      for (int t = 0; t < kMaxSsTiles / 4; ++t)
+        if (t < per) ssum += part[t];
+    }
     if constexpr (E == EPI_RESIDUAL) {
-      pre_x = *reinterpret_cast<const float4*>(a.x + long(b) * a.n + n);
+      pre_x = *reinterpret_cast<const float4*>(a.x + long(min(b, a.batch - 1)) * a.n + nl);
+      if (a.gain_next) pre_g = load_gain4<T>(static_cast<const T*>(a.gain_next) + nl);
     } else if constexpr (E == EPI_QKV) {
-      pre_p = a.pos[b];
-      if (n < 2 * a.d_model) {
-        const int half = a.head_dim / 2;
-        const long at = long(pre_p) * half + (n % a.d_model % a.head_dim) / 2;
-        pre_c = *reinterpret_cast<const float2*>(a.cos_t + at);
-        pre_s = *reinterpret_cast<const float2*>(a.sin_t + at);
-      }
+      pre_p = a.pos[min(b, a.batch - 1)];
+      const int half = a.head_dim / 2;
+      const long at = long(pre_p) * half + (nl % a.d_model % a.head_dim) / 2;
+      pre_c = *reinterpret_cast<const float2*>(a.cos_t + at);
+      pre_s = *reinterpret_cast<const float2*>(a.sin_t + at);
     }
-  }
-
-  if constexpr (NORM) {
-    // RMSNorm rows into LDS in the activation format (layers.py:133-141:
-    // x / sqrt(mean(x^2) + eps) * w, here x * (1 / sqrt(...)) * w); pad rows
-    // are zero. Each wave owns kMaxRows/kWaves rows and issues every load of
-    // its rows and of the gain before the first use: one memory round trip.
-    constexpr int R = kMaxRows / kWaves;
-    const T* nw = static_cast<const T*>(a.norm_w);
-    float4 xv[R][kNormVecs];
-    float4 gv[kNormVecs];
-#pragma unroll
-    for (int j = 0; j < kNormVecs; ++j) {
-      const int col = min((lane + j * kWave) * 4, K - 4);
-      gv[j] = load_gain4<T>(nw + col);
-    }
-#pragma unroll
-    for (int rr = 0; rr < R; ++rr) {
-      const float* xr = a.x + long(min(wave + rr * kWaves, a.batch - 1)) * K;
-#pragma unroll
-      for (int j = 0; j < kNormVecs; ++j) {
-        const int col = min((lane + j * kWave) * 4, K - 4);
-        xv[rr][j] = *reinterpret_cast<const float4*>(xr + col);
-      }
-    }
-#pragma unroll
-    for (int rr = 0; rr < R; ++rr) {
-      const int r = wave + rr * kWaves;
-      float ss = 0.f;
-#pragma unroll
-      for (int j = 0; j < kNormVecs; ++j) {
-        const float4 v = xv[rr][j];
-        if ((lane + j * kWave) * 4 < K) ss = fmaf(v.x, v.x, fmaf(v.y, v.y, fmaf(v.z, v.z, fmaf(v.w, v.w, ss))));
-      }
-      ss = wave_sum(ss);
-      const float inv = r < a.batch ? 1.f / sqrtf(ss / float(K) + kEps) : 0.f;
-      unsigned char* dst = act_s + size_t(r) * ld;
-#pragma unroll
-      for (int j = 0; j < kNormVecs; ++j) {
-        const int col = (lane + j * kWave) * 4;
-        if (col < K) {
-          const float4 v = xv[rr][j];
-          const float4 g = gv[j];
-          const float h[4] = {(v.x * inv) * g.x, (v.y * inv) * g.y, (v.z * inv) * g.z, (v.w * inv) * g.w};
-          store_act4<T>(dst, col, h);
-        }
-      }
-    }
-    __syncthreads();
   }
 
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   f32x4 acc3 = {0.f, 0.f, 0.f, 0.f};
-  const unsigned char* bsrc = act_s + size_t(b) * ld + grp * EPL * 4;
   for (;;) {
 #pragma unroll
     for (int j = 0; j < kChunkGroup; ++j) {
       const int c = c0 + j * kWaves;
       if (c < nchunks) {
-        const ActChunk<T> x = NORM ? load_act<T>(bsrc + size_t(c) * KC * 4) : af[j];
-        acc = mfma_act<T>(wa[j], x, live || NORM, acc);
-        if constexpr (kTwo) acc3 = mfma_act<T>(wb[j], x, live || NORM, acc3);
+        acc = mfma_act<T>(wa[j], af[j], live, acc);
+        if constexpr (kTwo) acc3 = mfma_act<T>(wb[j], af[j], live, acc3);
       }
     }
     c0 += kChunkGroup * kWaves;
@@ -315,7 +243,7 @@ __global__ __launch_bounds__(kWaves * kWave) void linear_kernel(LinearArgs a) {
       const long c = min(c0 + j * kWaves, last);
       wa[j] = load16(wrow + c * KC);
       if constexpr (kTwo) wb[j] = load16(w3row + c * KC);
-      if constexpr (!NORM) af[j] = load_act<T>(arow + c * KC * 4);
+      af[j] = load_act<T>(arow + c * KC * 4);
     }
   }
 
@@ -335,6 +263,17 @@ __global__ __launch_bounds__(kWaves * kWave) void linear_kernel(LinearArgs a) {
     for (int i = 0; i < 4; ++i) {
       v1[i] += p[i];
       if constexpr (kTwo) v3[i] += p[4 + i];
+    }
+  }
+  if (a.ss) {
+    // sum(x^2) over the row in a fixed order: lane partials, then lane groups.
+    ssum += __shfl_xor(ssum, 16, kWave);
+    ssum += __shfl_xor(ssum, 32, kWave);
+    const float inv = 1.f / sqrtf(ssum / float(K) + kEps);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v1[i] *= inv;
+      v3[i] *= inv;
     }
   }
 
@@ -367,11 +306,25 @@ __global__ __launch_bounds__(kWaves * kWave) void linear_kernel(LinearArgs a) {
     }
     return;
   }
-  if (!live || n >= a.n) return;
   if constexpr (E == EPI_RESIDUAL) {
-    *reinterpret_cast<float4*>(a.x_out + long(b) * a.n + n) =
-        make_float4(pre_x.x + v1[0], pre_x.y + v1[1], pre_x.z + v1[2], pre_x.w + v1[3]);
-  } else if constexpr (E == EPI_SWIGLU) {
+    const float xo[4] = {pre_x.x + v1[0], pre_x.y + v1[1], pre_x.z + v1[2], pre_x.w + v1[3]};
+    if (a.gain_next) {
+      // Partial sum of x^2 over this workgroup's 16 features (4 lanes of row b).
+      float sq = xo[0] * xo[0] + xo[1] * xo[1] + xo[2] * xo[2] + xo[3] * xo[3];
+      sq += __shfl_xor(sq, 16, kWave);
+      sq += __shfl_xor(sq, 32, kWave);
+      if (live && n < a.n) {
+        const float gx[4] = {xo[0] * pre_g.x, xo[1] * pre_g.y, xo[2] * pre_g.z, xo[3] * pre_g.w};
+        store_act4<T>(static_cast<unsigned char*>(a.act_next) + size_t(b) * a.n * 4, n, gx);
+        if (grp == 0) a.ss_next[long(b) * (a.n / 16) + blockIdx.x] = sq;
+      }
+    }
+    if (live && n < a.n)
+      *reinterpret_cast<float4*>(a.x_out + long(b) * a.n + n) = make_float4(xo[0], xo[1], xo[2], xo[3]);
+    return;
+  }
+  if (!live || n >= a.n) return;
+  if constexpr (E == EPI_SWIGLU) {
     float h[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) h[i] = v1[i] / (1.f + expf(-v1[i])) * v3[i];
@@ -403,40 +356,30 @@ __global__ __launch_bounds__(kWaves * kWave) void linear_kernel(LinearArgs a) {
   }
 }
 
-template <typename T, int E, bool NORM, int CPW>
+template <typename T, int E, int CPW>
 int launch_linear_cpw(const LinearArgs& a, hipStream_t stream, const char* what) {
-  const size_t lds = (NORM ? size_t(kMaxRows) * (size_t(a.k) * 4 + kPadBytes) : 0) +
-                     size_t(kWaves) * kWave * (E == EPI_SWIGLU ? 8 : 4) * sizeof(float);
-  if (lds > 160 * 1024)
-    return set_error(SFL_ERR_UNSUPPORTED, "%s: K=%d needs %zu bytes of LDS (max 163840)", what, a.k, lds);
-  if (NORM && a.k > kNormVecs * kWave * 4)
-    return set_error(SFL_ERR_UNSUPPORTED, "%s: RMSNorm prologue supports d_model <= %d", what, kNormVecs * kWave * 4);
-  static bool attr_set = false;
-  if (!attr_set) {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&linear_kernel<T, E, NORM, CPW>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-    attr_set = true;
-  }
   const unsigned tiles = unsigned((a.n + kTileN - 1) / kTileN);
-  hipLaunchKernelGGL((linear_kernel<T, E, NORM, CPW>), dim3(tiles), dim3(kWaves * kWave), lds, stream, a);
+  hipLaunchKernelGGL((linear_kernel<T, E, CPW>), dim3(tiles), dim3(kWaves * kWave), 0, stream, a);
   return check_launch(what);
 }
 
-template <typename T, int E, bool NORM>
+template <typename T, int E>
 int launch_linear(const LinearArgs& a, hipStream_t stream, const char* what) {
   const int per_wave = (a.k / chunk_k<T>() + kWaves - 1) / kWaves;
-  if (per_wave <= 1) return launch_linear_cpw<T, E, NORM, 1>(a, stream, what);
-  if (per_wave <= 2) return launch_linear_cpw<T, E, NORM, 2>(a, stream, what);
-  if (per_wave <= 4) return launch_linear_cpw<T, E, NORM, 4>(a, stream, what);
-  if (per_wave <= 6) return launch_linear_cpw<T, E, NORM, 6>(a, stream, what);
-  if (per_wave <= 8) return launch_linear_cpw<T, E, NORM, 8>(a, stream, what);
-  return launch_linear_cpw<T, E, NORM, 11>(a, stream, what);  // larger K loops in rounds of 11
+  if (per_wave <= 1) return launch_linear_cpw<T, E, 1>(a, stream, what);
+  if (per_wave <= 2) return launch_linear_cpw<T, E, 2>(a, stream, what);
+  if (per_wave <= 4) return launch_linear_cpw<T, E, 4>(a, stream, what);
+  if (per_wave <= 6) return launch_linear_cpw<T, E, 6>(a, stream, what);
+  if (per_wave <= 8) return launch_linear_cpw<T, E, 8>(a, stream, what);
+  return launch_linear_cpw<T, E, 11>(a, stream, what);  // larger K loops in rounds of 11
 }
 
-int check_common(const char* what, int batch, int n, int k, int dtype) {
+// vec4: the epilogue moves 4 consecutive features per lane (all but LOGITS).
+int check_common(const char* what, int batch, int n, int k, int dtype, bool vec4 = true) {
   if (batch < 1 || batch > kMaxRows)
     return set_error(SFL_ERR_INVALID, "%s: batch must be in [1, %d] per launch", what, kMaxRows);
   if (n < 1 || k < 1) return set_error(SFL_ERR_INVALID, "%s: sizes must be positive", what);
+  if (vec4 && n % 4) return set_error(SFL_ERR_UNSUPPORTED, "%s: N must be a multiple of 4", what);
   if (dtype != SFL_DTYPE_F32 && dtype != SFL_DTYPE_BF16)
     return set_error(SFL_ERR_UNSUPPORTED, "%s: model dtype must be F32 or BF16", what);
   const int kc = dtype == SFL_DTYPE_BF16 ? chunk_k<bf16_t>() : chunk_k<float>();
@@ -444,10 +387,35 @@ int check_common(const char* what, int batch, int n, int k, int dtype) {
   return SFL_OK;
 }
 
-template <int E, bool NORM>
+// Normalized inputs: K/16 tiles of partial sums, split evenly over 4 lanes.
+int check_normed(const char* what, int k) {
+  if (k % 64 || k / 16 > kMaxSsTiles)
+    return set_error(SFL_ERR_UNSUPPORTED, "%s: normalized inputs need d_model %% 64 == 0 and <= %d", what,
+                     kMaxSsTiles * 16);
+  return SFL_OK;
+}
+
+template <int E>
 int dispatch_linear(const LinearArgs& a, int dtype, hipStream_t s, const char* what) {
-  if (dtype == SFL_DTYPE_BF16) return launch_linear<bf16_t, E, NORM>(a, s, what);
-  return launch_linear<float, E, NORM>(a, s, what);
+  if (dtype == SFL_DTYPE_BF16) return launch_linear<bf16_t, E>(a, s, what);
+  return launch_linear<float, E>(a, s, what);
+}
+
+// act = x * g and the per-tile sums of x^2 for a normalized consumer, from x.
+template <typename T>
+__global__ __launch_bounds__(64) void norm_act_kernel(const float* x, const T* gain, unsigned char* act,
+                                                      float* ss, int d) {
+  const int b = blockIdx.x;
+  const float* xr = x + long(b) * d;
+  for (int t = threadIdx.x; t < d / 16; t += kWave) {
+    float v[16];
+#pragma unroll
+    for (int i = 0; i < 16; i += 4) {
+      const float4 q = *reinterpret_cast<const float4*>(xr + 16 * t + i);
+      v[i] = q.x; v[i + 1] = q.y; v[i + 2] = q.z; v[i + 3] = q.w;
+    }
+    emit_tile<T>(v, gain, t, nullptr, act + size_t(b) * d * 4, ss + long(b) * (d / 16));
+  }
 }
 
 }  // namespace
@@ -455,66 +423,89 @@ int dispatch_linear(const LinearArgs& a, int dtype, hipStream_t s, const char* w
 
 using namespace sfl;
 
-extern "C" int sfl_rmsnorm_qkv_rope_append(const float* x, const void* norm_w, const void* w_qkv,
+extern "C" int sfl_rmsnorm_qkv_rope_append(const void* act, const float* ss, const void* w_qkv,
                                            const float* cos_t, const float* sin_t,
                                            const int32_t* pos, void* q_out, void* k_cache,
                                            void* v_cache, int batch, int d_model, int heads,
                                            int capacity, int dtype, void* stream) {
   const char* what = "rmsnorm_qkv_rope_append";
-  if (!x || !norm_w || !w_qkv || !cos_t || !sin_t || !pos || !q_out || !k_cache || !v_cache)
+  if (!act || !ss || !w_qkv || !cos_t || !sin_t || !pos || !q_out || !k_cache || !v_cache)
     return set_error(SFL_ERR_INVALID, "%s: null pointer argument", what);
   if (heads < 1 || d_model % heads) return set_error(SFL_ERR_INVALID, "%s: d_model must be divisible by heads", what);
   const int dk = d_model / heads;
   if (dk % 16) return set_error(SFL_ERR_UNSUPPORTED, "%s: head dim must be a multiple of 16", what);
   if (capacity < 1) return set_error(SFL_ERR_INVALID, "%s: capacity must be positive", what);
   if (int rc = check_common(what, batch, 3 * d_model, d_model, dtype)) return rc;
+  if (int rc = check_normed(what, d_model)) return rc;
   LinearArgs a{};
-  a.x = x; a.norm_w = norm_w; a.w = w_qkv; a.batch = batch; a.n = 3 * d_model; a.k = d_model;
+  a.act = act; a.ss = ss; a.w = w_qkv; a.batch = batch; a.n = 3 * d_model; a.k = d_model;
   a.cos_t = cos_t; a.sin_t = sin_t; a.pos = pos; a.q_out = q_out; a.k_cache = k_cache;
   a.v_cache = v_cache; a.heads = heads; a.head_dim = dk; a.cap = capacity; a.d_model = d_model;
-  return dispatch_linear<EPI_QKV, true>(a, dtype, static_cast<hipStream_t>(stream), what);
+  return dispatch_linear<EPI_QKV>(a, dtype, static_cast<hipStream_t>(stream), what);
 }
 
 extern "C" int sfl_linear_residual(const void* act, const void* w, const float* x, float* x_out,
-                                   int batch, int n, int k, int dtype, void* stream) {
+                                   const void* gain_next, void* act_next, float* ss_next, int batch,
+                                   int n, int k, int dtype, void* stream) {
   const char* what = "linear_residual";
   if (!act || !w || !x || !x_out) return set_error(SFL_ERR_INVALID, "%s: null pointer argument", what);
+  if (gain_next && (!act_next || !ss_next))
+    return set_error(SFL_ERR_INVALID, "%s: gain_next needs act_next and ss_next", what);
   if (int rc = check_common(what, batch, n, k, dtype)) return rc;
-  if (n % 4) return set_error(SFL_ERR_UNSUPPORTED, "%s: N must be a multiple of 4", what);
+  if (gain_next && n % 16) return set_error(SFL_ERR_UNSUPPORTED, "%s: N must be a multiple of 16", what);
   LinearArgs a{};
   a.act = act; a.w = w; a.x = x; a.x_out = x_out; a.batch = batch; a.n = n; a.k = k;
-  return dispatch_linear<EPI_RESIDUAL, false>(a, dtype, static_cast<hipStream_t>(stream), what);
+  a.gain_next = gain_next; a.act_next = act_next; a.ss_next = ss_next;
+  return dispatch_linear<EPI_RESIDUAL>(a, dtype, static_cast<hipStream_t>(stream), what);
 }
 
-extern "C" int sfl_rmsnorm_swiglu(const float* x, const void* norm_w, const void* w1, const void* w3,
+extern "C" int sfl_rmsnorm_swiglu(const void* act, const float* ss, const void* w1, const void* w3,
                                   void* h_out, int batch, int d_model, int d_ff, int dtype,
                                   void* stream) {
   const char* what = "rmsnorm_swiglu";
-  if (!x || !norm_w || !w1 || !w3 || !h_out) return set_error(SFL_ERR_INVALID, "%s: null pointer argument", what);
+  if (!act || !ss || !w1 || !w3 || !h_out) return set_error(SFL_ERR_INVALID, "%s: null pointer argument", what);
   if (int rc = check_common(what, batch, d_ff, d_model, dtype)) return rc;
-  if (d_ff % 4) return set_error(SFL_ERR_UNSUPPORTED, "%s: d_ff must be a multiple of 4", what);
+  if (int rc = check_normed(what, d_model)) return rc;
   LinearArgs a{};
-  a.x = x; a.norm_w = norm_w; a.w = w1; a.w3 = w3; a.h_out = h_out; a.batch = batch; a.n = d_ff;
+  a.act = act; a.ss = ss; a.w = w1; a.w3 = w3; a.h_out = h_out; a.batch = batch; a.n = d_ff;
   a.k = d_model;
-  return dispatch_linear<EPI_SWIGLU, true>(a, dtype, static_cast<hipStream_t>(stream), what);
+  return dispatch_linear<EPI_SWIGLU>(a, dtype, static_cast<hipStream_t>(stream), what);
 }
 
-extern "C" int sfl_rmsnorm_lm_head(const float* x, const void* norm_w, const void* w_head,
+extern "C" int sfl_rmsnorm_lm_head(const void* act, const float* ss, const void* w_head,
                                    void* logits, long logits_batch_stride, const int32_t* pos,
                                    long logits_pos_stride, float* best_val, int32_t* best_idx,
                                    int best_stride, int batch, int d_model, int vocab, int dtype,
                                    void* stream) {
   const char* what = "rmsnorm_lm_head";
-  if (!x || !norm_w || !w_head || !best_val || !best_idx)
+  if (!act || !ss || !w_head || !best_val || !best_idx)
     return set_error(SFL_ERR_INVALID, "%s: null pointer argument", what);
-  if (int rc = check_common(what, batch, vocab, d_model, dtype)) return rc;
+  if (int rc = check_common(what, batch, vocab, d_model, dtype, false)) return rc;
+  if (int rc = check_normed(what, d_model)) return rc;
   if (best_stride < batch) return set_error(SFL_ERR_INVALID, "%s: best_stride must be >= batch", what);
   LinearArgs a{};
-  a.x = x; a.norm_w = norm_w; a.w = w_head; a.logits = logits; a.logits_batch_stride = logits_batch_stride;
+  a.act = act; a.ss = ss; a.w = w_head; a.logits = logits; a.logits_batch_stride = logits_batch_stride;
   a.pos = pos; a.logits_pos_stride = logits_pos_stride; a.best_val = best_val; a.best_idx = best_idx;
   a.best_stride = best_stride;
   a.batch = batch; a.n = vocab; a.k = d_model;
-  return dispatch_linear<EPI_LOGITS, true>(a, dtype, static_cast<hipStream_t>(stream), what);
+  return dispatch_linear<EPI_LOGITS>(a, dtype, static_cast<hipStream_t>(stream), what);
+}
+
+extern "C" int sfl_norm_act(const float* x, const void* gain, void* act, float* ss, int batch, int d_model,
+                            int dtype, void* stream) {
+  const char* what = "norm_act";
+  if (!x || !gain || !act || !ss) return set_error(SFL_ERR_INVALID, "%s: null pointer argument", what);
+  if (batch < 1 || d_model < 16 || d_model % 16) return set_error(SFL_ERR_INVALID, "%s: d_model must be a multiple of 16", what);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == SFL_DTYPE_BF16)
+    hipLaunchKernelGGL(norm_act_kernel<bf16_t>, dim3(batch), dim3(64), 0, s, x, static_cast<const bf16_t*>(gain),
+                       static_cast<unsigned char*>(act), ss, d_model);
+  else if (dtype == SFL_DTYPE_F32)
+    hipLaunchKernelGGL(norm_act_kernel<float>, dim3(batch), dim3(64), 0, s, x, static_cast<const float*>(gain),
+                       static_cast<unsigned char*>(act), ss, d_model);
+  else
+    return set_error(SFL_ERR_UNSUPPORTED, "%s: model dtype must be F32 or BF16", what);
+  return check_launch(what);
 }
 
 extern "C" int sfl_lm_head_tiles(int vocab) { return (vocab + kTileN - 1) / kTileN; }

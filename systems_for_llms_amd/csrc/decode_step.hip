@@ -6,7 +6,7 @@
 // first maximal index. These kernels keep the whole loop on the device so a
 // decode step can be captured once and replayed: the next token, the position
 // and the attention lengths are advanced in place.
-#include "common.hpp"
+#include "act_format.hpp"
 
 namespace sfl {
 namespace {
@@ -30,13 +30,15 @@ __global__ __launch_bounds__(256) void embed_kernel(const int64_t* __restrict__ 
 // One wave per sequence: finish the argmax over the lm_head tiles (lowest
 // index on ties), record it, pick the next token (the given one while the
 // sequence is still inside its prompt, else the argmax), gather its
-// embedding into x and advance pos/lengths by one.
+// embedding into x, write the first layer's normalized-consumer input
+// (x * gain0 and the per-16-feature sums of x^2) and advance pos/lengths.
 template <typename T>
 __global__ __launch_bounds__(64) void next_token_kernel(
     const float* __restrict__ best_val, const int32_t* __restrict__ best_idx, int tiles, int batch,
     int64_t* __restrict__ tokens, int64_t* __restrict__ predicted, long stride,
     const int32_t* __restrict__ prompt_len, int32_t* __restrict__ pos, int32_t* __restrict__ lengths,
-    const T* __restrict__ emb, float* __restrict__ x, int d, int cap) {
+    const T* __restrict__ emb, float* __restrict__ x, const T* __restrict__ gain0,
+    unsigned char* __restrict__ act, float* __restrict__ ss, int d, int cap) {
   const int b = blockIdx.x;
   const int lane = threadIdx.x;
   const int p = pos[b];
@@ -70,27 +72,15 @@ __global__ __launch_bounds__(64) void next_token_kernel(
   const bool forced = np < plen;
   const long tok = forced ? given : long(bi);
   const T* src = emb + tok * d;
-  float* dst = x + long(b) * d;
   constexpr int V = vec_elems<T>();
-  if (d % V == 0) {
-    for (int i0 = 0; i0 < d; i0 += 4 * kWave * V) {
-      uint4 r[4];
+  for (int t = lane; t < d / 16; t += kWave) {  // one 16-feature tile per lane per round
+    uint4 r[16 / V];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) r[j] = load16(src + min(i0 + (lane + j * kWave) * V, d - V));
+    for (int j = 0; j < 16 / V; ++j) r[j] = load16(src + 16 * t + j * V);
+    float v[16];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int i = i0 + (lane + j * kWave) * V;
-        if (i < d) {
-          float f[V];
-          unpack16<T>(r[j], f);
-#pragma unroll
-          for (int e = 0; e < V; e += 4)
-            *reinterpret_cast<float4*>(dst + i + e) = make_float4(f[e], f[e + 1], f[e + 2], f[e + 3]);
-        }
-      }
-    }
-  } else {
-    for (int i = lane; i < d; i += kWave) dst[i] = load_scalar<T>(src + i);
+    for (int j = 0; j < 16 / V; ++j) unpack16<T>(r[j], v + j * V);
+    emit_tile<T>(v, gain0, t, x + long(b) * d, act + size_t(b) * d * 4, ss + long(b) * (d / 16));
   }
   if (lane == 0) {
     predicted[b * stride + np] = bi;
@@ -125,23 +115,27 @@ extern "C" int sfl_embedding_gather(const int64_t* tokens, long token_stride, co
 extern "C" int sfl_next_token(const float* best_val, const int32_t* best_idx, int tiles,
                               int64_t* tokens, int64_t* predicted, long token_stride,
                               const int32_t* prompt_len, int32_t* pos, int32_t* lengths,
-                              const void* emb, float* x, int batch, int d_model, int capacity,
-                              int dtype, void* stream) {
-  if (!best_val || !best_idx || !tokens || !predicted || !prompt_len || !pos || !lengths || !emb || !x)
+                              const void* emb, float* x, const void* gain0, void* act, float* ss,
+                              int batch, int d_model, int capacity, int dtype, void* stream) {
+  if (!best_val || !best_idx || !tokens || !predicted || !prompt_len || !pos || !lengths || !emb || !x ||
+      !gain0 || !act || !ss)
     return set_error(SFL_ERR_INVALID, "next_token: null pointer argument");
   if (batch < 1 || tiles < 1 || d_model < 1 || capacity < 1)
     return set_error(SFL_ERR_INVALID, "next_token: sizes must be positive");
+  if (d_model % 16) return set_error(SFL_ERR_UNSUPPORTED, "next_token: d_model must be a multiple of 16");
   if (token_stride < capacity)
     return set_error(SFL_ERR_INVALID, "next_token: token_stride must be >= capacity");
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (dtype == SFL_DTYPE_BF16)
     hipLaunchKernelGGL(next_token_kernel<bf16_t>, dim3(batch), dim3(64), 0, s, best_val, best_idx, tiles,
                        batch, tokens, predicted, token_stride, prompt_len, pos, lengths,
-                       static_cast<const bf16_t*>(emb), x, d_model, capacity);
+                       static_cast<const bf16_t*>(emb), x, static_cast<const bf16_t*>(gain0),
+                       static_cast<unsigned char*>(act), ss, d_model, capacity);
   else if (dtype == SFL_DTYPE_F32)
     hipLaunchKernelGGL(next_token_kernel<float>, dim3(batch), dim3(64), 0, s, best_val, best_idx, tiles,
                        batch, tokens, predicted, token_stride, prompt_len, pos, lengths,
-                       static_cast<const float*>(emb), x, d_model, capacity);
+                       static_cast<const float*>(emb), x, static_cast<const float*>(gain0),
+                       static_cast<unsigned char*>(act), ss, d_model, capacity);
   else
     return set_error(SFL_ERR_UNSUPPORTED, "next_token: model dtype must be F32 or BF16");
   return check_launch("next_token");

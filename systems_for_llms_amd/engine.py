@@ -10,6 +10,11 @@ a fixed sequence of C-ABI launches on the current stream:
                 -> linear_residual (w2)
     then:       rmsnorm_lm_head (+ tile argmax) -> next_token
 
+RMSNorm is folded into its consumer: whichever launch produces x (a residual
+GEMV or next_token) also writes ``act = x * g`` for the next norm's gain ``g``
+and the per-16-feature sums of x^2 (``ss``); the consumer scales its sums by
+the inverse RMS.
+
 All step state lives in device memory and is advanced by ``next_token``, so a
 step has no host inputs: it is captured once into a HIP graph and replayed.
 While a sequence is inside its prompt, ``next_token`` keeps the prompt token
@@ -42,6 +47,8 @@ class DecodeSession:
         cap = capacity or model.context_length
         if not 0 < cap <= model.context_length:
             raise ValueError("capacity must be in [1, context_length]")
+        if model.d_model % 64 or model.d_model > 2048:
+            raise ValueError("the decode step needs d_model % 64 == 0 and d_model <= 2048")
         self.model = model
         self.device = param.device
         self.dtype = param.dtype
@@ -65,6 +72,10 @@ class DecodeSession:
         self.q = torch.zeros((batch, h, self.dk), device=dev, dtype=torch.float32)
         self.attn = torch.zeros((batch, h, self.dk), device=dev, dtype=torch.float32)
         self.hidden = torch.zeros((batch, f), device=dev, dtype=torch.float32)
+        # Normalized input of the next RMSNorm consumer: x * g (activation format) and
+        # the sums of x^2 over each 16-feature tile.
+        self.act = torch.zeros((batch, d), device=dev, dtype=torch.float32)
+        self.ss = torch.zeros((batch, d // 16), device=dev, dtype=torch.float32)
         self.act_code = _lib.DTYPE_BF16X2 if dt == torch.bfloat16 else _lib.DTYPE_CODES[torch.float32]
         self.splits = splits or auto_splits(batch, h, cap)
         self.pmax = torch.empty((batch, h, self.splits), device=dev, dtype=torch.float32)
@@ -93,11 +104,12 @@ class DecodeSession:
         scale = float(dk) ** -0.5
         row_chunks = [(r, min(ROWS_PER_LAUNCH, self.batch - r)) for r in range(0, self.batch, ROWS_PER_LAUNCH)]
         self._row_chunks = row_chunks
+        gains = [blk.attn_norm.weight for blk in m.layers[1:]] + [m.ln_final.weight]
         for layer, blk in enumerate(m.layers):
             kc, vc = self.k_cache[layer], self.v_cache[layer]
             for r, rows in row_chunks:
                 calls.append((lib.sfl_rmsnorm_qkv_rope_append, (
-                    self.x[r].data_ptr(), blk.attn_norm.weight.data_ptr(), self.wqkv[layer].data_ptr(),
+                    self.act[r].data_ptr(), self.ss[r].data_ptr(), self.wqkv[layer].data_ptr(),
                     self.cos.data_ptr(), self.sin.data_ptr(), self.pos[r:].data_ptr(),
                     self.q[r].data_ptr(), kc[r].data_ptr(), vc[r].data_ptr(), rows, d, h, cap, code)))
             calls.append((lib.sfl_decode_attention, (
@@ -106,25 +118,27 @@ class DecodeSession:
                 self.batch, h, h, cap, dk, self.splits, scale, code, _lib.DTYPE_CODES[torch.float32],
                 self.act_code)))
             for r, rows in row_chunks:
+                x, act, ss = self.x[r].data_ptr(), self.act[r].data_ptr(), self.ss[r].data_ptr()
                 calls.append((lib.sfl_linear_residual, (
-                    self.attn[r].data_ptr(), blk.attn.output_proj.weight.data_ptr(), self.x[r].data_ptr(),
-                    self.x[r].data_ptr(), rows, d, d, code)))
+                    self.attn[r].data_ptr(), blk.attn.output_proj.weight.data_ptr(), x, x,
+                    blk.ffn_norm.weight.data_ptr(), act, ss, rows, d, d, code)))
                 calls.append((lib.sfl_rmsnorm_swiglu, (
-                    self.x[r].data_ptr(), blk.ffn_norm.weight.data_ptr(), blk.ffn.w1.weight.data_ptr(),
-                    blk.ffn.w3.weight.data_ptr(), self.hidden[r].data_ptr(), rows, d, f, code)))
+                    act, ss, blk.ffn.w1.weight.data_ptr(), blk.ffn.w3.weight.data_ptr(),
+                    self.hidden[r].data_ptr(), rows, d, f, code)))
                 calls.append((lib.sfl_linear_residual, (
-                    self.hidden[r].data_ptr(), blk.ffn.w2.weight.data_ptr(), self.x[r].data_ptr(),
-                    self.x[r].data_ptr(), rows, d, f, code)))
+                    self.hidden[r].data_ptr(), blk.ffn.w2.weight.data_ptr(), x, x,
+                    gains[layer].data_ptr(), act, ss, rows, d, f, code)))
         for r, rows in row_chunks:
             logits = self.logits[r].data_ptr() if self.logits is not None else None
             calls.append((lib.sfl_rmsnorm_lm_head, (
-                self.x[r].data_ptr(), m.ln_final.weight.data_ptr(), m.lm_head.weight.data_ptr(),
+                self.act[r].data_ptr(), self.ss[r].data_ptr(), m.lm_head.weight.data_ptr(),
                 logits, cap * v, self.pos[r:].data_ptr(), v, self.best_val[:, r:].data_ptr(),
                 self.best_idx[:, r:].data_ptr(), self.batch, rows, d, v, code)))
         calls.append((lib.sfl_next_token, (
             self.best_val.data_ptr(), self.best_idx.data_ptr(), self.tiles, self.tokens.data_ptr(),
             self.predicted.data_ptr(), cap, self.prompt_len.data_ptr(), self.pos.data_ptr(),
             self.lengths.data_ptr(), m.token_embeddings.weight.data_ptr(), self.x.data_ptr(),
+            m.layers[0].attn_norm.weight.data_ptr(), self.act.data_ptr(), self.ss.data_ptr(),
             self.batch, d, cap, code)))
         return calls
 
@@ -147,10 +161,19 @@ class DecodeSession:
         self.pos.zero_()
         self.lengths.fill_(1)
         self.prompt_len.fill_(forced_length or prompt.shape[1])
+        self._embed_current()
+
+    def _embed_current(self) -> None:
+        """x = embedding of each row's token at pos, plus the first layer's normalized input."""
         stream = _lib.stream_handle(self.device)
         _lib.call("sfl_embedding_gather", self.tokens.data_ptr(), self.cap, self.pos.data_ptr(),
                   self.model.token_embeddings.weight.data_ptr(), self.x.data_ptr(), self.batch,
                   self.d, self.code, stream)
+        self._norm_input(self.model.layers[0].attn_norm.weight, stream)
+
+    def _norm_input(self, gain, stream) -> None:
+        _lib.call("sfl_norm_act", self.x.data_ptr(), gain.data_ptr(), self.act.data_ptr(), self.ss.data_ptr(),
+                  self.batch, self.d, self.code, stream)
 
     # -- prefill ------------------------------------------------------------
     def _prefill_weights(self):
@@ -228,6 +251,7 @@ class DecodeSession:
             logits = logits.view(b, t, v)
         # Hand the last position to the decode head: pick token T and advance.
         self.x.copy_(x.view(b, t, d)[:, t - 1])
+        self._norm_input(self.model.ln_final.weight, st)
         self.pos.fill_(t - 1)
         self.lengths.fill_(t)
         for fn, args in self._calls[-(len(self._row_chunks) + 1):]:
@@ -241,9 +265,7 @@ class DecodeSession:
         """Rewind/advance every row to ``position`` (the cache below it is kept) and re-embed."""
         self.pos.fill_(position)
         self.lengths.fill_(position + 1)
-        _lib.call("sfl_embedding_gather", self.tokens.data_ptr(), self.cap, self.pos.data_ptr(),
-                  self.model.token_embeddings.weight.data_ptr(), self.x.data_ptr(), self.batch,
-                  self.d, self.code, _lib.stream_handle(self.device))
+        self._embed_current()
 
     # -- execution ----------------------------------------------------------
     def step(self) -> None:
