@@ -13,8 +13,8 @@
  * Element types are selected by an SFL_DTYPE_* code. In the decode-step
  * entry points weights and the KV cache use the model dtype; the residual
  * stream x and q are fp32; the GEMV inputs that other kernels produce (the
- * attention output, the SwiGLU hidden state) are fp32 for F32 models and
- * SFL_DTYPE_BF16X2 for BF16 models.
+ * attention output, the SwiGLU hidden state, x * g) are in the activation
+ * layout: SFL_DTYPE_F32X for F32 models and SFL_DTYPE_BF16X2 for BF16 models.
  */
 #ifndef SFL_H_
 #define SFL_H_
@@ -29,11 +29,17 @@ enum {
   SFL_DTYPE_F32 = 0,
   SFL_DTYPE_BF16 = 1,
   SFL_DTYPE_F16 = 2,
-  /* Activation format of the bf16 decode GEMVs, 4 bytes per value: each group
-   * of 8 consecutive values is stored as 8 bf16 "hi" halves (the values
-   * truncated to bf16) followed by 8 bf16 "lo" halves (the remainders
-   * truncated to bf16); hi + lo keeps ~16 mantissa bits. */
+  /* Inputs of the decode GEMVs ("activation layout"), 4 bytes per value, for a
+   * [B, K] matrix: blocks of 16 rows; each block is K/KC chunks of KC values
+   * (KC = 32 for BF16X2, 16 for F32X), and chunk c of a block is stored as 64
+   * lanes x 16 bytes, lane l = 16*g + r holding row r's values
+   * [c*KC + g*KC/4, c*KC + (g+1)*KC/4). BF16X2 stores each value as hi = the
+   * value truncated to bf16 and lo = the remainder truncated to bf16; a
+   * chunk's 64 lanes of hi halves (1 KB) are followed by its lo halves (1 KB),
+   * hi + lo keeping ~16 mantissa bits. F32X stores fp32 values (1 KB chunks).
+   * Buffers hold whole 16-row blocks: ceil(B/16) * 16 * K * 4 bytes. */
   SFL_DTYPE_BF16X2 = 3,
+  SFL_DTYPE_F32X = 4,
 };
 
 enum {
@@ -64,7 +70,8 @@ const char* sfl_last_error(void);
  * ceil(cap/splits) keys (decode.cu:50-52); chunks past a row's length do no
  * work. D in {16, 32, 64, 128}; Hq/Hkv in {1, 2, 4, 8}; splits in [1, 1024].
  * kv_dtype: element type of k and v (F32, BF16 or F16); q_dtype: kv_dtype or
- * F32; out_dtype: kv_dtype, F32 or BF16X2. Softmax state is fp32.
+ * F32; out_dtype: kv_dtype, F32, BF16X2 or F32X (the last two: the GEMV
+ * activation layout of [B, Hq*D]). Softmax state is fp32.
  */
 int sfl_decode_attention(const void* q, const void* k, const void* v, const int32_t* lengths,
                          float* partial_max, float* partial_sum, float* partial_out, void* out,
@@ -80,15 +87,26 @@ int sfl_decode_attention(const void* q, const void* k, const void* v, const int3
  */
 
 /*
+ * GEMV weights. The decode GEMVs read their [N, K] weights (the reference's
+ * Linear layout, layers.py:34-35) repacked by sfl_pack_gemv_weights into
+ * sfl_packed_gemv_elems(N, K) elements: for each tile of 16 rows and each K
+ * chunk (KC = 32 bf16 or 16 fp32 values), 64 lanes x 16 bytes, lane
+ * l = 16*g + r holding row r's values [c*KC + g*KC/4, c*KC + (g+1)*KC/4);
+ * rows past N are zero. All GEMV inputs are in the activation layout.
+ *
  * Normalized GEMV inputs. RMSNorm(x) @ W^T is computed as
  * (x * g) @ W^T / sqrt(sum(x^2) / d_model + 1e-5) (layers.py:133-141), so a
  * normalized consumer takes
- *   act [batch, d_model]      x * g in the activation format (fp32 for F32
- *                             weights, BF16X2 for BF16 weights), and
+ *   act [batch, d_model]      x * g in the activation layout, and
  *   ss  [batch, d_model / 16] fp32 sums of x^2 over each 16-feature tile,
  * written by the producer of x (sfl_linear_residual, sfl_next_token or
  * sfl_norm_act). Normalized consumers need d_model % 64 == 0, d_model <= 2048.
  */
+
+/* Elements of a packed [n, k] GEMV weight, and the packing itself (w and
+ * packed 16-byte aligned, k a multiple of the chunk size). */
+long sfl_packed_gemv_elems(int n, int k);
+int sfl_pack_gemv_weights(const void* w, void* packed, int n, int k, int dtype, void* stream);
 
 /* act = x * gain and ss for a fp32 x [batch, d_model] (d_model % 16 == 0). */
 int sfl_norm_act(const float* x, const void* gain, void* act, float* ss, int batch, int d_model,
@@ -100,7 +118,7 @@ int sfl_norm_act(const float* x, const void* gain, void* act, float* ss, int bat
  * (src/llmlab/model/transformer.py:46, layers.py:133-141,
  * attention.py:160-185); the reference recomputes K/V for every position.
  *   act, ss  the normalized input (attn_norm gain folded into act)
- *   w_qkv    [3*d_model, d_model]: q_proj, k_proj, v_proj rows stacked
+ *   w_qkv    packed [3*d_model, d_model]: q_proj, k_proj, v_proj rows stacked
  *   cos_t, sin_t [capacity, head_dim/2] fp32 (the table of attention.py:31-42)
  *   pos      [batch] int32 position of this token; k/v are written at pos[b]
  *   q_out    [batch, heads, head_dim] fp32; k_cache, v_cache [batch, heads, capacity, head_dim]
@@ -111,7 +129,7 @@ int sfl_rmsnorm_qkv_rope_append(const void* act, const float* ss, const void* w_
                                 int d_model, int heads, int capacity, int dtype, void* stream);
 
 /*
- * x_out = x + act @ w^T (act [batch, k] in the activation format; w [n, k];
+ * x_out = x + act @ w^T (act [batch, k] in the activation layout; w packed [n, k];
  * x/x_out fp32 [batch, n], x_out may alias x). Replaces output_proj + residual
  * and ffn.w2 + residual (transformer.py:46-47, attention.py:199-203,
  * layers.py:114-115). With gain_next (the next RMSNorm's weight, n % 16 == 0)
@@ -124,7 +142,8 @@ int sfl_linear_residual(const void* act, const void* w, const float* x, float* x
 
 /*
  * h = silu(RMSNorm(x) @ w1^T) * (RMSNorm(x) @ w3^T), h [batch, d_ff] in the
- * activation format. act/ss: the normalized input (ffn_norm gain folded in).
+ * activation layout. act/ss: the normalized input (ffn_norm gain folded in);
+ * w1, w3 packed [d_ff, d_model].
  * Replaces ffn_norm + SwiGLU's w1/w3 half (transformer.py:47, layers.py:73-115).
  */
 int sfl_rmsnorm_swiglu(const void* act, const float* ss, const void* w1, const void* w3,
@@ -133,7 +152,7 @@ int sfl_rmsnorm_swiglu(const void* act, const float* ss, const void* w1, const v
 /*
  * logits = RMSNorm(x) @ w_head^T plus a per-tile argmax (lowest index on ties).
  * Replaces ln_final + lm_head (transformer.py:137-138) for the last position.
- *   act, ss  the normalized input (ln_final gain folded in)
+ *   act, ss  the normalized input (ln_final gain folded in); w_head packed [vocab, d_model]
  *   logits   optional [.., vocab] fp32; row b is written at
  *            logits + b*logits_batch_stride + pos[b]*logits_pos_stride (pos may be NULL)
  *   best_val, best_idx [sfl_lm_head_tiles(vocab), best_stride]: the tile maxima

@@ -16,13 +16,16 @@ import torch
 LIB_PATH = Path(__file__).resolve().parent / "lib" / "libsfl.so"
 
 DTYPE_CODES = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
-DTYPE_BF16X2 = 3  # split-bf16 activation format of the bf16 decode GEMVs
+DTYPE_BF16X2 = 3  # split-bf16 values in the decode GEMVs' activation layout
+DTYPE_F32X = 4    # fp32 values in the decode GEMVs' activation layout
 
 P = c_void_p
 SIGNATURES: dict[str, list] = {
     "sfl_decode_attention": [P, P, P, P, P, P, P, P, c_int, c_int, c_int, c_int, c_int, c_int,
                              c_float, c_int, c_int, c_int, P],
     "sfl_norm_act": [P, P, P, P, c_int, c_int, c_int, P],
+    "sfl_packed_gemv_elems": [c_int, c_int],
+    "sfl_pack_gemv_weights": [P, P, c_int, c_int, c_int, P],
     "sfl_rmsnorm_qkv_rope_append": [P, P, P, P, P, P, P, P, P, c_int, c_int, c_int, c_int, c_int, P],
     "sfl_linear_residual": [P, P, P, P, P, P, P, c_int, c_int, c_int, c_int, P],
     "sfl_rmsnorm_swiglu": [P, P, P, P, P, c_int, c_int, c_int, c_int, P],
@@ -64,6 +67,7 @@ def lib() -> ctypes.CDLL:
             fn = getattr(handle, name)
             fn.argtypes = args
             fn.restype = c_int
+        handle.sfl_packed_gemv_elems.restype = c_long
         _LIB = handle
     return _LIB
 
@@ -75,6 +79,16 @@ def call(name: str, *args) -> None:
     if status != 0:
         message = handle.sfl_last_error().decode(errors="replace")
         raise RuntimeError(f"{name} failed ({status}): {message}")
+
+
+def pack_gemv(w: torch.Tensor) -> torch.Tensor:
+    """A decode-GEMV copy of a [N, K] weight in the packed tile layout (``sfl.h``)."""
+    n, k = w.shape
+    w = w.contiguous()
+    packed = torch.empty(lib().sfl_packed_gemv_elems(n, k), device=w.device, dtype=w.dtype)
+    call("sfl_pack_gemv_weights", w.data_ptr(), packed.data_ptr(), n, k, dtype_code(w.dtype),
+         stream_handle(w.device))
+    return packed
 
 
 def ptr(t: torch.Tensor | None) -> int | None:

@@ -14,13 +14,15 @@
 // softmax over the keys it loads, so the inner loop needs only the short
 // intra-row dot-product reduction; the slots are merged once at the end of
 // the chunk with xor shuffles. Max and sum are kept in base-2 units.
-#include "common.hpp"
+#include "act_format.hpp"
 
 namespace sfl {
 namespace {
 
-// Tag type of the split-bf16 output writer (see store_out<split_t>).
+// Tag types of the outputs in the decode GEMVs' activation layout (act_format.hpp):
+// split-bf16 values (BF16X2) and fp32 values (F32X).
 struct split_t {};
+struct f32x_t {};
 
 template <typename T, int D, int G>
 struct DecodeShape {
@@ -32,8 +34,9 @@ struct DecodeShape {
   static_assert(LPT >= 1 && LPT <= kWave, "head dim does not fit a wave");
 };
 
+// Store output element f = row * D + d of [batch * q_heads, D] (K = q_heads * D).
 template <typename TO>
-__device__ __forceinline__ void store_out(void* out, long f, float v);
+__device__ __forceinline__ void store_out(void* out, long f, int K, float v);
 
 // One workgroup of W waves per (batch, kv head, split). The split's keys are
 // divided among the waves; each wave streams its range with the per-slot
@@ -207,7 +210,7 @@ __global__ __launch_bounds__(W * kWave) void decode_attn_kernel(
     }
     const long qrow = long(b) * q_heads + h * G + g;
     if (splits == 1) {
-      store_out<TO>(out, qrow * D + d, den > 0.f ? num / den : 0.f);
+      store_out<TO>(out, qrow * D + d, q_heads * D, den > 0.f ? num / den : 0.f);
     } else {
       const long prow = qrow * splits + split;
       pout[prow * D + d] = num;
@@ -219,20 +222,19 @@ __global__ __launch_bounds__(W * kWave) void decode_attn_kernel(
   }
 }
 
-// Output writers of the merge: the KV dtype, fp32, or the split-bf16
-// activation format read by the bf16 GEMVs (groups of 8 values stored as 8
-// truncated-bf16 "hi" halves followed by 8 "lo" halves of the remainders).
+// Output writers: the KV dtype, fp32, or the GEMV activation layout of a
+// [batch, q_heads * D] input (split-bf16 or fp32 values).
 template <typename TO>
-__device__ __forceinline__ void store_out(void* out, long f, float v) {
+__device__ __forceinline__ void store_out(void* out, long f, int, float v) {
   store_scalar<TO>(static_cast<TO*>(out) + f, v);
 }
 template <>
-__device__ __forceinline__ void store_out<split_t>(void* out, long f, float v) {
-  const uint32_t hb = __float_as_uint(v) & 0xffff0000u;
-  const uint32_t lb = __float_as_uint(v - __uint_as_float(hb)) & 0xffff0000u;
-  uint16_t* g = reinterpret_cast<uint16_t*>(static_cast<unsigned char*>(out) + (f / 8) * 32) + f % 8;
-  g[0] = uint16_t(hb >> 16);
-  g[8] = uint16_t(lb >> 16);
+__device__ __forceinline__ void store_out<split_t>(void* out, long f, int K, float v) {
+  store_act1<bf16_t>(static_cast<unsigned char*>(out), int(f / K), int(f % K), K, v);
+}
+template <>
+__device__ __forceinline__ void store_out<f32x_t>(void* out, long f, int K, float v) {
+  store_act1<float>(static_cast<unsigned char*>(out), int(f / K), int(f % K), K, v);
 }
 
 // One wave per (batch, query head): combine the chunks below the row's length.
@@ -302,7 +304,7 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(
 #pragma unroll
   for (int i = 0; i < DPL; ++i) {
     const int d = lane + i * kWave;
-    if (d < D) store_out<TO>(out, row * D + d, den > 0.f ? num[i] / den : 0.f);
+    if (d < D) store_out<TO>(out, row * D + d, q_heads * D, den > 0.f ? num[i] / den : 0.f);
   }
 }
 
@@ -385,6 +387,7 @@ int attn_out(const DecodeCall& c, int out_dtype) {
   switch (out_dtype) {
     case SFL_DTYPE_F32: return attn_dims<T, TQ, float>(c);
     case SFL_DTYPE_BF16X2: return attn_dims<T, TQ, split_t>(c);
+    case SFL_DTYPE_F32X: return attn_dims<T, TQ, f32x_t>(c);
     default: return attn_dims<T, TQ, T>(c);
   }
 }
@@ -418,10 +421,12 @@ extern "C" int sfl_decode_attention(const void* q, const void* k, const void* v,
     return set_error(SFL_ERR_UNSUPPORTED, "decode_attention: unsupported dtype %d", kv_dtype);
   if (q_dtype != kv_dtype && q_dtype != SFL_DTYPE_F32)
     return set_error(SFL_ERR_UNSUPPORTED, "decode_attention: q dtype must equal the KV dtype or be F32");
-  if (out_dtype != kv_dtype && out_dtype != SFL_DTYPE_F32 && out_dtype != SFL_DTYPE_BF16X2)
-    return set_error(SFL_ERR_UNSUPPORTED, "decode_attention: out dtype must be the KV dtype, F32 or BF16X2");
-  if (out_dtype == SFL_DTYPE_BF16X2 && head_dim % 8)
-    return set_error(SFL_ERR_UNSUPPORTED, "decode_attention: BF16X2 output needs head_dim % 8 == 0");
+  const bool act_out = out_dtype == SFL_DTYPE_BF16X2 || out_dtype == SFL_DTYPE_F32X;
+  if (out_dtype != kv_dtype && out_dtype != SFL_DTYPE_F32 && !act_out)
+    return set_error(SFL_ERR_UNSUPPORTED, "decode_attention: out dtype must be the KV dtype, F32, BF16X2 or F32X");
+  if (act_out && (q_heads * head_dim) % (out_dtype == SFL_DTYPE_BF16X2 ? 32 : 16))
+    return set_error(SFL_ERR_UNSUPPORTED, "decode_attention: %s output needs q_heads*head_dim %% %d == 0",
+                     out_dtype == SFL_DTYPE_BF16X2 ? "BF16X2" : "F32X", out_dtype == SFL_DTYPE_BF16X2 ? 32 : 16);
   const DecodeCall c{q, k, v, lengths, partial_max, partial_sum, partial_out, out, batch, q_heads,
                      kv_heads, capacity, head_dim, splits, scale, static_cast<hipStream_t>(stream)};
   int rc;
@@ -436,6 +441,7 @@ extern "C" int sfl_decode_attention(const void* q, const void* k, const void* v,
     case SFL_DTYPE_F32: return merge_dims<float>(c);
     case SFL_DTYPE_BF16: return merge_dims<bf16_t>(c);
     case SFL_DTYPE_F16: return merge_dims<f16_t>(c);
+    case SFL_DTYPE_F32X: return merge_dims<f32x_t>(c);
     default: return merge_dims<split_t>(c);
   }
 }

@@ -1,14 +1,17 @@
 // Decode-step projections as MFMA GEMVs with fused prologues and epilogues.
 //
 // Every kernel computes out[b, n] = sum_k act[b, k] * W[n, k] for a batch of
-// at most 16 rows (one decode token per sequence), with W stored [N, K]
-// K-contiguous as the reference's Linear keeps it (src/llmlab/model/layers.py:34-35).
-// A workgroup owns 16 output features; its waves split K, stream their weight
-// slices straight from HBM into MFMA A-operand registers (16 bytes per lane)
-// and feed the activations as the B operand; partial tiles are summed across
-// waves in LDS. The MFMA result layout puts 4 consecutive features of one
-// batch row in each lane, so RoPE pairs, SwiGLU pairs and vector stores stay
-// in-lane.
+// at most 16 rows (one decode token per sequence). W is the reference's [N, K]
+// Linear weight (src/llmlab/model/layers.py:34-35) repacked once by
+// sfl_pack_gemv_weights into the load order of the kernel: for every tile of
+// 16 output rows and every K chunk, the 64 lanes' 16-byte A operands are
+// stored contiguously (1 KB), as are the activations (act_format.hpp). A
+// workgroup owns 16 output features; its waves split K, and every load
+// instruction reads whole contiguous cache lines. (Reading the [N, K] rows
+// directly touches 16 rows x 64 bytes per instruction and runs at about half
+// the speed.) Partial tiles are summed across waves in LDS. The MFMA result
+// layout puts 4 consecutive features of one batch row in each lane, so RoPE
+// pairs, SwiGLU pairs and vector stores stay in-lane.
 //
 // Precision: weights and the KV cache are in the model dtype; activations,
 // the residual stream and every epilogue stay in fp32. For bf16 weights each
@@ -51,8 +54,8 @@ constexpr float kEps = 1e-5f;
 struct LinearArgs {
   const void* act;       // [B, K] activation format (x * g for normalized consumers)
   const float* ss;       // [B, K/16] partial sums of x^2 (normalized consumers), else nullptr
-  const void* w;         // [N, K]
-  const void* w3;        // [N, K] second matrix of SWIGLU
+  const void* w;         // packed [ceil(N/16)][K/chunk][64 lanes][16 B]
+  const void* w3;        // packed second matrix of SWIGLU
   int batch, n, k;
   // QKV
   const float* cos_t;    // [ctx, dk/2] fp32
@@ -78,9 +81,6 @@ struct LinearArgs {
   int32_t* best_idx;
   int best_stride;
 };
-
-// One 16-byte weight chunk of K covers 4 lane groups of vec_elems<T>() values.
-template <typename T> constexpr int chunk_k() { return 4 * vec_elems<T>(); }
 
 template <typename T>
 __device__ __forceinline__ f32x4 mfma_chunk(const uint4& a, const u32x4& b, f32x4 acc);
@@ -135,7 +135,7 @@ __device__ __forceinline__ ActChunk<float> load_act<float>(const unsigned char* 
 }
 template <>
 __device__ __forceinline__ ActChunk<bf16_t> load_act<bf16_t>(const unsigned char* p) {
-  return {load16(p), load16(p + 16)};
+  return {load16(p), load16(p + kActLoOffset)};
 }
 
 template <typename T>
@@ -158,7 +158,6 @@ __device__ __forceinline__ f32x4 mfma_act<float>(const uint4& w, const ActChunk<
 template <typename T, int E, int CPW>
 __global__ __launch_bounds__(kWaves * kWave) void linear_kernel(LinearArgs a) {
   constexpr int kChunkGroup = CPW;
-  constexpr int EPL = vec_elems<T>();  // k values per lane per chunk
   constexpr int KC = chunk_k<T>();
   constexpr bool kTwo = (E == EPI_SWIGLU);
   __shared__ float red[kWaves * kWave * (kTwo ? 8 : 4)];
@@ -167,16 +166,17 @@ __global__ __launch_bounds__(kWaves * kWave) void linear_kernel(LinearArgs a) {
   const int lane = tid % kWave;
   const int K = a.k;
 
+  constexpr int CB = act_chunk_bytes<T>();
   const int n0 = blockIdx.x * kTileN;
-  const int row = min(n0 + lane % 16, a.n - 1);
   const int grp = lane / 16;
   const int b = lane % 16;
-  const T* wrow = static_cast<const T*>(a.w) + long(row) * K + grp * EPL;
-  const T* w3row = kTwo ? static_cast<const T*>(a.w3) + long(row) * K + grp * EPL : nullptr;
-  const unsigned char* arow = static_cast<const unsigned char*>(a.act) +
-                              (long(min(b, a.batch - 1)) * K + grp * EPL) * 4;
-  const bool live = b < a.batch;
   const int nchunks = K / KC;
+  // This lane's 16 bytes of chunk c: w + c*1KB, act + c*CB (packed layouts).
+  const unsigned char* wl = static_cast<const unsigned char*>(a.w) + (long(blockIdx.x) * nchunks * kWave + lane) * 16;
+  const unsigned char* w3l =
+      kTwo ? static_cast<const unsigned char*>(a.w3) + (long(blockIdx.x) * nchunks * kWave + lane) * 16 : nullptr;
+  const unsigned char* al = static_cast<const unsigned char*>(a.act) + lane * 16;
+  const bool live = b < a.batch;
 
   // Issue the first group of weight and activation loads up front. Loads are
   // unconditional, from clamped addresses, and masked where they are used: a
@@ -189,9 +189,9 @@ __global__ __launch_bounds__(kWaves * kWave) void linear_kernel(LinearArgs a) {
 #pragma unroll
   for (int j = 0; j < kChunkGroup; ++j) {
     const long c = min(c0 + j * kWaves, last);
-    wa[j] = load16(wrow + c * KC);
-    if constexpr (kTwo) wb[j] = load16(w3row + c * KC);
-    af[j] = load_act<T>(arow + c * KC * 4);
+    wa[j] = load16(wl + c * kWave * 16);
+    if constexpr (kTwo) wb[j] = load16(w3l + c * kWave * 16);
+    af[j] = load_act<T>(al + c * CB);
   }
 
   // Prefetch what wave 0's epilogue reads, so it overlaps the weight loads.
@@ -241,9 +241,9 @@ __global__ __launch_bounds__(kWaves * kWave) void linear_kernel(LinearArgs a) {
 #pragma unroll
     for (int j = 0; j < kChunkGroup; ++j) {
       const long c = min(c0 + j * kWaves, last);
-      wa[j] = load16(wrow + c * KC);
-      if constexpr (kTwo) wb[j] = load16(w3row + c * KC);
-      af[j] = load_act<T>(arow + c * KC * 4);
+      wa[j] = load16(wl + c * kWave * 16);
+      if constexpr (kTwo) wb[j] = load16(w3l + c * kWave * 16);
+      af[j] = load_act<T>(al + c * CB);
     }
   }
 
@@ -315,7 +315,7 @@ __global__ __launch_bounds__(kWaves * kWave) void linear_kernel(LinearArgs a) {
       sq += __shfl_xor(sq, 32, kWave);
       if (live && n < a.n) {
         const float gx[4] = {xo[0] * pre_g.x, xo[1] * pre_g.y, xo[2] * pre_g.z, xo[3] * pre_g.w};
-        store_act4<T>(static_cast<unsigned char*>(a.act_next) + size_t(b) * a.n * 4, n, gx);
+        store_act4<T>(static_cast<unsigned char*>(a.act_next), b, n, a.n, gx);
         if (grp == 0) a.ss_next[long(b) * (a.n / 16) + blockIdx.x] = sq;
       }
     }
@@ -328,7 +328,7 @@ __global__ __launch_bounds__(kWaves * kWave) void linear_kernel(LinearArgs a) {
     float h[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) h[i] = v1[i] / (1.f + expf(-v1[i])) * v3[i];
-    store_act4<T>(static_cast<unsigned char*>(a.h_out) + size_t(b) * a.n * 4, n, h);
+    store_act4<T>(static_cast<unsigned char*>(a.h_out), b, n, a.n, h);
   } else {  // EPI_QKV
     const int section = n / a.d_model;  // 0 q, 1 k, 2 v
     const int f = n % a.d_model;
@@ -401,6 +401,25 @@ int dispatch_linear(const LinearArgs& a, int dtype, hipStream_t s, const char* w
   return launch_linear<float, E>(a, s, what);
 }
 
+// Packed GEMV weights: 16-byte unit u = (tile * nchunks + c) * 64 + lane holds
+// row tile*16 + lane%16, k values [c*KC + (lane/16)*EPL, +EPL) (zeros past N).
+template <typename T>
+__global__ __launch_bounds__(256) void pack_weights_kernel(const T* __restrict__ w, uint4* __restrict__ packed,
+                                                           int n, int k) {
+  constexpr int KC = chunk_k<T>(), EPL = vec_elems<T>();
+  const int nchunks = k / KC;
+  const long units = long((n + kTileN - 1) / kTileN) * nchunks * kWave;
+  for (long u = long(blockIdx.x) * 256 + threadIdx.x; u < units; u += long(gridDim.x) * 256) {
+    const int lane = int(u % kWave);
+    const long tc = u / kWave;
+    const int c = int(tc % nchunks);
+    const int row = int(tc / nchunks) * kTileN + lane % 16;
+    uint4 v = make_uint4(0u, 0u, 0u, 0u);
+    if (row < n) v = load16(w + long(row) * k + c * KC + (lane / 16) * EPL);
+    packed[u] = v;
+  }
+}
+
 // act = x * g and the per-tile sums of x^2 for a normalized consumer, from x.
 template <typename T>
 __global__ __launch_bounds__(64) void norm_act_kernel(const float* x, const T* gain, unsigned char* act,
@@ -414,7 +433,7 @@ __global__ __launch_bounds__(64) void norm_act_kernel(const float* x, const T* g
       const float4 q = *reinterpret_cast<const float4*>(xr + 16 * t + i);
       v[i] = q.x; v[i + 1] = q.y; v[i + 2] = q.z; v[i + 3] = q.w;
     }
-    emit_tile<T>(v, gain, t, nullptr, act + size_t(b) * d * 4, ss + long(b) * (d / 16));
+    emit_tile<T>(v, gain, t, nullptr, act, b, d, ss + long(b) * (d / 16));
   }
 }
 
@@ -509,3 +528,27 @@ extern "C" int sfl_norm_act(const float* x, const void* gain, void* act, float* 
 }
 
 extern "C" int sfl_lm_head_tiles(int vocab) { return (vocab + kTileN - 1) / kTileN; }
+
+extern "C" long sfl_packed_gemv_elems(int n, int k) { return long((n + kTileN - 1) / kTileN) * kTileN * k; }
+
+extern "C" int sfl_pack_gemv_weights(const void* w, void* packed, int n, int k, int dtype, void* stream) {
+  const char* what = "pack_gemv_weights";
+  if (!w || !packed) return set_error(SFL_ERR_INVALID, "%s: null pointer argument", what);
+  if (n < 1 || k < 1) return set_error(SFL_ERR_INVALID, "%s: sizes must be positive", what);
+  if (dtype != SFL_DTYPE_F32 && dtype != SFL_DTYPE_BF16)
+    return set_error(SFL_ERR_UNSUPPORTED, "%s: dtype must be F32 or BF16", what);
+  const int kc = dtype == SFL_DTYPE_BF16 ? chunk_k<bf16_t>() : chunk_k<float>();
+  if (k % kc) return set_error(SFL_ERR_UNSUPPORTED, "%s: K=%d must be a multiple of %d", what, k, kc);
+  if (reinterpret_cast<uintptr_t>(w) % 16 || reinterpret_cast<uintptr_t>(packed) % 16)
+    return set_error(SFL_ERR_INVALID, "%s: pointers must be 16-byte aligned", what);
+  const long units = sfl_packed_gemv_elems(n, k) / (16 / (dtype == SFL_DTYPE_BF16 ? 2 : 4));
+  const unsigned blocks = unsigned(std::min<long>((units + 255) / 256, 4096));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == SFL_DTYPE_BF16)
+    hipLaunchKernelGGL(pack_weights_kernel<bf16_t>, dim3(blocks), dim3(256), 0, s, static_cast<const bf16_t*>(w),
+                       static_cast<uint4*>(packed), n, k);
+  else
+    hipLaunchKernelGGL(pack_weights_kernel<float>, dim3(blocks), dim3(256), 0, s, static_cast<const float*>(w),
+                       static_cast<uint4*>(packed), n, k);
+  return check_launch(what);
+}

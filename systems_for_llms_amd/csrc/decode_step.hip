@@ -80,7 +80,7 @@ __global__ __launch_bounds__(64) void next_token_kernel(
     float v[16];
 #pragma unroll
     for (int j = 0; j < 16 / V; ++j) unpack16<T>(r[j], v + j * V);
-    emit_tile<T>(v, gain0, t, x + long(b) * d, act + size_t(b) * d * 4, ss + long(b) * (d / 16));
+    emit_tile<T>(v, gain0, t, x + long(b) * d, act, b, d, ss + long(b) * (d / 16));
   }
   if (lane == 0) {
     predicted[b * stride + np] = bi;

@@ -63,6 +63,15 @@ class DecodeSession:
         self.cos, self.sin = cos.to(dev), sin.to(dev)
         self.wqkv = [torch.cat([blk.attn.q_proj.weight, blk.attn.k_proj.weight, blk.attn.v_proj.weight])
                      .contiguous() for blk in model.layers]
+        # Decode-GEMV copies of the weights in the packed tile layout (one contiguous
+        # 1 KB block per 16 rows x K chunk); the prefill GEMMs read the [N, K] originals.
+        pk = _lib.pack_gemv
+        self.p_qkv = [pk(w) for w in self.wqkv]
+        self.p_out = [pk(blk.attn.output_proj.weight) for blk in model.layers]
+        self.p_w1 = [pk(blk.ffn.w1.weight) for blk in model.layers]
+        self.p_w3 = [pk(blk.ffn.w3.weight) for blk in model.layers]
+        self.p_w2 = [pk(blk.ffn.w2.weight) for blk in model.layers]
+        self.p_head = pk(model.lm_head.weight)
         self.k_cache = torch.zeros((n, batch, h, cap, self.dk), device=dev, dtype=dt)
         self.v_cache = torch.zeros_like(self.k_cache)
         self.x = torch.zeros((batch, d), device=dev, dtype=torch.float32)
@@ -70,13 +79,16 @@ class DecodeSession:
         # GEMV inputs (attention output, SwiGLU hidden) are 4 bytes per value:
         # fp32 for fp32 models, the split-bf16 (hi, lo) format for bf16 models.
         self.q = torch.zeros((batch, h, self.dk), device=dev, dtype=torch.float32)
-        self.attn = torch.zeros((batch, h, self.dk), device=dev, dtype=torch.float32)
-        self.hidden = torch.zeros((batch, f), device=dev, dtype=torch.float32)
-        # Normalized input of the next RMSNorm consumer: x * g (activation format) and
-        # the sums of x^2 over each 16-feature tile.
-        self.act = torch.zeros((batch, d), device=dev, dtype=torch.float32)
+        # GEMV inputs in the activation layout: whole blocks of 16 rows, 4 bytes per
+        # value (viewed here as fp32 words): the attention output, the SwiGLU hidden
+        # state, and x * g for the next RMSNorm consumer with the sums of x^2 over
+        # each 16-feature tile (ss).
+        blocks = -(-batch // ROWS_PER_LAUNCH)
+        self.attn = torch.zeros((blocks, ROWS_PER_LAUNCH * d), device=dev, dtype=torch.float32)
+        self.hidden = torch.zeros((blocks, ROWS_PER_LAUNCH * f), device=dev, dtype=torch.float32)
+        self.act = torch.zeros((blocks, ROWS_PER_LAUNCH * d), device=dev, dtype=torch.float32)
         self.ss = torch.zeros((batch, d // 16), device=dev, dtype=torch.float32)
-        self.act_code = _lib.DTYPE_BF16X2 if dt == torch.bfloat16 else _lib.DTYPE_CODES[torch.float32]
+        self.act_code = _lib.DTYPE_BF16X2 if dt == torch.bfloat16 else _lib.DTYPE_F32X
         self.splits = splits or auto_splits(batch, h, cap)
         self.pmax = torch.empty((batch, h, self.splits), device=dev, dtype=torch.float32)
         self.psum = torch.empty_like(self.pmax)
@@ -109,7 +121,7 @@ class DecodeSession:
             kc, vc = self.k_cache[layer], self.v_cache[layer]
             for r, rows in row_chunks:
                 calls.append((lib.sfl_rmsnorm_qkv_rope_append, (
-                    self.act[r].data_ptr(), self.ss[r].data_ptr(), self.wqkv[layer].data_ptr(),
+                    self.act[r // ROWS_PER_LAUNCH].data_ptr(), self.ss[r].data_ptr(), self.p_qkv[layer].data_ptr(),
                     self.cos.data_ptr(), self.sin.data_ptr(), self.pos[r:].data_ptr(),
                     self.q[r].data_ptr(), kc[r].data_ptr(), vc[r].data_ptr(), rows, d, h, cap, code)))
             calls.append((lib.sfl_decode_attention, (
@@ -118,20 +130,21 @@ class DecodeSession:
                 self.batch, h, h, cap, dk, self.splits, scale, code, _lib.DTYPE_CODES[torch.float32],
                 self.act_code)))
             for r, rows in row_chunks:
-                x, act, ss = self.x[r].data_ptr(), self.act[r].data_ptr(), self.ss[r].data_ptr()
+                j = r // ROWS_PER_LAUNCH
+                x, act, ss = self.x[r].data_ptr(), self.act[j].data_ptr(), self.ss[r].data_ptr()
                 calls.append((lib.sfl_linear_residual, (
-                    self.attn[r].data_ptr(), blk.attn.output_proj.weight.data_ptr(), x, x,
+                    self.attn[j].data_ptr(), self.p_out[layer].data_ptr(), x, x,
                     blk.ffn_norm.weight.data_ptr(), act, ss, rows, d, d, code)))
                 calls.append((lib.sfl_rmsnorm_swiglu, (
-                    act, ss, blk.ffn.w1.weight.data_ptr(), blk.ffn.w3.weight.data_ptr(),
-                    self.hidden[r].data_ptr(), rows, d, f, code)))
+                    act, ss, self.p_w1[layer].data_ptr(), self.p_w3[layer].data_ptr(),
+                    self.hidden[j].data_ptr(), rows, d, f, code)))
                 calls.append((lib.sfl_linear_residual, (
-                    self.hidden[r].data_ptr(), blk.ffn.w2.weight.data_ptr(), x, x,
+                    self.hidden[j].data_ptr(), self.p_w2[layer].data_ptr(), x, x,
                     gains[layer].data_ptr(), act, ss, rows, d, f, code)))
         for r, rows in row_chunks:
             logits = self.logits[r].data_ptr() if self.logits is not None else None
             calls.append((lib.sfl_rmsnorm_lm_head, (
-                self.act[r].data_ptr(), self.ss[r].data_ptr(), m.lm_head.weight.data_ptr(),
+                self.act[r // ROWS_PER_LAUNCH].data_ptr(), self.ss[r].data_ptr(), self.p_head.data_ptr(),
                 logits, cap * v, self.pos[r:].data_ptr(), v, self.best_val[:, r:].data_ptr(),
                 self.best_idx[:, r:].data_ptr(), self.batch, rows, d, v, code)))
         calls.append((lib.sfl_next_token, (
