@@ -54,6 +54,7 @@ constexpr float kEps = 1e-5f;
 struct LinearArgs {
   const void* act;       // [B, K] activation format (x * g for normalized consumers)
   const float* ss;       // [B, K/16] partial sums of x^2 (normalized consumers), else nullptr
+  int ss_vec4;           // ss rows load as float4 (K % 256 == 0, 16-byte aligned)
   const void* w;         // packed [ceil(N/16)][K/chunk][64 lanes][16 B]
   const void* w3;        // packed second matrix of SWIGLU
   int batch, n, k;
@@ -206,12 +207,22 @@ __global__ __launch_bounds__(kWaves * kWave) void linear_kernel(LinearArgs a) {
     if (a.ss) {
       const float* sr = a.ss + long(min(b, a.batch - 1)) * ntiles;
       const int per = ntiles / 4;  // tiles summed by each of the 4 lanes of row b
-      float part[kMaxSsTiles / 4];
+      if (a.ss_vec4) {  // per % 4 == 0 and 16-byte aligned rows: float4 loads
+        const float4* s4 = reinterpret_cast<const float4*>(sr + grp * per);
+        float4 part[kMaxSsTiles / 16];
 #pragma unroll
-      for (int t = 0; t < kMaxSsTiles / 4; ++t) part[t] = sr[grp * per + min(t, per - 1)];
+        for (int t = 0; t < kMaxSsTiles / 16; ++t) part[t] = s4[min(t, per / 4 - 1)];
 #pragma unroll
-      for (int t = 0; t < kMaxSsTiles / 4; ++t)
-        if (t < per) ssum += part[t];
+        for (int t = 0; t < kMaxSsTiles / 16; ++t)
+          if (t < per / 4) ssum += (part[t].x + part[t].y) + (part[t].z + part[t].w);
+      } else {
+        float part[kMaxSsTiles / 4];
+#pragma unroll
+        for (int t = 0; t < kMaxSsTiles / 4; ++t) part[t] = sr[grp * per + min(t, per - 1)];
+#pragma unroll
+        for (int t = 0; t < kMaxSsTiles / 4; ++t)
+          if (t < per) ssum += part[t];
+      }
     }
     if constexpr (E == EPI_RESIDUAL) {
       pre_x = *reinterpret_cast<const float4*>(a.x + long(min(b, a.batch - 1)) * a.n + nl);
@@ -396,7 +407,8 @@ int check_normed(const char* what, int k) {
 }
 
 template <int E>
-int dispatch_linear(const LinearArgs& a, int dtype, hipStream_t s, const char* what) {
+int dispatch_linear(LinearArgs a, int dtype, hipStream_t s, const char* what) {
+  a.ss_vec4 = a.ss && a.k % 256 == 0 && reinterpret_cast<uintptr_t>(a.ss) % 16 == 0;
   if (dtype == SFL_DTYPE_BF16) return launch_linear<bf16_t, E>(a, s, what);
   return launch_linear<float, E>(a, s, what);
 }
