@@ -54,6 +54,12 @@ __device__ __forceinline__ f32x4 mfma_bf16(const u32x4& a, const u32x4& b, f32x4
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
 }
 
+// v, or zeros when !keep. Selected per component: a select of whole uint4
+// structs is lowered through scratch memory.
+__device__ __forceinline__ uint4 keep16(const uint4& v, bool keep) {
+  return make_uint4(keep ? v.x : 0u, keep ? v.y : 0u, keep ? v.z : 0u, keep ? v.w : 0u);
+}
+
 __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
   return uint32_t(f32_to_bf16_bits(lo)) | (uint32_t(f32_to_bf16_bits(hi)) << 16);
 }
@@ -75,28 +81,23 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
   // zeroed when the registers go to LDS, so no load waits inside its guard.
   uint4 wr[4], ar[4];
   bool kin[4];
-  auto gload = [&](int kt) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int idx = tid + i * kThreads;  // 0 .. 1023
-      const int r = idx / (TK / 8), cg = idx % (TK / 8);
-      const int kk = kt * TK + cg * 8;
-      kin[i] = kk < g.k;
-      const int kc = kin[i] ? kk : 0;
-      wr[i] = load16(g.w + long(min(n0 + r, g.n - 1)) * g.k + kc);
-      ar[i] = load16(g.a + long(min(m0 + r, g.m - 1)) * g.k + kc);
-    }
-  };
-  auto sstore = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int idx = tid + i * kThreads;
-      const int r = idx / (TK / 8), cg = idx % (TK / 8);
-      const uint4 z = make_uint4(0, 0, 0, 0);
-      *reinterpret_cast<uint4*>(&ws[buf][r * LDT + cg * 8]) = kin[i] ? wr[i] : z;
-      *reinterpret_cast<uint4*>(&as[buf][r * LDT + cg * 8]) = kin[i] ? ar[i] : z;
-    }
-  };
+#define SFL_GEMM_GLOAD(kt)                                                   \
+  _Pragma("unroll") for (int i = 0; i < 4; ++i) {                            \
+    const int idx = tid + i * kThreads;                                      \
+    const int r = idx / (TK / 8), cg = idx % (TK / 8);                       \
+    const int kk = (kt) * TK + cg * 8;                                       \
+    kin[i] = kk < g.k;                                                       \
+    const int kc = kin[i] ? kk : 0;                                          \
+    wr[i] = load16(g.w + long(min(n0 + r, g.n - 1)) * g.k + kc);             \
+    ar[i] = load16(g.a + long(min(m0 + r, g.m - 1)) * g.k + kc);             \
+  }
+#define SFL_GEMM_SSTORE(buf)                                                 \
+  _Pragma("unroll") for (int i = 0; i < 4; ++i) {                            \
+    const int idx = tid + i * kThreads;                                      \
+    const int r = idx / (TK / 8), cg = idx % (TK / 8);                       \
+    *reinterpret_cast<uint4*>(&ws[buf][r * LDT + cg * 8]) = keep16(wr[i], kin[i]); \
+    *reinterpret_cast<uint4*>(&as[buf][r * LDT + cg * 8]) = keep16(ar[i], kin[i]); \
+  }
 
   f32x4 acc[4][4];
 #pragma unroll
@@ -104,12 +105,12 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  gload(0);
-  sstore(0);
+  SFL_GEMM_GLOAD(0)
+  SFL_GEMM_SSTORE(0)
   __syncthreads();
   for (int kt = 0; kt < ksteps; ++kt) {
     const int buf = kt & 1;
-    if (kt + 1 < ksteps) gload(kt + 1);
+    if (kt + 1 < ksteps) { SFL_GEMM_GLOAD(kt + 1) }
 #pragma unroll
     for (int ks = 0; ks < TK / 32; ++ks) {
       u32x4 af[4], bfr[4];
@@ -125,10 +126,12 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
         for (int j = 0; j < 4; ++j) acc[i][j] = mfma_bf16(af[i], bfr[j], acc[i][j]);
     }
     if (kt + 1 < ksteps) {
-      sstore(buf ^ 1);
+      SFL_GEMM_SSTORE(buf ^ 1)
       __syncthreads();
     }
   }
+#undef SFL_GEMM_GLOAD
+#undef SFL_GEMM_SSTORE
 
   // Epilogue: acc[i][j] holds features n0 + wn*64 + 16i + 4grp + (0..3) of token m0 + wm*64 + 16j + col.
 #pragma unroll
