@@ -44,6 +44,18 @@ __device__ __forceinline__ f32x4 mfma16<f16_t>(const u32x4& a, const u32x4& b, f
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
 }
 
+// Two values rounded to T and packed (v_cvt_pk_bf16_f32 / v_cvt_pk_f16_f32).
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+template <typename T> __device__ __forceinline__ uint32_t pack2(float lo, float hi);
+template <> __device__ __forceinline__ uint32_t pack2<bf16_t>(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t{lo, hi}), bf16x2_t));
+}
+template <> __device__ __forceinline__ uint32_t pack2<f16_t>(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t{lo, hi}), f16x2_t));
+}
+
 template <typename T> __device__ __forceinline__ uint16_t to_bits(float v);
 template <> __device__ __forceinline__ uint16_t to_bits<bf16_t>(float v) { return f32_to_bf16_bits(v); }
 template <> __device__ __forceinline__ uint16_t to_bits<f16_t>(float v) { return f32_to_f16_bits(v); }
@@ -82,6 +94,17 @@ __device__ __forceinline__ bool allowed(const MaskArgs& m, int q, int k, int n) 
   if (m.left >= 0 && q - k > m.left) return false;
   if (m.right >= 0 && k - q > m.right) return false;
   return true;
+}
+
+// allowed() without short-circuit branches, with the document labels of q and
+// k already loaded (ignored when m.docs is null).
+__device__ __forceinline__ bool allowed_flat(const MaskArgs& m, int q, int k, int n, int64_t dq, int64_t dk) {
+  const bool in = (k < n) & (q < n);
+  const bool causal_ok = !m.causal | (k <= q);
+  const bool doc_ok = !m.docs | (dq == dk);
+  const bool left_ok = (m.left < 0) | (q - k <= m.left);
+  const bool right_ok = (m.right < 0) | (k - q <= m.right);
+  return in & causal_ok & doc_ok & ((k < m.prefix) | (left_ok & right_ok));
 }
 
 // Tile geometry of one query tile, as masks.py/_tile_geometry derives it.
@@ -284,12 +307,258 @@ __global__ __launch_bounds__(kThreads) void masked_attention_kernel(AttnArgs a) 
   }
 }
 
+// Head dim 64: one wave per 64-query tile (its CSR row or interval bounds), 4
+// independent waves per workgroup, no workgroup barrier. The wave computes
+// all 64 queries of its tile (4 MFMA column tiles), so every K/V byte feeds 4x
+// the MFMAs of the 16-queries-per-wave kernel above. K goes from global memory
+// straight into MFMA A operands; V rows go to registers and are written
+// transposed into the wave's own LDS buffer. The next tile's K/V loads are
+// issued before the current tile's math.
+constexpr int kWaveTiles = 4;  // query tiles (waves) per workgroup
+
+template <typename T>
+__global__ __launch_bounds__(kWaveTiles * kWave) void masked_attention_wave_kernel(AttnArgs a) {
+  constexpr int D = 64, KSTEPS = D / 32, DT = D / 16, QS = BQ / 16;
+  constexpr int LDV = BK + kPadK;
+  __shared__ __align__(16) uint16_t vt_all[kWaveTiles][D * LDV];
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int col = lane % 16, grp = lane / 16;
+  const int n = a.n;
+  const int qt = blockIdx.x * kWaveTiles + wave;
+  if (qt * BQ >= n) return;  // waves are independent: no barrier below
+  uint16_t* vt_s = vt_all[wave];
+  const int bh = blockIdx.y;
+  const int b = bh / a.heads, h = bh % a.heads;
+  const int q0 = qt * BQ;
+  const int q1 = min(q0 + BQ, n) - 1;
+
+  const uint16_t* qp = static_cast<const uint16_t*>(a.q) + b * a.qs[0] + h * a.qs[1];
+  const uint16_t* kp = static_cast<const uint16_t*>(a.k) + b * a.ks[0] + h * a.ks[1];
+  const uint16_t* vp = static_cast<const uint16_t*>(a.v) + b * a.vs[0] + h * a.vs[1];
+
+  // Q^T operands: subtile qs, lane holds Q[q0 + 16qs + col][32ks + 8grp .. +8].
+  u32x4 qreg[QS][KSTEPS];
+#pragma unroll
+  for (int qs = 0; qs < QS; ++qs) {
+    const uint16_t* qr = qp + long(min(q0 + 16 * qs + col, n - 1)) * a.qs[2];
+#pragma unroll
+    for (int ks = 0; ks < KSTEPS; ++ks) {
+      const uint4 r = load16(qr + 32 * ks + 8 * grp);
+      qreg[qs][ks] = u32x4{r.x, r.y, r.z, r.w};
+    }
+  }
+
+  float m_run[QS], l_run[QS];
+  f32x4 oacc[QS][DT];
+#pragma unroll
+  for (int qs = 0; qs < QS; ++qs) {
+    m_run[qs] = -INFINITY;
+    l_run[qs] = 0.f;
+#pragma unroll
+    for (int t = 0; t < DT; ++t) oacc[qs][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  const TileBounds tb = tile_bounds(a.m, n, q0, q1);
+  int count, base = 0;
+  if (a.s.mode == 1) {
+    base = a.s.row_ptr[qt];
+    count = a.s.row_ptr[qt + 1] - base;
+  } else {
+    const int lowg = min(tb.gend, tb.begin);
+    count = lowg + max(0, max(tb.end, tb.gend) - tb.begin);
+  }
+  const int lowg = min(tb.gend, tb.begin);
+
+  // K operands of key subtile j (keys 16j + col) and V rows 4*col + u of
+  // dims 8grp + 32hh .. +8, for the tile at key block kb.
+  u32x4 kreg[4][KSTEPS];
+  uint4 vreg[2][4];
+#define SFL_LOAD_TILE(kb)                                                                   \
+  {                                                                                         \
+    const int k0_ = (kb) * BK;                                                              \
+    _Pragma("unroll") for (int j = 0; j < 4; ++j) {                                         \
+      const uint16_t* kr_ = kp + long(min(k0_ + 16 * j + col, n - 1)) * a.ks[2];            \
+      _Pragma("unroll") for (int ks = 0; ks < KSTEPS; ++ks) {                               \
+        const uint4 r_ = load16(kr_ + 32 * ks + 8 * grp);                                   \
+        kreg[j][ks] = u32x4{r_.x, r_.y, r_.z, r_.w};                                        \
+      }                                                                                     \
+    }                                                                                       \
+    _Pragma("unroll") for (int hh = 0; hh < 2; ++hh)                                        \
+      _Pragma("unroll") for (int u = 0; u < 4; ++u)                                         \
+        vreg[hh][u] = load16(vp + long(min(k0_ + 4 * col + u, n - 1)) * a.vs[2] + 8 * grp + 32 * hh); \
+  }
+#define SFL_TILE_AT(it, kb_, fl_)                                                           \
+  if (a.s.mode == 1) {                                                                      \
+    kb_ = a.s.col_idx[base + (it)];                                                         \
+    fl_ = a.s.full[base + (it)] != 0;                                                       \
+  } else {                                                                                  \
+    kb_ = (it) < lowg ? (it) : tb.begin + ((it) - lowg);                                    \
+    fl_ = !a.m.docs && covered(tb, kb_ * BK, min(kb_ * BK + BK, n) - 1);                    \
+  }
+
+  if (count > 0) {
+    int kb0;
+    bool f0;
+    SFL_TILE_AT(0, kb0, f0)
+    (void)f0;
+    SFL_LOAD_TILE(kb0)
+  }
+  for (int it = 0; it < count; ++it) {
+    int kb;
+    bool full;
+    SFL_TILE_AT(it, kb, full)
+    full = full && a.s.use_full;
+    const int k0 = kb * BK;
+
+    // V^T into this wave's LDS buffer: dim 8grp + 32hh + e, keys 4col .. 4col+3.
+    // (The previous tile's reads of the buffer precede these writes in the
+    // wave's in-order LDS queue; the fences keep the compiler from moving them.)
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      const uint32_t w0[4] = {vreg[hh][0].x, vreg[hh][0].y, vreg[hh][0].z, vreg[hh][0].w};
+      const uint32_t w1[4] = {vreg[hh][1].x, vreg[hh][1].y, vreg[hh][1].z, vreg[hh][1].w};
+      const uint32_t w2[4] = {vreg[hh][2].x, vreg[hh][2].y, vreg[hh][2].z, vreg[hh][2].w};
+      const uint32_t w3[4] = {vreg[hh][3].x, vreg[hh][3].y, vreg[hh][3].z, vreg[hh][3].w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int sh = (e & 1) * 16;
+        const uint32_t k01 = ((w0[e / 2] >> sh) & 0xffffu) | (((w1[e / 2] >> sh) & 0xffffu) << 16);
+        const uint32_t k23 = ((w2[e / 2] >> sh) & 0xffffu) | (((w3[e / 2] >> sh) & 0xffffu) << 16);
+        *reinterpret_cast<uint2*>(vt_s + (8 * grp + 32 * hh + e) * LDV + 4 * col) = make_uint2(k01, k23);
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    u32x4 kcur[4][KSTEPS];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int ks = 0; ks < KSTEPS; ++ks) kcur[j][ks] = kreg[j][ks];
+    if (it + 1 < count) {
+      int kbn;
+      bool fn;
+      SFL_TILE_AT(it + 1, kbn, fn)
+      (void)fn;
+      SFL_LOAD_TILE(kbn)
+    }
+
+    // V^T operands (shared by the 4 query subtiles): element e of step s2 is
+    // key 16*(2s2 + e/4) + 4grp + e%4 of dim 16t + col.
+    u32x4 vop[2][DT];
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+      for (int t = 0; t < DT; ++t) {
+        const uint16_t* vrow = vt_s + (16 * t + col) * LDV;
+        const uint2 a0 = *reinterpret_cast<const uint2*>(vrow + 16 * (2 * s2) + 4 * grp);
+        const uint2 a1 = *reinterpret_cast<const uint2*>(vrow + 16 * (2 * s2 + 1) + 4 * grp);
+        vop[s2][t] = u32x4{a0.x, a0.y, a1.x, a1.y};
+      }
+    const bool fast = full && k0 + BK <= n;
+    int64_t dkey[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e)
+      dkey[e] = (!fast && a.m.docs) ? a.m.docs[min(k0 + 16 * (e / 4) + 4 * grp + e % 4, n - 1)] : 0;
+
+#pragma unroll
+    for (int qs = 0; qs < QS; ++qs) {
+      const int qrow = q0 + 16 * qs + col;
+      // S^T = K Q^T: lane holds keys 16j + 4grp + i of query qrow.
+      f32x4 sacc[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        sacc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < KSTEPS; ++ks) sacc[j] = mfma16<T>(kcur[j][ks], qreg[qs][ks], sacc[j]);
+      }
+      // Full tiles need no mask (rows past n are never stored); the branch is
+      // uniform. Other tiles evaluate the mask arithmetically per score.
+      // Scores stay unscaled: scale > 0 commutes with the max, and the scale
+      // is folded into the exponent, p = 2^(s*c - m) with one FMA.
+      float sv[16];
+      if (fast) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) sv[e] = sacc[e / 4][e % 4];
+      } else {
+        const int64_t dq = a.m.docs ? a.m.docs[min(qrow, n - 1)] : 0;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int key = k0 + 16 * (e / 4) + 4 * grp + e % 4;
+          const bool ok = full ? (key < n) & (qrow < n) : allowed_flat(a.m, qrow, key, n, dq, dkey[e]);
+          sv[e] = ok ? sacc[e / 4][e % 4] : -INFINITY;
+        }
+      }
+      float mx = fmaxf(fmaxf(sv[0], sv[1]), sv[2]);
+#pragma unroll
+      for (int e = 3; e < 15; e += 2) mx = fmaxf(fmaxf(mx, sv[e]), sv[e + 1]);
+      mx = fmaxf(mx, sv[15]);
+      mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+      const float c = a.scale_log2;
+      const float m_new = fmaxf(m_run[qs], mx * c);
+      const float ms = m_new == -INFINITY ? 0.f : m_new;
+      const float alpha = __builtin_amdgcn_exp2f(m_run[qs] - ms);
+      float psum = 0.f;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        sv[e] = __builtin_amdgcn_exp2f(fmaf(sv[e], c, -ms));
+        psum += sv[e];
+      }
+      psum += __shfl_xor(psum, 16, kWave);
+      psum += __shfl_xor(psum, 32, kWave);
+      l_run[qs] = l_run[qs] * alpha + psum;
+      m_run[qs] = m_new;
+      if (__ballot(alpha != 1.f)) {  // wave-uniform: skip the rescale once the maxima settle
+#pragma unroll
+        for (int t = 0; t < DT; ++t) oacc[qs][t] *= alpha;
+      }
+
+      // O^T += V^T P^T with the key order of the 16-queries kernel above.
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2) {
+        uint32_t pb[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          pb[e] = pack2<T>(sv[4 * (2 * s2 + e / 2) + (2 * e) % 4], sv[4 * (2 * s2 + e / 2) + (2 * e) % 4 + 1]);
+        const u32x4 pop = {pb[0], pb[1], pb[2], pb[3]};
+#pragma unroll
+        for (int t = 0; t < DT; ++t) oacc[qs][t] = mfma16<T>(vop[s2][t], pop, oacc[qs][t]);
+      }
+    }
+  }
+#undef SFL_LOAD_TILE
+#undef SFL_TILE_AT
+
+#pragma unroll
+  for (int qs = 0; qs < QS; ++qs) {
+    const int qrow = q0 + 16 * qs + col;
+    if (qrow >= n) continue;
+    const float inv = l_run[qs] > 0.f ? 1.f / l_run[qs] : 0.f;
+    uint16_t* op = static_cast<uint16_t*>(a.o) + b * a.os[0] + h * a.os[1] + long(qrow) * a.os[2];
+#pragma unroll
+    for (int t = 0; t < DT; ++t)
+      *reinterpret_cast<uint2*>(op + 16 * t + 4 * grp) =
+          make_uint2(pack2<T>(oacc[qs][t][0] * inv, oacc[qs][t][1] * inv),
+                     pack2<T>(oacc[qs][t][2] * inv, oacc[qs][t][3] * inv));
+    if (a.lse && grp == 0) {
+      const float lse = l_run[qs] > 0.f ? (m_run[qs] + log2f(l_run[qs])) * 0.6931471805599453f : -INFINITY;
+      a.lse[(long(b) * a.heads + h) * n + qrow] = lse;
+    }
+  }
+}
+
 template <typename T>
 int launch_masked(const AttnArgs& a, int batch, int dim, hipStream_t stream) {
   dim3 grid((a.n + BQ - 1) / BQ, batch * a.heads);
   switch (dim) {
     case 32: hipLaunchKernelGGL((masked_attention_kernel<T, 32>), grid, dim3(kThreads), 0, stream, a); break;
-    case 64: hipLaunchKernelGGL((masked_attention_kernel<T, 64>), grid, dim3(kThreads), 0, stream, a); break;
+    case 64: {
+      const int tiles = (a.n + BQ - 1) / BQ;
+      dim3 wgrid((tiles + kWaveTiles - 1) / kWaveTiles, batch * a.heads);
+      hipLaunchKernelGGL((masked_attention_wave_kernel<T>), wgrid, dim3(kWaveTiles * kWave), 0, stream, a);
+      break;
+    }
     case 128: hipLaunchKernelGGL((masked_attention_kernel<T, 128>), grid, dim3(kThreads), 0, stream, a); break;
     default: return set_error(SFL_ERR_UNSUPPORTED, "masked_attention: head dim must be 32, 64 or 128");
   }
