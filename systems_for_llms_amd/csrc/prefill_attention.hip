@@ -307,40 +307,130 @@ __global__ __launch_bounds__(kThreads) void masked_attention_kernel(AttnArgs a) 
   }
 }
 
-// Head dim 64: one wave per 64-query tile (its CSR row or interval bounds), 4
-// independent waves per workgroup, no workgroup barrier. The wave computes
-// all 64 queries of its tile (4 MFMA column tiles), so every K/V byte feeds 4x
-// the MFMAs of the 16-queries-per-wave kernel above. K goes from global memory
-// straight into MFMA A operands; V rows go to registers and are written
-// transposed into the wave's own LDS buffer. The next tile's K/V loads are
-// issued before the current tile's math.
-constexpr int kWaveTiles = 4;  // query tiles (waves) per workgroup
+// Head dim 64: one workgroup of 2 waves per 64-query tile (its CSR row or
+// interval bounds); each wave computes 32 queries (2 MFMA column tiles), so
+// the K/V bytes of a tile feed 2x the MFMAs of the 16-queries-per-wave kernel
+// above while the registers stay within 256 per lane (2 waves per SIMD, no
+// accumulator moves). Each wave reads K straight from global memory into its
+// MFMA A operands; the pair loads V together and writes it transposed into a
+// double-buffered LDS tile, one barrier per key tile. The next tile's K/V
+// loads are issued before the current tile's math. The softmax keeps the
+// scores unscaled (scale > 0 commutes with the max) and folds the scale into
+// the exponent: p = 2^(s*c - m) with one FMA.
+// One key tile of the pair kernel for this wave's QS query subtiles: S^T =
+// K Q^T from the K operands `kc`, the masked online softmax, and O^T += V^T P^T
+// from the transposed V tile `vt` in LDS.
+template <typename T, int QS, int DT, int KSTEPS, int LDV>
+__device__ __forceinline__ void tile_math(const AttnArgs& a, const u32x4 (&kc)[4][KSTEPS],
+                                          const u32x4 (&qreg)[QS][KSTEPS], const uint16_t* vt,
+                                          f32x4 (&oacc)[QS][DT], float (&m_run)[QS], float (&l_run)[QS],
+                                          int qw, int col, int grp, int n, int k0, bool full) {
+  // V^T operands: element e of step s2 is key 16*(2s2 + e/4) + 4grp + e%4 of dim 16t + col.
+  u32x4 vop[2][DT];
+#pragma unroll
+  for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+    for (int t = 0; t < DT; ++t) {
+      const uint16_t* vrow = &vt[(16 * t + col) * LDV];
+      const uint2 a0 = *reinterpret_cast<const uint2*>(vrow + 16 * (2 * s2) + 4 * grp);
+      const uint2 a1 = *reinterpret_cast<const uint2*>(vrow + 16 * (2 * s2 + 1) + 4 * grp);
+      vop[s2][t] = u32x4{a0.x, a0.y, a1.x, a1.y};
+    }
+  const bool fast = full && k0 + BK <= n;
+
+#pragma unroll
+  for (int qs = 0; qs < QS; ++qs) {
+    const int qrow = qw + 16 * qs + col;
+    // S^T = K Q^T: lane holds keys 16j + 4grp + i of query qrow.
+    f32x4 sacc[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      sacc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < KSTEPS; ++ks) sacc[j] = mfma16<T>(kc[j][ks], qreg[qs][ks], sacc[j]);
+    }
+    // Full tiles need no mask (rows past n are never stored); the branch is
+    // uniform. Other tiles evaluate the mask arithmetically per score.
+    float sv[16];
+    if (fast) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) sv[e] = sacc[e / 4][e % 4];
+    } else {
+      const int64_t dq = a.m.docs ? a.m.docs[min(qrow, n - 1)] : 0;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int key = k0 + 16 * (e / 4) + 4 * grp + e % 4;
+        const int64_t dk = a.m.docs ? a.m.docs[min(key, n - 1)] : 0;
+        const bool ok = full ? (key < n) & (qrow < n) : allowed_flat(a.m, qrow, key, n, dq, dk);
+        sv[e] = ok ? sacc[e / 4][e % 4] : -INFINITY;
+      }
+    }
+    float mx = fmaxf(fmaxf(sv[0], sv[1]), sv[2]);
+#pragma unroll
+    for (int e = 3; e < 15; e += 2) mx = fmaxf(fmaxf(mx, sv[e]), sv[e + 1]);
+    mx = fmaxf(mx, sv[15]);
+    mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+    const float c = a.scale_log2;
+    const float m_new = fmaxf(m_run[qs], mx * c);
+    const float ms = m_new == -INFINITY ? 0.f : m_new;
+    const float alpha = __builtin_amdgcn_exp2f(m_run[qs] - ms);
+    float psum = 0.f;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      sv[e] = __builtin_amdgcn_exp2f(fmaf(sv[e], c, -ms));
+      psum += sv[e];
+    }
+    psum += __shfl_xor(psum, 16, kWave);
+    psum += __shfl_xor(psum, 32, kWave);
+    l_run[qs] = l_run[qs] * alpha + psum;
+    m_run[qs] = m_new;
+    if (__ballot(alpha != 1.f)) {  // wave-uniform: skip the rescale once the maxima settle
+#pragma unroll
+      for (int t = 0; t < DT; ++t) oacc[qs][t] *= alpha;
+    }
+
+    // O^T += V^T P^T; the key order makes the B operand the lane's own probabilities.
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2) {
+      uint32_t pb[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        pb[e] = pack2<T>(sv[4 * (2 * s2 + e / 2) + (2 * e) % 4], sv[4 * (2 * s2 + e / 2) + (2 * e) % 4 + 1]);
+      const u32x4 pop = {pb[0], pb[1], pb[2], pb[3]};
+#pragma unroll
+      for (int t = 0; t < DT; ++t) oacc[qs][t] = mfma16<T>(vop[s2][t], pop, oacc[qs][t]);
+    }
+  }
+}
+
+constexpr int kPairWaves = 2;
 
 template <typename T>
-__global__ __launch_bounds__(kWaveTiles * kWave) void masked_attention_wave_kernel(AttnArgs a) {
-  constexpr int D = 64, KSTEPS = D / 32, DT = D / 16, QS = BQ / 16;
+__global__ __launch_bounds__(kPairWaves * kWave) __attribute__((amdgpu_waves_per_eu(2))) void masked_attention_pair_kernel(AttnArgs a) {
+  constexpr int D = 64, KSTEPS = D / 32, DT = D / 16, QS = BQ / 16 / kPairWaves;
   constexpr int LDV = BK + kPadK;
-  __shared__ __align__(16) uint16_t vt_all[kWaveTiles][D * LDV];
-  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  __shared__ __align__(16) uint16_t vt_s[2][D * LDV];
+  const int tid = threadIdx.x;
+  const int wave = tid / kWave, lane = tid % kWave;
   const int col = lane % 16, grp = lane / 16;
   const int n = a.n;
-  const int qt = blockIdx.x * kWaveTiles + wave;
-  if (qt * BQ >= n) return;  // waves are independent: no barrier below
-  uint16_t* vt_s = vt_all[wave];
+  const int qt = blockIdx.x;
   const int bh = blockIdx.y;
   const int b = bh / a.heads, h = bh % a.heads;
   const int q0 = qt * BQ;
   const int q1 = min(q0 + BQ, n) - 1;
+  const int qw = q0 + wave * 16 * QS;  // this wave's first query
 
   const uint16_t* qp = static_cast<const uint16_t*>(a.q) + b * a.qs[0] + h * a.qs[1];
   const uint16_t* kp = static_cast<const uint16_t*>(a.k) + b * a.ks[0] + h * a.ks[1];
   const uint16_t* vp = static_cast<const uint16_t*>(a.v) + b * a.vs[0] + h * a.vs[1];
 
-  // Q^T operands: subtile qs, lane holds Q[q0 + 16qs + col][32ks + 8grp .. +8].
+  // Q^T operands: subtile qs, lane holds Q[qw + 16qs + col][32ks + 8grp .. +8].
   u32x4 qreg[QS][KSTEPS];
 #pragma unroll
   for (int qs = 0; qs < QS; ++qs) {
-    const uint16_t* qr = qp + long(min(q0 + 16 * qs + col, n - 1)) * a.qs[2];
+    const uint16_t* qr = qp + long(min(qw + 16 * qs + col, n - 1)) * a.qs[2];
 #pragma unroll
     for (int ks = 0; ks < KSTEPS; ++ks) {
       const uint4 r = load16(qr + 32 * ks + 8 * grp);
@@ -369,23 +459,24 @@ __global__ __launch_bounds__(kWaveTiles * kWave) void masked_attention_wave_kern
   }
   const int lowg = min(tb.gend, tb.begin);
 
-  // K operands of key subtile j (keys 16j + col) and V rows 4*col + u of
-  // dims 8grp + 32hh .. +8, for the tile at key block kb.
-  u32x4 kreg[4][KSTEPS];
-  uint4 vreg[2][4];
-#define SFL_LOAD_TILE(kb)                                                                   \
+  // Per tile at key block kb: K operands of key subtile j (keys 16j + col),
+  // and this thread's share of V: rows 4*(tid % 16) + u (u < 4), dims
+  // 8*(tid / 16) .. +8 (128 threads cover 64 keys x 64 dims).
+  const int vr0 = 4 * (tid % 16), vd0 = 8 * (tid / 16);
+  u32x4 ka[4][KSTEPS], kb2[4][KSTEPS];  // K operands, alternating between tiles
+  uint4 vreg[4];
+#define SFL_LOAD_TILE(kb, KD)                                                               \
   {                                                                                         \
     const int k0_ = (kb) * BK;                                                              \
     _Pragma("unroll") for (int j = 0; j < 4; ++j) {                                         \
       const uint16_t* kr_ = kp + long(min(k0_ + 16 * j + col, n - 1)) * a.ks[2];            \
       _Pragma("unroll") for (int ks = 0; ks < KSTEPS; ++ks) {                               \
         const uint4 r_ = load16(kr_ + 32 * ks + 8 * grp);                                   \
-        kreg[j][ks] = u32x4{r_.x, r_.y, r_.z, r_.w};                                        \
+        KD[j][ks] = u32x4{r_.x, r_.y, r_.z, r_.w};                                          \
       }                                                                                     \
     }                                                                                       \
-    _Pragma("unroll") for (int hh = 0; hh < 2; ++hh)                                        \
-      _Pragma("unroll") for (int u = 0; u < 4; ++u)                                         \
-        vreg[hh][u] = load16(vp + long(min(k0_ + 4 * col + u, n - 1)) * a.vs[2] + 8 * grp + 32 * hh); \
+    _Pragma("unroll") for (int u = 0; u < 4; ++u)                                           \
+      vreg[u] = load16(vp + long(min(k0_ + vr0 + u, n - 1)) * a.vs[2] + vd0);               \
   }
 #define SFL_TILE_AT(it, kb_, fl_)                                                           \
   if (a.s.mode == 1) {                                                                      \
@@ -395,144 +486,67 @@ __global__ __launch_bounds__(kWaveTiles * kWave) void masked_attention_wave_kern
     kb_ = (it) < lowg ? (it) : tb.begin + ((it) - lowg);                                    \
     fl_ = !a.m.docs && covered(tb, kb_ * BK, min(kb_ * BK + BK, n) - 1);                    \
   }
+  // V^T tile into LDS buffer `buf`: dims vd0 + e, keys vr0 .. vr0+3 (one 8-byte store each).
+#define SFL_STORE_VT(buf)                                                                   \
+  {                                                                                         \
+    const uint32_t w0_[4] = {vreg[0].x, vreg[0].y, vreg[0].z, vreg[0].w};                  \
+    const uint32_t w1_[4] = {vreg[1].x, vreg[1].y, vreg[1].z, vreg[1].w};                  \
+    const uint32_t w2_[4] = {vreg[2].x, vreg[2].y, vreg[2].z, vreg[2].w};                  \
+    const uint32_t w3_[4] = {vreg[3].x, vreg[3].y, vreg[3].z, vreg[3].w};                  \
+    _Pragma("unroll") for (int e = 0; e < 8; ++e) {                                         \
+      /* byte permute: the low (e even) or high (e odd) halves of two words */              \
+      const uint32_t sel_ = (e & 1) ? 0x07060302u : 0x05040100u;                             \
+      const uint32_t k01_ = __builtin_amdgcn_perm(w1_[e / 2], w0_[e / 2], sel_);             \
+      const uint32_t k23_ = __builtin_amdgcn_perm(w3_[e / 2], w2_[e / 2], sel_);             \
+      *reinterpret_cast<uint2*>(&vt_s[buf][(vd0 + e) * LDV + vr0]) = make_uint2(k01_, k23_); \
+    }                                                                                       \
+  }
 
   if (count > 0) {
     int kb0;
     bool f0;
     SFL_TILE_AT(0, kb0, f0)
     (void)f0;
-    SFL_LOAD_TILE(kb0)
+    SFL_LOAD_TILE(kb0, ka)
+    SFL_STORE_VT(0)
   }
-  for (int it = 0; it < count; ++it) {
-    int kb;
-    bool full;
-    SFL_TILE_AT(it, kb, full)
-    full = full && a.s.use_full;
-    const int k0 = kb * BK;
-
-    // V^T into this wave's LDS buffer: dim 8grp + 32hh + e, keys 4col .. 4col+3.
-    // (The previous tile's reads of the buffer precede these writes in the
-    // wave's in-order LDS queue; the fences keep the compiler from moving them.)
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-#pragma unroll
-    for (int hh = 0; hh < 2; ++hh) {
-      const uint32_t w0[4] = {vreg[hh][0].x, vreg[hh][0].y, vreg[hh][0].z, vreg[hh][0].w};
-      const uint32_t w1[4] = {vreg[hh][1].x, vreg[hh][1].y, vreg[hh][1].z, vreg[hh][1].w};
-      const uint32_t w2[4] = {vreg[hh][2].x, vreg[hh][2].y, vreg[hh][2].z, vreg[hh][2].w};
-      const uint32_t w3[4] = {vreg[hh][3].x, vreg[hh][3].y, vreg[hh][3].z, vreg[hh][3].w};
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int sh = (e & 1) * 16;
-        const uint32_t k01 = ((w0[e / 2] >> sh) & 0xffffu) | (((w1[e / 2] >> sh) & 0xffffu) << 16);
-        const uint32_t k23 = ((w2[e / 2] >> sh) & 0xffffu) | (((w3[e / 2] >> sh) & 0xffffu) << 16);
-        *reinterpret_cast<uint2*>(vt_s + (8 * grp + 32 * hh + e) * LDV + 4 * col) = make_uint2(k01, k23);
-      }
-    }
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-
-    u32x4 kcur[4][KSTEPS];
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int ks = 0; ks < KSTEPS; ++ks) kcur[j][ks] = kreg[j][ks];
-    if (it + 1 < count) {
-      int kbn;
-      bool fn;
-      SFL_TILE_AT(it + 1, kbn, fn)
-      (void)fn;
-      SFL_LOAD_TILE(kbn)
-    }
-
-    // V^T operands (shared by the 4 query subtiles): element e of step s2 is
-    // key 16*(2s2 + e/4) + 4grp + e%4 of dim 16t + col.
-    u32x4 vop[2][DT];
-#pragma unroll
-    for (int s2 = 0; s2 < 2; ++s2)
-#pragma unroll
-      for (int t = 0; t < DT; ++t) {
-        const uint16_t* vrow = vt_s + (16 * t + col) * LDV;
-        const uint2 a0 = *reinterpret_cast<const uint2*>(vrow + 16 * (2 * s2) + 4 * grp);
-        const uint2 a1 = *reinterpret_cast<const uint2*>(vrow + 16 * (2 * s2 + 1) + 4 * grp);
-        vop[s2][t] = u32x4{a0.x, a0.y, a1.x, a1.y};
-      }
-    const bool fast = full && k0 + BK <= n;
-    int64_t dkey[16];
-#pragma unroll
-    for (int e = 0; e < 16; ++e)
-      dkey[e] = (!fast && a.m.docs) ? a.m.docs[min(k0 + 16 * (e / 4) + 4 * grp + e % 4, n - 1)] : 0;
-
-#pragma unroll
-    for (int qs = 0; qs < QS; ++qs) {
-      const int qrow = q0 + 16 * qs + col;
-      // S^T = K Q^T: lane holds keys 16j + 4grp + i of query qrow.
-      f32x4 sacc[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        sacc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int ks = 0; ks < KSTEPS; ++ks) sacc[j] = mfma16<T>(kcur[j][ks], qreg[qs][ks], sacc[j]);
-      }
-      // Full tiles need no mask (rows past n are never stored); the branch is
-      // uniform. Other tiles evaluate the mask arithmetically per score.
-      // Scores stay unscaled: scale > 0 commutes with the max, and the scale
-      // is folded into the exponent, p = 2^(s*c - m) with one FMA.
-      float sv[16];
-      if (fast) {
-#pragma unroll
-        for (int e = 0; e < 16; ++e) sv[e] = sacc[e / 4][e % 4];
-      } else {
-        const int64_t dq = a.m.docs ? a.m.docs[min(qrow, n - 1)] : 0;
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const int key = k0 + 16 * (e / 4) + 4 * grp + e % 4;
-          const bool ok = full ? (key < n) & (qrow < n) : allowed_flat(a.m, qrow, key, n, dq, dkey[e]);
-          sv[e] = ok ? sacc[e / 4][e % 4] : -INFINITY;
-        }
-      }
-      float mx = fmaxf(fmaxf(sv[0], sv[1]), sv[2]);
-#pragma unroll
-      for (int e = 3; e < 15; e += 2) mx = fmaxf(fmaxf(mx, sv[e]), sv[e + 1]);
-      mx = fmaxf(mx, sv[15]);
-      mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
-      mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
-      const float c = a.scale_log2;
-      const float m_new = fmaxf(m_run[qs], mx * c);
-      const float ms = m_new == -INFINITY ? 0.f : m_new;
-      const float alpha = __builtin_amdgcn_exp2f(m_run[qs] - ms);
-      float psum = 0.f;
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        sv[e] = __builtin_amdgcn_exp2f(fmaf(sv[e], c, -ms));
-        psum += sv[e];
-      }
-      psum += __shfl_xor(psum, 16, kWave);
-      psum += __shfl_xor(psum, 32, kWave);
-      l_run[qs] = l_run[qs] * alpha + psum;
-      m_run[qs] = m_new;
-      if (__ballot(alpha != 1.f)) {  // wave-uniform: skip the rescale once the maxima settle
-#pragma unroll
-        for (int t = 0; t < DT; ++t) oacc[qs][t] *= alpha;
-      }
-
-      // O^T += V^T P^T with the key order of the 16-queries kernel above.
-#pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2) {
-        uint32_t pb[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          pb[e] = pack2<T>(sv[4 * (2 * s2 + e / 2) + (2 * e) % 4], sv[4 * (2 * s2 + e / 2) + (2 * e) % 4 + 1]);
-        const u32x4 pop = {pb[0], pb[1], pb[2], pb[3]};
-#pragma unroll
-        for (int t = 0; t < DT; ++t) oacc[qs][t] = mfma16<T>(vop[s2][t], pop, oacc[qs][t]);
-      }
-    }
+  __syncthreads();
+  // Tile `it` uses the K operands in KC and prefetches tile it+1 into KN; the
+  // loop is unrolled twice so the two register sets swap roles without copies.
+#define SFL_TILE_STEP(it, KC, KN)                                                           \
+  {                                                                                         \
+    int kb;                                                                                 \
+    bool full;                                                                              \
+    SFL_TILE_AT(it, kb, full)                                                               \
+    full = full && a.s.use_full;                                                            \
+    const int k0 = kb * BK;                                                                 \
+    const int buf = (it) & 1;                                                               \
+    const bool more = (it) + 1 < count;                                                     \
+    if (more) {                                                                             \
+      int kbn;                                                                              \
+      bool fn;                                                                              \
+      SFL_TILE_AT((it) + 1, kbn, fn)                                                        \
+      (void)fn;                                                                             \
+      SFL_LOAD_TILE(kbn, KN)                                                                \
+    }                                                                                       \
+    tile_math<T, QS, DT, KSTEPS, LDV>(a, KC, qreg, vt_s[buf], oacc, m_run, l_run, qw, col,  \
+                                      grp, n, k0, full);                                    \
+    if (more) SFL_STORE_VT(buf ^ 1)                                                         \
+    __syncthreads();                                                                        \
   }
+  for (int it = 0; it < count; it += 2) {
+    SFL_TILE_STEP(it, ka, kb2)
+    if (it + 1 >= count) break;
+    SFL_TILE_STEP(it + 1, kb2, ka)
+  }
+#undef SFL_TILE_STEP
 #undef SFL_LOAD_TILE
 #undef SFL_TILE_AT
+#undef SFL_STORE_VT
 
 #pragma unroll
   for (int qs = 0; qs < QS; ++qs) {
-    const int qrow = q0 + 16 * qs + col;
+    const int qrow = qw + 16 * qs + col;
     if (qrow >= n) continue;
     const float inv = l_run[qs] > 0.f ? 1.f / l_run[qs] : 0.f;
     uint16_t* op = static_cast<uint16_t*>(a.o) + b * a.os[0] + h * a.os[1] + long(qrow) * a.os[2];
@@ -553,12 +567,9 @@ int launch_masked(const AttnArgs& a, int batch, int dim, hipStream_t stream) {
   dim3 grid((a.n + BQ - 1) / BQ, batch * a.heads);
   switch (dim) {
     case 32: hipLaunchKernelGGL((masked_attention_kernel<T, 32>), grid, dim3(kThreads), 0, stream, a); break;
-    case 64: {
-      const int tiles = (a.n + BQ - 1) / BQ;
-      dim3 wgrid((tiles + kWaveTiles - 1) / kWaveTiles, batch * a.heads);
-      hipLaunchKernelGGL((masked_attention_wave_kernel<T>), wgrid, dim3(kWaveTiles * kWave), 0, stream, a);
+    case 64:
+      hipLaunchKernelGGL((masked_attention_pair_kernel<T>), grid, dim3(kPairWaves * kWave), 0, stream, a);
       break;
-    }
     case 128: hipLaunchKernelGGL((masked_attention_kernel<T, 128>), grid, dim3(kThreads), 0, stream, a); break;
     default: return set_error(SFL_ERR_UNSUPPORTED, "masked_attention: head dim must be 32, 64 or 128");
   }
