@@ -13,8 +13,13 @@ steps always cover positions 3072 .. 3072+K-1 (attention lengths 3073 ..
 Printed JSON (one line): decode tok/s; ``roofline`` for the dominant kernel,
 split-KV decode attention, timed with HIP events on its launch stream at the
 mean decode context of the timed region, rotating over the 24 layers' caches so
-that every call streams from HBM as it does inside the decode loop; ``cpu_baseline``: the CPU oracle's
-KV-cached decode step on this host's cores on a bounded sample.
+that every call streams from HBM as it does inside the decode loop; ``prefill``
+(the prompt pass, MFMA TFLOP/s against the bf16 dense peak);
+``decode_attention_config4`` and ``masked_attention_config5`` (BASELINE
+configs 4 and 5 as operator microbenchmarks); ``cpu_baseline``: the CPU
+oracle's KV-cached decode step on this host's cores on a bounded sample, and
+``cpu_reference_semantics``: one full-recompute forward over the prompt, as the
+reference produces a token.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline]
 """
@@ -33,6 +38,7 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
 PROMPT = 3072
 CONTEXT = 4096
 BATCH = 16
@@ -54,6 +60,17 @@ def step_bytes(cfg, batch, length):
     kv_read = cfg.num_layers * batch * length * 2 * cfg.d_model * 2
     kv_append = cfg.num_layers * batch * 2 * cfg.d_model * 2
     return weights + kv_read + kv_append
+
+
+def prefill_flops(cfg, batch, length):
+    """MFMA work of the prefill: the per-layer GEMMs over B*T rows, the mask-exact
+    causal attention (QK^T and PV, 4*dk flops per admissible pair), and the head
+    for the last row of each sequence (the only row the decode loop needs)."""
+    rows = batch * length
+    d, f = cfg.d_model, cfg.d_ff
+    gemm = 2 * rows * cfg.num_layers * (4 * d * d + 3 * d * f) + 2 * batch * d * cfg.vocab_size
+    attention = 4 * cfg.head_dim * (length * (length + 1) // 2) * batch * cfg.num_heads * cfg.num_layers
+    return gemm, attention
 
 
 def time_events(fn, reps):
@@ -94,6 +111,27 @@ def cpu_baseline(cfg, seconds=12.0, max_steps=32):
             "kind": "port",
             "sample": f"{steps} KV-cached fp32 decode steps of the CPU oracle (oracle/model.py KVCacheOracle), "
                       f"324M, batch {BATCH}, attention length {PROMPT}..{PROMPT + steps}; os.cpu_count()={threads}"}
+
+
+def cpu_reference_semantics(cfg, length=PROMPT):
+    """One step as the reference must run it: a full forward over the whole prefix (no KV cache),
+    fp32 on the host cores, for one sequence of ``length`` tokens; its cost per generated token."""
+    import torch
+
+    from oracle.model import forward
+    from systems_for_llms_amd.weights import seeded_prompt, seeded_state_dict
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    sd = seeded_state_dict(cfg, WEIGHT_SEED)
+    ids = seeded_prompt(cfg.vocab_size, 1, length, PROMPT_SEED)
+    started = time.perf_counter()
+    with torch.no_grad():
+        forward(sd, cfg, ids, torch.float32)
+    elapsed = time.perf_counter() - started
+    return {"value": round(1.0 / elapsed, 4), "unit": "tok/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"one full-recompute fp32 forward of the CPU oracle (oracle/model.py forward) over a "
+                      f"{length}-token prefix, batch 1 = one generated token: {elapsed:.2f} s"}
 
 
 def profile_target_attention(reps: int = 24) -> int:
@@ -237,6 +275,26 @@ def main() -> int:
     del qc, kc, vc
     log(f"config-4 decode attention: {c4_ms * 1000:.1f} us, {c4_gbs:.0f} GB/s")
 
+    # BASELINE config 5 masked prefill attention: [4,16,4096,64] bf16, causal,
+    # window_left 1023, 4 global prefix blocks of 64 (CSR schedule).
+    from systems_for_llms_amd.attention import attention
+    from systems_for_llms_amd.masks import MaskSpec, compile_mask
+
+    spec5 = MaskSpec(causal=True, window_left=1023, global_prefix=256)
+    g5 = torch.Generator(device="cuda").manual_seed(5)
+    q5, k5, v5 = (torch.randn((4, 16, 4096, 64), device="cuda", generator=g5, dtype=torch.bfloat16)
+                  for _ in range(3))
+    sched5 = compile_mask(4096, spec5, 64, 64)
+    pairs5 = sum(min(i, 1023) + 1 + max(0, min(256, i - 1023)) for i in range(4096))
+    for _ in range(3):
+        attention(q5, k5, v5, sched5, spec5)
+    c5_ms = time_events(lambda: attention(q5, k5, v5, sched5, spec5), 20)
+    c5_tflops = 4 * 64 * pairs5 * 4 * 16 / (c5_ms * 1e-3) / 1e12
+    del q5, k5, v5
+    log(f"config-5 masked attention: {c5_ms * 1000:.1f} us, {c5_tflops:.0f} TFLOP/s (mask-exact)")
+    gemm_flops, attn_flops = prefill_flops(cfg, BATCH, PROMPT)
+    prefill_tflops = (gemm_flops + attn_flops) / prefill_s / 1e12
+
     # HBM traffic per launch from the committed PMC record of the same launch
     # shape (FETCH_SIZE + WRITE_SIZE, calibrated on a copy of known size).
     traffic = None
@@ -246,11 +304,13 @@ def main() -> int:
 
     e2e_bytes = step_bytes(cfg, BATCH, mean_len)
     e2e_gbs = e2e_bytes / (ms_per_step * 1e-3) / 1e9
-    baseline = None
+    baseline = reference_semantics = None
     if not args.no_cpu_baseline:
         log("timing the CPU oracle baseline ...")
         baseline = cpu_baseline(cfg)
         log(f"cpu baseline {baseline['value']} tok/s on {baseline['cores']} threads")
+        reference_semantics = cpu_reference_semantics(cfg)
+        log(f"cpu full-recompute step: {reference_semantics['value']} tok/s")
 
     record = {
         "metric": "decode tok/s, 324M bf16 ctx4K B=16; decode-attn HBM GB/s as % of peak",
@@ -281,10 +341,22 @@ def main() -> int:
                 "roofline_tok_s": round(BATCH / (e2e_bytes / (HBM_PEAK_GBS * 1e9)), 1),
                 "prefill_s": round(prefill_s, 4), "prefill_tok_s": round(BATCH * PROMPT / prefill_s, 1),
                 "prefill_path": "MFMA GEMMs (QKV+RoPE+append, O, SwiGLU, W2) + MFMA causal attention"},
+        "prefill": {"ms": round(prefill_s * 1000, 2), "tok_s": round(BATCH * PROMPT / prefill_s, 1),
+                    "gemm_tflop": round(gemm_flops / 1e12, 3), "attention_tflop": round(attn_flops / 1e12, 3),
+                    "achieved_tflops": round(prefill_tflops, 1), "peak_tflops": MFMA_BF16_PEAK_TFLOPS,
+                    "frac": round(prefill_tflops / MFMA_BF16_PEAK_TFLOPS, 4),
+                    "note": "whole prefill (GEMMs, causal attention, norms, embedding) timed end to end"},
         "decode_attention_config4": {"us": round(c4_ms * 1000, 1), "achieved_gbs": round(c4_gbs, 1),
                                      "frac": round(c4_gbs / HBM_PEAK_GBS, 4), "bytes": c4_bytes,
                                      "shape": "B=64 H=16 D=64 bf16 ragged lengths U[1024,16384] seed 4"},
+        "masked_attention_config5": {"us": round(c5_ms * 1000, 1), "tflops": round(c5_tflops, 1),
+                                     "peak_tflops": MFMA_BF16_PEAK_TFLOPS,
+                                     "frac": round(c5_tflops / MFMA_BF16_PEAK_TFLOPS, 4),
+                                     "flop": 4 * 64 * pairs5 * 4 * 16,
+                                     "shape": "B=4 H=16 N=4096 D=64 bf16, causal, window_left 1023, "
+                                              "4 global prefix blocks, CSR schedule; mask-exact flops"},
         "cpu_baseline": baseline,
+        "cpu_reference_semantics": reference_semantics,
     }
     print(json.dumps(record), flush=True)
     return 0
