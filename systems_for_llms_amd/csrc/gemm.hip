@@ -54,6 +54,30 @@ __device__ __forceinline__ f32x4 mfma_bf16(const u32x4& a, const u32x4& b, f32x4
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
 }
 
+// One 16-byte-per-lane buffer load with an LDS destination: lane i's bytes
+// land at LDS byte offset lds + 16 i (M0 holds the wave-uniform base). Written
+// as inline assembly because the compiler, unable to tell LDS-DMA targets
+// apart, otherwise waits for every outstanding load before each LDS read,
+// which serialises the prefetch; the caller therefore counts these loads
+// itself (s_waitcnt vmcnt). Out-of-range offsets read zeros (buffer range
+// check).
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ i32x4_t buffer_rsrc(const void* base, unsigned bytes) {
+  const unsigned long long b = reinterpret_cast<unsigned long long>(base);
+  return i32x4_t{int(b & 0xffffffffu), int(b >> 32), int(bytes), 0x00020000};
+}
+__device__ __forceinline__ void lds_load16(i32x4_t rsrc, unsigned lds, unsigned voff, unsigned soff) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               :: "s"(lds), "v"(voff), "s"(rsrc), "s"(soff) : "memory");
+}
+__device__ __forceinline__ unsigned lds_offset(const void* p) {
+  return unsigned(size_t((__attribute__((address_space(3))) const char*)(p)));
+}
+
+// s_waitcnt operand that waits for vmcnt <= n only (gfx9 encoding: vmcnt in
+// bits 3:0 and 15:14, expcnt 6:4 and lgkmcnt 11:8 left at their maxima).
+constexpr int sfl_vmcnt(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+
 // v, or zeros when !keep. Selected per component: a select of whole uint4
 // structs is lowered through scratch memory.
 __device__ __forceinline__ uint4 keep16(const uint4& v, bool keep) {
@@ -62,6 +86,92 @@ __device__ __forceinline__ uint4 keep16(const uint4& v, bool keep) {
 
 __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
   return uint32_t(f32_to_bf16_bits(lo)) | (uint32_t(f32_to_bf16_bits(hi)) << 16);
+}
+
+// Where a lane's 4 QKV features and its token go: section (0 q, 1 k, 2 v),
+// head, dim of the first feature; batch row and position of the token.
+// Computed once per feature tile / token tile by the caller (integer
+// divisions by runtime sizes are long instruction sequences).
+struct QkvFeat { int section, head, dim; };
+struct QkvTok { int b, t; };
+
+__device__ __forceinline__ QkvFeat qkv_feat(const GemmArgs& g, int n) {
+  const int section = n / g.d_model;
+  const int f = n - section * g.d_model;
+  const int head = f / g.head_dim;
+  return QkvFeat{section, head, f - head * g.head_dim};
+}
+__device__ __forceinline__ QkvTok qkv_tok(const GemmArgs& g, int m) {
+  const int b = m / g.seq;
+  return QkvTok{b, m - b * g.seq};
+}
+
+// Epilogue of one 16x16 MFMA tile: v holds features nt + 4*grp + (0..3) of
+// token m. Every lane must call it (the SwiGLU pairing shuffles).
+template <int E>
+__device__ __forceinline__ void store_tile(const GemmArgs& g, const f32x4& v, int nt, int grp, int m,
+                                           QkvFeat qf = QkvFeat{}, QkvTok qt = QkvTok{}) {
+  const int n = nt + 4 * grp;
+  float y[4] = {v[0], v[1], v[2], v[3]};
+  if constexpr (E == G_SWIGLU) {
+    // Rows 0..7 of the 16-row tile are W1 features, rows 8..15 the
+    // matching W3 features: lane groups 0,1 pair with groups 2,3.
+    float c3[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) c3[e] = __shfl_xor(y[e], 32, kWave);
+    if (grp >= 2 || m >= g.m) return;
+    const int f = nt / 2 + 4 * grp;  // hidden feature index
+    if (f >= g.n / 2) return;
+    float h[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) h[e] = y[e] / (1.f + expf(-y[e])) * c3[e];
+    *reinterpret_cast<uint2*>(g.h_out + long(m) * (g.n / 2) + f) = make_uint2(pack_bf16(h[0], h[1]), pack_bf16(h[2], h[3]));
+  } else {
+    if (m >= g.m || n >= g.n) return;
+    if constexpr (E == G_PLAIN) {
+      if (g.c_f32) {
+        float* c = static_cast<float*>(g.c) + long(m) * g.n + n;
+        if (n + 3 < g.n && (g.n & 3) == 0) {
+          float4 old = g.accumulate ? *reinterpret_cast<const float4*>(c) : make_float4(0.f, 0.f, 0.f, 0.f);
+          *reinterpret_cast<float4*>(c) = make_float4(old.x + y[0], old.y + y[1], old.z + y[2], old.w + y[3]);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (n + e < g.n) c[e] = (g.accumulate ? c[e] : 0.f) + y[e];
+        }
+      } else {
+        uint16_t* c = static_cast<uint16_t*>(g.c) + long(m) * g.n + n;
+        if (n + 3 < g.n && (g.n & 3) == 0) {
+          *reinterpret_cast<uint2*>(c) = make_uint2(pack_bf16(y[0], y[1]), pack_bf16(y[2], y[3]));
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (n + e < g.n) c[e] = f32_to_bf16_bits(y[e]);
+        }
+      }
+    } else {  // G_QKV
+      const int section = qf.section, head = qf.head, dim = qf.dim;
+      const int b = qt.b, t = qt.t;
+      if (section < 2) {
+        const int half = g.head_dim / 2;
+        const float2 c = *reinterpret_cast<const float2*>(g.cos_t + long(t) * half + dim / 2);
+        const float2 s = *reinterpret_cast<const float2*>(g.sin_t + long(t) * half + dim / 2);
+        const float e0 = y[0], o0 = y[1], e1 = y[2], o1 = y[3];
+        y[0] = e0 * c.x - o0 * s.x;
+        y[1] = e0 * s.x + o0 * c.x;
+        y[2] = e1 * c.y - o1 * s.y;
+        y[3] = e1 * s.y + o1 * c.y;
+      }
+      uint16_t* dst;
+      if (section == 0) {
+        dst = g.q_out + ((long(b) * g.heads + head) * g.seq + t) * g.head_dim + dim;
+      } else {
+        uint16_t* cache = section == 1 ? g.k_cache : g.v_cache;
+        dst = cache + ((long(b) * g.heads + head) * g.cap + t) * g.head_dim + dim;
+      }
+      *reinterpret_cast<uint2*>(dst) = make_uint2(pack_bf16(y[0], y[1]), pack_bf16(y[2], y[3]));
+    }
+  }
 }
 
 template <int E>
@@ -134,68 +244,179 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
 #undef SFL_GEMM_SSTORE
 
   // Epilogue: acc[i][j] holds features n0 + wn*64 + 16i + 4grp + (0..3) of token m0 + wm*64 + 16j + col.
+  QkvTok tok[4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int m = m0 + wm * 64 + j * 16 + col;
+  for (int j = 0; j < 4; ++j) tok[j] = E == G_QKV ? qkv_tok(g, m0 + wm * 64 + j * 16 + col) : QkvTok{};
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int n = n0 + wn * 64 + i * 16 + 4 * grp;
-      float y[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
+  for (int i = 0; i < 4; ++i) {
+    const QkvFeat feat = E == G_QKV ? qkv_feat(g, n0 + wn * 64 + i * 16 + 4 * grp) : QkvFeat{};
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      store_tile<E>(g, acc[i][j], n0 + wn * 64 + i * 16, grp, m0 + wm * 64 + j * 16 + col, feat, tok[j]);
+  }
+}
+
+// GEMM for K % 64 == 0 on v_mfma_f32_32x32x16_bf16 (on gfx950 the 32x32
+// form sustains about twice the bf16 rate of the 16x16x32 form used above).
+// A workgroup of 4 waves (2 x 2) computes 128 features x 128 tokens; wave
+// (wn, wm) owns 2 x 2 MFMA tiles of 32x32. Operands reach LDS through buffer
+// loads with an LDS destination (no register staging). A K step stores each
+// operand tile row-major, 128 bytes (64 k values) per row in 8 slots of 16
+// bytes, slot = (16-byte column) ^ ((row >> 1) & 7): a load instruction moves
+// 8 whole rows (1 KB, full cache lines, the lanes of a row in swizzled order)
+// and every MFMA operand read -- 32 rows x 2 columns per instruction -- is
+// free of bank conflicts. Rows past the matrix read as zeros through the
+// buffer range check. K advances by 64 through two LDS stages, the loads of
+// the next step in flight while a step computes.
+constexpr int K2 = 64;     // K step
+constexpr int TB = 128;    // features and tokens per workgroup
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ f32x16 mfma32_bf16(const u32x4& a, const u32x4& b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+
+struct Stage32 {
+  uint4 w[TB][8];  // [row][swizzled 16-byte slot]
+  uint4 a[TB][8];
+};
+
+// Tile of workgroup b in a 1-D grid of tn x tm tiles, XCD-aware: workgroups
+// are dealt to the 8 XCDs round-robin (b % 8) and each XCD has its own L2, so
+// XCD x is given a contiguous range of the tile order, and that order walks
+// groups of kGroupM token tiles across the feature tiles. The ~32 workgroups
+// an XCD runs at once then cover about 4 token tiles x 8 feature tiles, whose
+// operands (~3 MB) stay in its 4 MB L2.
+constexpr int kXcds = 8;
+constexpr int kGroupM = 4;
+
+__device__ __forceinline__ int2 xcd_tile(int b, int tn, int tm) {
+  const int total = tn * tm;
+  const int x = b % kXcds, idx = b / kXcds;
+  const int base = total / kXcds, extra = total % kXcds;  // XCD x gets base + (x < extra) tiles
+  const int t = x * base + min(x, extra) + idx;
+  const int group = t / (kGroupM * tn);
+  const int gm0 = group * kGroupM;
+  const int gsize = min(kGroupM, tm - gm0);
+  const int r = t - group * kGroupM * tn;
+  return make_int2(r / gsize, gm0 + r % gsize);  // (feature tile, token tile)
+}
+
+template <int E>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) void gemm32_kernel(GemmArgs g) {
+  // Distinct LDS objects per stage; see lds_load16 for why the loads are counted by hand.
+  __shared__ Stage32 st0, st1;
+  const int tid = threadIdx.x;
+  // readfirstlane: the wave index is uniform, so the LDS destinations live in scalar registers.
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave), lane = tid % kWave;
+  const int wn = wave / 2, wm = wave % 2;
+  const int l32 = lane % 32, hf = lane / 32;
+  const int2 tile = xcd_tile(blockIdx.x, (g.n + TB - 1) / TB, (g.m + TB - 1) / TB);
+  const int n0 = tile.x * TB;
+  const int m0 = tile.y * TB;
+  const int ksteps = g.k / K2;
+
+  // Loads: the 2 x 128 rows of a step are 32 chunks of 8 rows; wave w takes
+  // chunks w, w + 4, ... Lane i of a chunk moves row 8c + i/8 into slot i%8,
+  // i.e. column (i%8) ^ ((row >> 1) & 7); the swizzle depends on the chunk's
+  // parity only, so two byte offsets per lane cover every chunk.
+  const i32x4_t rw = buffer_rsrc(g.w, unsigned(g.n * g.k * 2));
+  const i32x4_t ra = buffer_rsrc(g.a, unsigned(g.m * g.k * 2));
+  const int rr = lane / 8, pos = lane % 8;
+  unsigned voff[2];
+#pragma unroll
+  for (int par = 0; par < 2; ++par) voff[par] = unsigned((rr * g.k + 8 * (pos ^ ((4 * par + rr / 2) & 7))) * 2);
+  constexpr int CH = TB / 8;  // chunks per operand
+
+#define SFL_G32_ISSUE(stage, kt)                                                            \
+  {                                                                                         \
+    _Pragma("unroll") for (int c0 = 0; c0 < 2 * CH; c0 += 4) {                              \
+      const int c = c0 + wave;                                                              \
+      if (c < CH)                                                                           \
+        lds_load16(rw, lds_offset(&stage.w[8 * c][0]), voff[c & 1],                         \
+                   unsigned(((n0 + 8 * c) * g.k + (kt) * K2) * 2));                         \
+      else                                                                                  \
+        lds_load16(ra, lds_offset(&stage.a[8 * (c - CH)][0]), voff[(c - CH) & 1],           \
+                   unsigned(((m0 + 8 * (c - CH)) * g.k + (kt) * K2) * 2));                  \
+    }                                                                                       \
+  }
+  // Operand reads: lane (l32, hf) takes row 32t + l32, column 2kk + hf.
+  const int sw = (l32 >> 1) & 7;
+#define SFL_G32_COMPUTE(stage)                                                              \
+  _Pragma("unroll") for (int kk = 0; kk < 4; ++kk) {                                        \
+    const int slot = (2 * kk + hf) ^ sw;                                                    \
+    u32x4 af[2], bfr[2];                                                                    \
+    _Pragma("unroll") for (int t = 0; t < 2; ++t) {                                         \
+      const uint4 ra_ = stage.w[32 * (2 * wn + t) + l32][slot];                             \
+      const uint4 rb_ = stage.a[32 * (2 * wm + t) + l32][slot];                             \
+      af[t] = u32x4{ra_.x, ra_.y, ra_.z, ra_.w};                                            \
+      bfr[t] = u32x4{rb_.x, rb_.y, rb_.z, rb_.w};                                           \
+    }                                                                                       \
+    _Pragma("unroll") for (int i = 0; i < 2; ++i)                                           \
+      _Pragma("unroll") for (int j = 0; j < 2; ++j) acc[i][j] = mfma32_bf16(af[i], bfr[j], acc[i][j]); \
+  }
+
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+
+  // Two LDS stages (64 KB, two workgroups per CU): step kt computes from one
+  // stage while the loads of step kt+1 fill the other; unrolled twice so both
+  // stages are compile-time objects.
+  SFL_G32_ISSUE(st0, 0)
+#define SFL_G32_STEP(kt, cur, next)                                                         \
+  {                                                                                         \
+    __builtin_amdgcn_s_waitcnt(sfl_vmcnt(0));                                               \
+    __syncthreads(); /* every wave's loads of `cur` landed; `next` is no longer read */    \
+    if ((kt) + 1 < ksteps) SFL_G32_ISSUE(next, (kt) + 1)                                    \
+    SFL_G32_COMPUTE(cur)                                                                    \
+  }
+  for (int kt = 0; kt < ksteps; kt += 2) {
+    SFL_G32_STEP(kt, st0, st1)
+    if (kt + 1 >= ksteps) break;
+    SFL_G32_STEP(kt + 1, st1, st0)
+  }
+#undef SFL_G32_STEP
+#undef SFL_G32_COMPUTE
+#undef SFL_G32_ISSUE
+
+  // acc[i][j][4q + e] holds feature n0 + 64wn + 32i + 8q + 4hf + e of token m0 + 64wm + 32j + l32.
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int m = m0 + 64 * wm + 32 * j + l32;
+    const QkvTok tok = E == G_QKV ? qkv_tok(g, m) : QkvTok{};
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int nt = n0 + 64 * wn + 32 * i;
       if constexpr (E == G_SWIGLU) {
-        // Rows 16i + 0..7 of the tile are W1 features, rows 16i + 8..15 the
-        // matching W3 features: lane groups 0,1 pair with groups 2,3.
-        float c3[4];
+        // W1/W3 interleaved in blocks of 8 rows: groups q = 0, 2 are W1 features,
+        // q + 1 the matching W3 features, all in this lane.
+        if (m >= g.m) continue;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) c3[e] = __shfl_xor(y[e], 32, kWave);
-        if (grp >= 2 || m >= g.m) continue;
-        const int f = (n0 + wn * 64 + i * 16) / 2 + 4 * grp;  // hidden feature index
-        if (f >= g.n / 2) continue;
-        float h[4];
+        for (int q = 0; q < 4; q += 2) {
+          const int f = nt / 2 + 4 * q + 4 * hf;  // hidden feature index
+          if (f >= g.n / 2) continue;
+          float h[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) h[e] = y[e] / (1.f + expf(-y[e])) * c3[e];
-        *reinterpret_cast<uint2*>(g.h_out + long(m) * (g.n / 2) + f) = make_uint2(pack_bf16(h[0], h[1]), pack_bf16(h[2], h[3]));
+          for (int e = 0; e < 4; ++e) {
+            const float a1 = acc[i][j][4 * q + e], a3 = acc[i][j][4 * q + 4 + e];
+            h[e] = a1 / (1.f + expf(-a1)) * a3;
+          }
+          *reinterpret_cast<uint2*>(g.h_out + long(m) * (g.n / 2) + f) =
+              make_uint2(pack_bf16(h[0], h[1]), pack_bf16(h[2], h[3]));
+        }
       } else {
-        if (m >= g.m || n >= g.n) continue;
-        if constexpr (E == G_PLAIN) {
-          if (g.c_f32) {
-            float* c = static_cast<float*>(g.c) + long(m) * g.n + n;
-            if (n + 3 < g.n && (g.n & 3) == 0) {
-              float4 old = g.accumulate ? *reinterpret_cast<const float4*>(c) : make_float4(0.f, 0.f, 0.f, 0.f);
-              *reinterpret_cast<float4*>(c) = make_float4(old.x + y[0], old.y + y[1], old.z + y[2], old.w + y[3]);
-            } else {
-              for (int e = 0; e < 4 && n + e < g.n; ++e) c[e] = (g.accumulate ? c[e] : 0.f) + y[e];
-            }
-          } else {
-            uint16_t* c = static_cast<uint16_t*>(g.c) + long(m) * g.n + n;
-            if (n + 3 < g.n && (g.n & 3) == 0) {
-              *reinterpret_cast<uint2*>(c) = make_uint2(pack_bf16(y[0], y[1]), pack_bf16(y[2], y[3]));
-            } else {
-              for (int e = 0; e < 4 && n + e < g.n; ++e) c[e] = f32_to_bf16_bits(y[e]);
-            }
-          }
-        } else {  // G_QKV
-          const int section = n / g.d_model;
-          const int f = n % g.d_model;
-          const int head = f / g.head_dim, dim = f % g.head_dim;
-          const int b = m / g.seq, t = m % g.seq;
-          if (section < 2) {
-            const int half = g.head_dim / 2;
-            const float2 c = *reinterpret_cast<const float2*>(g.cos_t + long(t) * half + dim / 2);
-            const float2 s = *reinterpret_cast<const float2*>(g.sin_t + long(t) * half + dim / 2);
-            const float e0 = y[0], o0 = y[1], e1 = y[2], o1 = y[3];
-            y[0] = e0 * c.x - o0 * s.x;
-            y[1] = e0 * s.x + o0 * c.x;
-            y[2] = e1 * c.y - o1 * s.y;
-            y[3] = e1 * s.y + o1 * c.y;
-          }
-          uint16_t* dst;
-          if (section == 0) {
-            dst = g.q_out + ((long(b) * g.heads + head) * g.seq + t) * g.head_dim + dim;
-          } else {
-            uint16_t* cache = section == 1 ? g.k_cache : g.v_cache;
-            dst = cache + ((long(b) * g.heads + head) * g.cap + t) * g.head_dim + dim;
-          }
-          *reinterpret_cast<uint2*>(dst) = make_uint2(pack_bf16(y[0], y[1]), pack_bf16(y[2], y[3]));
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const f32x4 v = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+          // store_tile's feature index is nt + 4 * grp: grp = 2q + hf.
+          const QkvFeat feat = E == G_QKV ? qkv_feat(g, nt + 8 * q + 4 * hf) : QkvFeat{};
+          store_tile<E>(g, v, nt, 2 * q + hf, m, feat, tok);
         }
       }
     }
@@ -206,6 +427,12 @@ template <int E>
 int launch_gemm(const GemmArgs& g, hipStream_t s, const char* what) {
   if (g.m < 1 || g.n < 1 || g.k < 1) return set_error(SFL_ERR_INVALID, "%s: sizes must be positive", what);
   if (g.k % 8) return set_error(SFL_ERR_UNSUPPORTED, "%s: K must be a multiple of 8", what);
+  if (g.k % K2 == 0 && long(g.m) * g.k < (1L << 30) && long(g.n) * g.k < (1L << 30)) {
+    const long tiles = long((g.n + TB - 1) / TB) * ((g.m + TB - 1) / TB);
+    if (tiles > (1L << 31) - 1) return set_error(SFL_ERR_UNSUPPORTED, "%s: too many tiles", what);
+    hipLaunchKernelGGL((gemm32_kernel<E>), dim3(unsigned(tiles)), dim3(kThreads), 0, s, g);
+    return check_launch(what);
+  }
   dim3 grid((g.n + TN - 1) / TN, (g.m + TM - 1) / TM);
   if (grid.y > 65535) return set_error(SFL_ERR_UNSUPPORTED, "%s: M too large", what);
   hipLaunchKernelGGL((gemm_kernel<E>), grid, dim3(kThreads), 0, s, g);
