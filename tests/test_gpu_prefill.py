@@ -13,7 +13,10 @@ from systems_for_llms_amd.weights import seeded_prompt, seeded_state_dict
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("m,n,k", [(1, 16, 64), (37, 100, 72), (128, 128, 64), (300, 520, 200), (64, 3072, 1024)])
+# K % 64 == 0 takes the 32x32-MFMA kernel (ragged M and N included: rows past
+# the matrices read as zeros, stores are masked); other K the 16x16 kernel.
+@pytest.mark.parametrize("m,n,k", [(1, 16, 64), (37, 100, 72), (128, 128, 64), (300, 520, 200), (64, 3072, 1024),
+                                   (300, 520, 256), (5, 10000, 128), (129, 127, 192), (1000, 36, 2752)])
 def test_gemm_matches_fp32_matmul(m, n, k):
     g = torch.Generator().manual_seed(m + n + k)
     a = torch.randn((m, k), generator=g).bfloat16()
