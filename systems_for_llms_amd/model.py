@@ -162,6 +162,35 @@ class TransformerLM(nn.Module):
                    attention_backend=config.attention_backend,
                    activation_checkpointing=config.activation_checkpointing)
 
+    @classmethod
+    def from_checkpoint(cls, path, device=None, dtype=None) -> "TransformerLM":
+        """The model a reference training checkpoint describes, with its weights.
+
+        Reads the ``checkpoint.pt`` written by ``src/llmlab/train.py:265-275``
+        (``format_version`` 1): the training configuration as a dict under
+        ``"config"``, whose ``"model"`` section gives the shape (``config.py:7-17``),
+        and the module ``state_dict`` under ``"model"``. The file is read with
+        ``torch.load(weights_only=True)``, which executes nothing from it; the
+        optimizer and RNG states it also holds are ignored. Weights are cast to
+        ``dtype`` (default: as stored) and moved to ``device``.
+        """
+        from .config import ModelConfig
+
+        checkpoint = torch.load(path, map_location="cpu", weights_only=True)
+        if not isinstance(checkpoint, dict) or "model" not in checkpoint or "config" not in checkpoint:
+            raise ValueError("checkpoint must hold 'config' and 'model' entries")
+        if checkpoint.get("format_version", 1) != 1:
+            raise ValueError(f"unsupported checkpoint format_version {checkpoint['format_version']}")
+        config = ModelConfig(**checkpoint["config"]["model"])
+        config.validate()
+        state = checkpoint["model"]
+        if dtype is None:
+            dtype = state["lm_head.weight"].dtype
+        model = cls.from_config(config, device="meta", dtype=dtype)
+        model = model.to_empty(device=device or "cpu")
+        model.load_state_dict({k: v.to(dtype) for k, v in state.items()}, strict=True)
+        return model
+
     @property
     def head_dim(self) -> int:
         return self.d_model // self.num_heads

@@ -88,3 +88,47 @@ def test_named_configs_parameter_counts():
     counts = {"pilot-22m-s256": 22_696_448, "scale-100m-s1024": 100_313_856, "scale-324m-s4096": 324_092_928}
     for name, count in counts.items():
         assert load_model_config(name).parameter_count() == count
+
+
+def reference_style_checkpoint(path, cfg, state, dtype=torch.float32):
+    """A file shaped like the one ``src/llmlab/train.py:265-275`` writes."""
+    config_dict = {"model": cfg.to_dict(), "data": {"kind": "synthetic"}, "seed": 1337,
+                   "device": "cuda", "precision": "bf16", "max_steps": 20}
+    optimizer = torch.optim.AdamW([torch.nn.Parameter(torch.zeros(2))]).state_dict()
+    torch.save({"format_version": 1, "config": config_dict, "data_identity": {"kind": "synthetic"},
+                "source_sha256": "0" * 64, "device_type": "cuda", "step": 20,
+                "model": {k: v.to(dtype) for k, v in state.items()}, "optimizer": optimizer,
+                "sampler_rng_state": {"seed": 1}, "torch_rng_state": torch.get_rng_state()}, path)
+
+
+def test_reference_checkpoint_loads(tmp_path):
+    cfg = ModelConfig(vocab_size=64, context_length=16, d_model=32, num_layers=2, num_heads=4, d_ff=64)
+    state = seeded_state_dict(cfg, 11)
+    path = tmp_path / "checkpoint.pt"
+    reference_style_checkpoint(path, cfg, state)
+    model = TransformerLM.from_checkpoint(path)
+    assert (model.vocab_size, model.num_layers, model.d_ff) == (64, 2, 64)
+    for key, value in model.state_dict().items():
+        assert value.dtype == torch.float32
+        assert torch.equal(value, state[key]), key
+    as_bf16 = TransformerLM.from_checkpoint(path, dtype=torch.bfloat16)
+    for key, value in as_bf16.state_dict().items():
+        assert torch.equal(value, state[key].to(torch.bfloat16)), key
+
+
+def test_checkpoint_errors(tmp_path):
+    cfg = ModelConfig(vocab_size=64, context_length=16, d_model=32, num_layers=2, num_heads=4, d_ff=64)
+    state = seeded_state_dict(cfg, 11)
+    path = tmp_path / "checkpoint.pt"
+    torch.save({"model": state}, path)
+    with pytest.raises(ValueError, match="config"):
+        TransformerLM.from_checkpoint(path)
+    truncated = dict(state)
+    truncated.pop("ln_final.weight")
+    reference_style_checkpoint(path, cfg, truncated)
+    with pytest.raises(RuntimeError, match="ln_final.weight"):
+        TransformerLM.from_checkpoint(path)
+    wrong = ModelConfig(vocab_size=64, context_length=16, d_model=32, num_layers=3, num_heads=4, d_ff=64)
+    reference_style_checkpoint(path, wrong, state)
+    with pytest.raises(RuntimeError, match="layers.2"):
+        TransformerLM.from_checkpoint(path)
