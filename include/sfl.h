@@ -79,6 +79,26 @@ int sfl_decode_attention(const void* q, const void* k, const void* v, const int3
                          int splits, float scale, int kv_dtype, int q_dtype, int out_dtype,
                          void* stream);
 
+/*
+ * Decode attention fused with the output projection and residual add:
+ *   x[b] += concat_h(attention(q[b, h], k[b, h], v[b, h])) @ w_out^T
+ * for multi-head attention (Hq == Hkv == heads) with one split. Replaces
+ * attention.py:187-203 (attention, head merge, output_proj) plus the residual
+ * add of transformer.py:46 for one position; the softmax is that of
+ * sfl_decode_attention. Each (batch, head) workgroup adds its head's share of
+ * the projection to x with fp32 atomics, so the summation order varies from
+ * call to call.
+ *   q        [batch, heads, head_dim] fp32 (RoPE applied)
+ *   k, v     [batch, heads, capacity, head_dim] in the model dtype (F32 or BF16)
+ *   lengths  [batch] int32; w_out: output_proj packed by sfl_pack_gemv_weights
+ *   x        fp32 [batch, heads*head_dim], updated in place (16-byte aligned)
+ * head_dim: a power of two in [32, 128] (bf16) or [16, 128] (fp32).
+ */
+int sfl_decode_attention_out_proj(const float* q, const void* k, const void* v,
+                                  const int32_t* lengths, const void* w_out, float* x, int batch,
+                                  int heads, int capacity, int head_dim, float scale, int dtype,
+                                  void* stream);
+
 
 /* ---- decode step of the llmlab decoder (model dtype F32 or BF16) ----------
  * One step processes one token per sequence for `batch` <= 16 sequences per
@@ -92,15 +112,15 @@ int sfl_decode_attention(const void* q, const void* k, const void* v, const int3
  * sfl_packed_gemv_elems(N, K) elements: for each tile of 16 rows and each K
  * chunk (KC = 32 bf16 or 16 fp32 values), 64 lanes x 16 bytes, lane
  * l = 16*g + r holding row r's values [c*KC + g*KC/4, c*KC + (g+1)*KC/4);
- * rows past N are zero. All GEMV inputs are in the activation layout.
+ * rows past N are zero.
  *
- * Normalized GEMV inputs. RMSNorm(x) @ W^T is computed as
- * (x * g) @ W^T / sqrt(sum(x^2) / d_model + 1e-5) (layers.py:133-141), so a
- * normalized consumer takes
- *   act [batch, d_model]      x * g in the activation layout, and
- *   ss  [batch, d_model / 16] fp32 sums of x^2 over each 16-feature tile,
- * written by the producer of x (sfl_linear_residual, sfl_next_token or
- * sfl_norm_act). Normalized consumers need d_model % 64 == 0, d_model <= 2048.
+ * GEMV inputs. A plain input (the attention output, the SwiGLU hidden state)
+ * is in the activation layout. A normalized input is the fp32 residual stream
+ * x [batch, d_model] itself plus the RMSNorm gain g [d_model]: the consumer
+ * computes RMSNorm(x) @ W^T as (x * g) @ W^T / sqrt(sum(x^2) / d_model + 1e-5)
+ * (layers.py:133-141) while it reads x. x and g must be 16-byte aligned.
+ * Producers of x only add to it (sfl_linear_residual,
+ * sfl_decode_attention_out_proj) or overwrite it (sfl_next_token).
  */
 
 /* Elements of a packed [n, k] GEMV weight, and the packing itself (w and
@@ -108,56 +128,52 @@ int sfl_decode_attention(const void* q, const void* k, const void* v, const int3
 long sfl_packed_gemv_elems(int n, int k);
 int sfl_pack_gemv_weights(const void* w, void* packed, int n, int k, int dtype, void* stream);
 
-/* act = x * gain and ss for a fp32 x [batch, d_model] (d_model % 16 == 0). */
-int sfl_norm_act(const float* x, const void* gain, void* act, float* ss, int batch, int d_model,
-                 int dtype, void* stream);
-
 /*
  * q/k/v projections of RMSNorm(x) with RoPE and the KV-cache append.
  * Replaces, for one position, TransformerBlock's attn_norm + q/k/v_proj + RoPE
  * (src/llmlab/model/transformer.py:46, layers.py:133-141,
  * attention.py:160-185); the reference recomputes K/V for every position.
- *   act, ss  the normalized input (attn_norm gain folded into act)
+ *   x, gain  the fp32 residual stream [batch, d_model] and attn_norm's weight
  *   w_qkv    packed [3*d_model, d_model]: q_proj, k_proj, v_proj rows stacked
  *   cos_t, sin_t [capacity, head_dim/2] fp32 (the table of attention.py:31-42)
  *   pos      [batch] int32 position of this token; k/v are written at pos[b]
  *   q_out    [batch, heads, head_dim] fp32; k_cache, v_cache [batch, heads, capacity, head_dim]
  */
-int sfl_rmsnorm_qkv_rope_append(const void* act, const float* ss, const void* w_qkv,
+int sfl_rmsnorm_qkv_rope_append(const float* x, const void* gain, const void* w_qkv,
                                 const float* cos_t, const float* sin_t, const int32_t* pos,
                                 void* q_out, void* k_cache, void* v_cache, int batch,
                                 int d_model, int heads, int capacity, int dtype, void* stream);
 
 /*
- * x_out = x + act @ w^T (act [batch, k] in the activation layout; w packed [n, k];
- * x/x_out fp32 [batch, n], x_out may alias x). Replaces output_proj + residual
+ * x += act @ w^T in place (act [batch, k] in the activation layout; w packed
+ * [n, k]; x fp32 [batch, n], 16-byte aligned). Replaces output_proj + residual
  * and ffn.w2 + residual (transformer.py:46-47, attention.py:199-203,
- * layers.py:114-115). With gain_next (the next RMSNorm's weight, n % 16 == 0)
- * it also writes act_next = x_out * gain_next and ss_next [batch, n/16], the
- * normalized input of the next consumer; gain_next may be NULL.
+ * layers.py:114-115). ksplit in [1, 16] workgroups share each 16-row tile
+ * along K: with ksplit > 1 they add their partial sums to x with fp32 atomics
+ * (more workgroups for small n; the summation order then varies from call to
+ * call); ksplit = 1 is deterministic.
  */
-int sfl_linear_residual(const void* act, const void* w, const float* x, float* x_out,
-                        const void* gain_next, void* act_next, float* ss_next, int batch, int n,
-                        int k, int dtype, void* stream);
+int sfl_linear_residual(const void* act, const void* w, float* x, int batch, int n, int k,
+                        int ksplit, int dtype, void* stream);
 
 /*
  * h = silu(RMSNorm(x) @ w1^T) * (RMSNorm(x) @ w3^T), h [batch, d_ff] in the
- * activation layout. act/ss: the normalized input (ffn_norm gain folded in);
+ * activation layout. x, gain: the residual stream and ffn_norm's weight;
  * w1, w3 packed [d_ff, d_model].
  * Replaces ffn_norm + SwiGLU's w1/w3 half (transformer.py:47, layers.py:73-115).
  */
-int sfl_rmsnorm_swiglu(const void* act, const float* ss, const void* w1, const void* w3,
+int sfl_rmsnorm_swiglu(const float* x, const void* gain, const void* w1, const void* w3,
                        void* h_out, int batch, int d_model, int d_ff, int dtype, void* stream);
 
 /*
  * logits = RMSNorm(x) @ w_head^T plus a per-tile argmax (lowest index on ties).
  * Replaces ln_final + lm_head (transformer.py:137-138) for the last position.
- *   act, ss  the normalized input (ln_final gain folded in); w_head packed [vocab, d_model]
+ *   x, gain  the residual stream and ln_final's weight; w_head packed [vocab, d_model]
  *   logits   optional [.., vocab] fp32; row b is written at
  *            logits + b*logits_batch_stride + pos[b]*logits_pos_stride (pos may be NULL)
  *   best_val, best_idx [sfl_lm_head_tiles(vocab), best_stride]: the tile maxima
  */
-int sfl_rmsnorm_lm_head(const void* act, const float* ss, const void* w_head, void* logits,
+int sfl_rmsnorm_lm_head(const float* x, const void* gain, const void* w_head, void* logits,
                         long logits_batch_stride, const int32_t* pos, long logits_pos_stride,
                         float* best_val, int32_t* best_idx, int best_stride, int batch,
                         int d_model, int vocab, int dtype, void* stream);
@@ -176,15 +192,14 @@ int sfl_embedding_gather(const int64_t* tokens, long token_stride, const int32_t
  * Greedy step: argmax over the lm_head tiles (first maximal index, as
  * torch.argmax), then, with np = pos[b] + 1: predicted[b, np] = argmax;
  * tokens[b, np] = argmax unless np < prompt_len[b] (the prompt token is kept);
- * x[b] = emb[tokens[b, np]] with act[b] = x[b] * gain0 and ss[b] (the first
- * layer's normalized input, d_model % 16 == 0); pos[b] = np; lengths[b] = np + 1.
+ * x[b] = emb[tokens[b, np]] (fp32, d_model % 16 == 0); pos[b] = np; lengths[b] = np + 1.
  * Nothing changes for a row whose np would reach capacity. The reference has
  * no token loop; its greedy continuation is argmax(TransformerLM.forward(ids)[:, -1]).
  */
 int sfl_next_token(const float* best_val, const int32_t* best_idx, int tiles, int64_t* tokens,
                    int64_t* predicted, long token_stride, const int32_t* prompt_len, int32_t* pos,
-                   int32_t* lengths, const void* emb, float* x, const void* gain0, void* act,
-                   float* ss, int batch, int d_model, int capacity, int dtype, void* stream);
+                   int32_t* lengths, const void* emb, float* x, int batch, int d_model,
+                   int capacity, int dtype, void* stream);
 
 /* ---- masked prefill attention ----------------------------------------------
  * Replaces attention_lab/triton_attention.py `attention` (:326-438) and its

@@ -23,16 +23,16 @@ P = c_void_p
 SIGNATURES: dict[str, list] = {
     "sfl_decode_attention": [P, P, P, P, P, P, P, P, c_int, c_int, c_int, c_int, c_int, c_int,
                              c_float, c_int, c_int, c_int, P],
-    "sfl_norm_act": [P, P, P, P, c_int, c_int, c_int, P],
+    "sfl_decode_attention_out_proj": [P, P, P, P, P, P, c_int, c_int, c_int, c_int, c_float, c_int, P],
     "sfl_packed_gemv_elems": [c_int, c_int],
     "sfl_pack_gemv_weights": [P, P, c_int, c_int, c_int, P],
     "sfl_rmsnorm_qkv_rope_append": [P, P, P, P, P, P, P, P, P, c_int, c_int, c_int, c_int, c_int, P],
-    "sfl_linear_residual": [P, P, P, P, P, P, P, c_int, c_int, c_int, c_int, P],
+    "sfl_linear_residual": [P, P, P, c_int, c_int, c_int, c_int, c_int, P],
     "sfl_rmsnorm_swiglu": [P, P, P, P, P, c_int, c_int, c_int, c_int, P],
     "sfl_rmsnorm_lm_head": [P, P, P, P, c_long, P, c_long, P, P, c_int, c_int, c_int, c_int, c_int, P],
     "sfl_lm_head_tiles": [c_int],
     "sfl_embedding_gather": [P, c_long, P, P, P, c_int, c_int, c_int, P],
-    "sfl_next_token": [P, P, c_int, P, P, c_long, P, P, P, P, P, P, P, P, c_int, c_int, c_int, c_int, P],
+    "sfl_next_token": [P, P, c_int, P, P, c_long, P, P, P, P, P, c_int, c_int, c_int, c_int, P],
     "sfl_masked_attention": [P, P, P, P, P, c_int, c_int, c_int, c_int, POINTER(c_long), POINTER(c_long),
                              POINTER(c_long), POINTER(c_long), c_float, c_int, c_int, c_int, c_int, P,
                              c_int, P, P, P, c_int, c_int, P],

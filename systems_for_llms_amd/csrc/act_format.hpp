@@ -1,4 +1,4 @@
-// Activation operand format and layout of the decode GEMVs, and its producers.
+// Activation operand format and layout of the decode GEMVs.
 //
 // Values, 4 bytes per element in both model dtypes:
 //   fp32 weights: fp32 values;
@@ -11,22 +11,10 @@
 // bytes at lane * 16 (bf16: the hi halves; the lo halves follow 1 KB later).
 // A chunk is 1 KB (fp32) or 2 KB (bf16) of contiguous memory, so every GEMV
 // load instruction reads whole cache lines.
-// A normalized consumer (RMSNorm folded into the GEMV) reads x * g in this
-// format plus the sums of x^2 over each 16-feature tile of x.
 #pragma once
 #include "common.hpp"
 
 namespace sfl {
-
-// Four consecutive RMSNorm gains as fp32 (one 8- or 16-byte load).
-template <typename T> __device__ __forceinline__ float4 load_gain4(const T* p);
-template <> __device__ __forceinline__ float4 load_gain4<float>(const float* p) {
-  return *reinterpret_cast<const float4*>(p);
-}
-template <> __device__ __forceinline__ float4 load_gain4<bf16_t>(const bf16_t* p) {
-  const uint2 w = *reinterpret_cast<const uint2*>(p);
-  return make_float4(bf16_lo(w.x), bf16_hi(w.x), bf16_lo(w.y), bf16_hi(w.y));
-}
 
 // Chunk geometry: one 16-byte lane load covers vec_elems<T>() values, a chunk
 // covers 4 lane groups.
@@ -77,27 +65,6 @@ __device__ __forceinline__ void store_act4<bf16_t>(unsigned char* act, int b, in
   unsigned char* g = act + act_offset<bf16_t>(b, e, K);
   *reinterpret_cast<uint2*>(g) = make_uint2((hb[0] >> 16) | hb[1], (hb[2] >> 16) | hb[3]);
   *reinterpret_cast<uint2*>(g + kActLoOffset) = make_uint2((lb[0] >> 16) | lb[1], (lb[2] >> 16) | lb[3]);
-}
-
-// One tile of 16 features of row b: optionally store x, then store x * g in the
-// activation format and the tile's sum of squares.
-template <typename T>
-__device__ __forceinline__ void emit_tile(const float* v, const T* gain, int t, float* x_row,
-                                          unsigned char* act, int b, int K, float* ss_row) {
-  if (x_row) {
-#pragma unroll
-    for (int i = 0; i < 16; i += 4)
-      *reinterpret_cast<float4*>(x_row + 16 * t + i) = make_float4(v[i], v[i + 1], v[i + 2], v[i + 3]);
-  }
-  float sq = 0.f;
-#pragma unroll
-  for (int i = 0; i < 16; i += 4) {
-    const float4 g = load_gain4<T>(gain + 16 * t + i);
-    const float gx[4] = {v[i] * g.x, v[i + 1] * g.y, v[i + 2] * g.z, v[i + 3] * g.w};
-    store_act4<T>(act, b, 16 * t + i, K, gx);
-    sq = fmaf(v[i], v[i], fmaf(v[i + 1], v[i + 1], fmaf(v[i + 2], v[i + 2], fmaf(v[i + 3], v[i + 3], sq))));
-  }
-  ss_row[t] = sq;
 }
 
 }  // namespace sfl

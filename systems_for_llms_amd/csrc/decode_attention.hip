@@ -20,9 +20,11 @@ namespace sfl {
 namespace {
 
 // Tag types of the outputs in the decode GEMVs' activation layout (act_format.hpp):
-// split-bf16 values (BF16X2) and fp32 values (F32X).
+// split-bf16 values (BF16X2) and fp32 values (F32X); and of the fused output
+// projection, x[b] += attention(b) . W_o^T, accumulated into x with atomics.
 struct split_t {};
 struct f32x_t {};
+struct resid_t {};
 
 template <typename T, int D, int G>
 struct DecodeShape {
@@ -38,21 +40,45 @@ struct DecodeShape {
 template <typename TO>
 __device__ __forceinline__ void store_out(void* out, long f, int K, float v);
 
+// Fused output projection (TO = resid_t, one split): the packed W_o of the
+// decode GEMVs (decode_linear.hip: 1 KB per 16 rows x one K chunk) is read for
+// this kv head's G*D columns, in rounds of kProjRound 16-byte loads per lane.
+constexpr int kProjRound = 8;
+
+template <typename T, int D, int G>
+struct ProjShape {
+  static constexpr int KC = 4 * vec_elems<T>();  // K values per packed chunk
+  // Chunks per kv head (a power of two; the host admits G*D % KC == 0 only).
+  static constexpr int NCK = G * D >= KC ? G * D / KC : 1;
+};
+
+// Unit u of a wave's share: tile wave + (u / NCK) * W, chunk h * NCK + u % NCK.
+template <typename T, int D, int G, int W>
+__device__ __forceinline__ uint4 load_proj_unit(const unsigned char* w_lane, int u, int wave, int h,
+                                                int nchunks_all) {
+  using P = ProjShape<T, D, G>;
+  const long tile = wave + (u / P::NCK) * W;
+  const long c = long(h) * P::NCK + u % P::NCK;
+  return load16(w_lane + (tile * nchunks_all + c) * kWave * 16);
+}
+
 // One workgroup of W waves per (batch, kv head, split). The split's keys are
 // divided among the waves; each wave streams its range with the per-slot
 // online softmax, the slots are merged with shuffles, and the W wave states
 // are merged through LDS. With one split the workgroup writes the final
-// output; otherwise it writes its (max, sum, numerator) partial for the merge
-// kernel.
+// output (or, fused, adds its heads' share of the output projection to x);
+// otherwise it writes its (max, sum, numerator) partial for the merge kernel.
 template <typename T, typename TQ, typename TO, int D, int G, int W>
 __global__ __launch_bounds__(W * kWave) void decode_attn_kernel(
     const TQ* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
     const int32_t* __restrict__ lengths, float* __restrict__ pmax, float* __restrict__ psum,
     float* __restrict__ pout, void* __restrict__ out, int kv_heads, int cap, int splits, int chunk,
-    float qscale) {
+    float qscale, float* __restrict__ x, int d_model) {
   using S = DecodeShape<T, D, G>;
   constexpr int EPL = S::EPL, LPT = S::LPT, TPL = S::TPL, NL = S::NL, TILE = S::TILE;
+  constexpr bool kProj = std::is_same<TO, resid_t>::value;
   __shared__ float sm[W][G][D + 2];
+  __shared__ float os[kProj ? G * D : 1];
   const int wave = threadIdx.x / kWave;
   const int lane = threadIdx.x % kWave;
   const int split = int(blockIdx.x % splits);
@@ -159,6 +185,19 @@ __global__ __launch_bounds__(W * kWave) void decode_attn_kernel(
     }
   }
 
+  // Fused projection: issue the first round of W_o loads now, so they land
+  // while the softmax states are merged. `out` is the packed W_o.
+  const unsigned char* w_lane = static_cast<const unsigned char*>(out) + lane * 16;
+  const int proj_tiles = d_model / 16;
+  const int proj_units = kProj ? max(0, (proj_tiles - wave + W - 1) / W) * ProjShape<T, D, G>::NCK : 0;
+  uint4 wr[kProj ? kProjRound : 1];
+  if constexpr (kProj) {
+#pragma unroll
+    for (int j = 0; j < kProjRound; ++j)
+      if (proj_units > 0)
+        wr[j] = load_proj_unit<T, D, G, W>(w_lane, min(j, proj_units - 1), wave, h, d_model / ProjShape<T, D, G>::KC);
+  }
+
   // Merge the slots' online-softmax states: xor over the slot bits of the lane id.
 #pragma unroll
   for (int mask = LPT; mask < kWave; mask <<= 1) {
@@ -209,7 +248,9 @@ __global__ __launch_bounds__(W * kWave) void decode_attn_kernel(
       }
     }
     const long qrow = long(b) * q_heads + h * G + g;
-    if (splits == 1) {
+    if constexpr (kProj) {
+      os[t] = den > 0.f ? num / den : 0.f;
+    } else if (splits == 1) {
       store_out<TO>(out, qrow * D + d, q_heads * D, den > 0.f ? num / den : 0.f);
     } else {
       const long prow = qrow * splits + split;
@@ -217,6 +258,43 @@ __global__ __launch_bounds__(W * kWave) void decode_attn_kernel(
       if (d == 0) {
         pmax[prow] = top;
         psum[prow] = den;
+      }
+    }
+  }
+  if constexpr (kProj) {
+    // x[b, n] += sum_c W_o[n, c] o[c] over this kv head's columns c: each
+    // lane takes a 16-byte piece of W_o (row n = tile*16 + lane%16, columns
+    // of its lane group), the 4 groups are added with shuffles and lanes 0..15
+    // add their row's value to x (16 kv heads add to each element).
+    using P = ProjShape<T, D, G>;
+    constexpr int EW = vec_elems<T>();
+    __syncthreads();
+    const int grp = lane / 16;
+    float* xb = x + long(b) * d_model;
+    float part = 0.f;
+    for (int r0 = 0; r0 < proj_units; r0 += kProjRound) {
+      if (r0 > 0) {
+#pragma unroll
+        for (int j = 0; j < kProjRound; ++j)
+          wr[j] = load_proj_unit<T, D, G, W>(w_lane, min(r0 + j, proj_units - 1), wave, h, d_model / P::KC);
+      }
+#pragma unroll
+      for (int j = 0; j < kProjRound; ++j) {
+        const int u = r0 + j;
+        if (u < proj_units) {  // uniform over the wave
+          float wv[EW];
+          unpack16<T>(wr[j], wv);
+          const float* op = os + (u % P::NCK) * P::KC + grp * EW;
+#pragma unroll
+          for (int e = 0; e < EW; ++e) part = fmaf(wv[e], op[e], part);
+          if (u % P::NCK == P::NCK - 1) {
+            part += __shfl_xor(part, 16, kWave);
+            part += __shfl_xor(part, 32, kWave);
+            const int tile = wave + (u / P::NCK) * W;
+            if (lane < 16) unsafeAtomicAdd(xb + tile * 16 + lane, part);
+            part = 0.f;
+          }
+        }
       }
     }
   }
@@ -326,6 +404,8 @@ struct DecodeCall {
   int batch, q_heads, kv_heads, cap, dim, splits;
   float scale;
   hipStream_t stream;
+  float* x;     // fused projection: residual stream [batch, d_model]
+  int d_model;
 };
 
 // Waves per workgroup: as many as keep the kernel within the register budget
@@ -342,7 +422,7 @@ int launch_attn(const DecodeCall& c) {
   hipLaunchKernelGGL((decode_attn_kernel<T, TQ, TO, D, G, W>), dim3(unsigned(groups)), dim3(W * kWave), 0,
                      c.stream, static_cast<const TQ*>(c.q), static_cast<const T*>(c.k),
                      static_cast<const T*>(c.v), c.lengths, c.pmax, c.psum, c.pout, c.out, c.kv_heads,
-                     c.cap, c.splits, chunk, c.scale * kLog2e);
+                     c.cap, c.splits, chunk, c.scale * kLog2e, c.x, c.d_model);
   return check_launch("decode_attention");
 }
 
@@ -392,8 +472,49 @@ int attn_out(const DecodeCall& c, int out_dtype) {
   }
 }
 
+template <typename T, int D>
+int launch_proj(const DecodeCall& c) {
+  return launch_attn<T, float, resid_t, D, 1>(c);
+}
+
+template <typename T>
+int proj_dims(const DecodeCall& c) {
+  switch (c.dim) {
+    case 16: if constexpr (sizeof(T) == 4) return launch_proj<T, 16>(c); else break;
+    case 32: return launch_proj<T, 32>(c);
+    case 64: return launch_proj<T, 64>(c);
+    case 128: return launch_proj<T, 128>(c);
+  }
+  return set_error(SFL_ERR_UNSUPPORTED, "decode_attention_out_proj: unsupported head dim %d", c.dim);
+}
+
 }  // namespace
 }  // namespace sfl
+
+extern "C" int sfl_decode_attention_out_proj(const float* q, const void* k, const void* v,
+                                             const int32_t* lengths, const void* w_out, float* x,
+                                             int batch, int heads, int capacity, int head_dim,
+                                             float scale, int dtype, void* stream) {
+  using namespace sfl;
+  const char* what = "decode_attention_out_proj";
+  if (!q || !k || !v || !lengths || !w_out || !x) return set_error(SFL_ERR_INVALID, "%s: null pointer argument", what);
+  if (batch <= 0 || heads <= 0 || capacity <= 0)
+    return set_error(SFL_ERR_INVALID, "%s: batch, heads and capacity must be positive", what);
+  if (!(scale > 0.f) || !__builtin_isfinite(scale))
+    return set_error(SFL_ERR_INVALID, "%s: scale must be finite and positive", what);
+  if (dtype != SFL_DTYPE_F32 && dtype != SFL_DTYPE_BF16)
+    return set_error(SFL_ERR_UNSUPPORTED, "%s: model dtype must be F32 or BF16", what);
+  const int kc = dtype == SFL_DTYPE_BF16 ? 32 : 16;
+  if (head_dim % kc || head_dim > 128 || (head_dim & (head_dim - 1)))
+    return set_error(SFL_ERR_UNSUPPORTED, "%s: head dim %d must be a power of two in [%d, 128]", what, head_dim, kc);
+  if (reinterpret_cast<uintptr_t>(x) % 16 || reinterpret_cast<uintptr_t>(w_out) % 16)
+    return set_error(SFL_ERR_INVALID, "%s: x and w_out must be 16-byte aligned", what);
+  DecodeCall c{q, k, v, lengths, nullptr, nullptr, nullptr, const_cast<void*>(w_out), batch, heads,
+               heads, capacity, head_dim, 1, scale, static_cast<hipStream_t>(stream)};
+  c.x = x;
+  c.d_model = heads * head_dim;
+  return dtype == SFL_DTYPE_BF16 ? proj_dims<bf16_t>(c) : proj_dims<float>(c);
+}
 
 extern "C" int sfl_decode_attention(const void* q, const void* k, const void* v,
                                     const int32_t* lengths, float* partial_max,

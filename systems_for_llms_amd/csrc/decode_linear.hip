@@ -19,19 +19,20 @@
 // MFMAs (the GEMV is bandwidth-bound, so the second MFMA is free), which keeps
 // ~16 mantissa bits of the activation instead of 8.
 //
-// RMSNorm is deferred (layers.py:133-141): RMSNorm(x) W^T = (1/rms(x)) *
-// ((x * g) W^T). The kernel that produces x (a residual epilogue, or the
-// token step) also writes the next consumer's input x * g in the activation
-// format and the per-16-feature partial sums of x^2; the consumer reads its
-// K chunks of x * g straight from global memory (each wave needs only its own
-// chunks, so nothing is staged in LDS) and scales its sums by
-// 1 / sqrt(sum(x^2) / K + eps), adding the partials in a fixed order.
+// RMSNorm is folded into its consumers (layers.py:133-141): RMSNorm(x) W^T =
+// (1/rms(x)) * ((x * g) W^T). The residual stream x stays a plain fp32 [B, K]
+// tensor; a normalized consumer (q/k/v, w1/w3, lm_head) reads its K chunks of
+// x and the gain g, forms x * g in the MFMA operand format as it goes, adds up
+// x^2 on the side, and scales its sums by 1 / sqrt(sum(x^2) / K + eps) once
+// the waves' partials are reduced (in a fixed order, so every workgroup
+// computes the same scale). Producers of x therefore only add to it, which
+// lets them split K over several workgroups and accumulate with atomics.
 // Epilogues:
 //   QKV      RoPE on q and k (attention.py:44-58) with the host-built fp32
 //            table; q to an fp32 [B, H, dk] buffer, k/v appended to the
 //            model-dtype [B, H, cap, dk] cache at each row's position.
-//   RESIDUAL x += W act (transformer.py:46-47), then x * g_next and the
-//            partial sums of x^2 for the next normalized consumer.
+//   RESIDUAL x += W act (transformer.py:46-47), in place; with K split over
+//            several workgroups each adds its partial with fp32 atomics.
 //   SWIGLU   h = silu(W1 act) * (W3 act) in fp32 (layers.py:114-115).
 //   LOGITS   lm_head rows (transformer.py:137-138) plus a per-tile argmax with
 //            the lowest index winning ties, taken on the fp32 accumulators.
@@ -48,16 +49,17 @@ enum Epi { EPI_QKV = 0, EPI_RESIDUAL = 1, EPI_SWIGLU = 2, EPI_LOGITS = 3 };
 constexpr int kWaves = 8;       // waves per workgroup (K split)
 constexpr int kTileN = 16;      // output features per workgroup
 constexpr int kMaxRows = 16;    // batch rows per launch
-constexpr int kMaxSsTiles = 128; // 16-feature tiles of a normalized input: d_model <= 2048
 constexpr float kEps = 1e-5f;
+constexpr int kMaxSplitK = 16;  // workgroups per tile along K (RESIDUAL)
 
 struct LinearArgs {
-  const void* act;       // [B, K] activation format (x * g for normalized consumers)
-  const float* ss;       // [B, K/16] partial sums of x^2 (normalized consumers), else nullptr
-  int ss_vec4;           // ss rows load as float4 (K % 256 == 0, 16-byte aligned)
+  const void* act;       // RESIDUAL: [B, K] input in the activation format
+  const float* x_in;     // normalized consumers: the fp32 residual stream [B, K]
+  const void* gain;      // and its RMSNorm gain [K] (model dtype)
   const void* w;         // packed [ceil(N/16)][K/chunk][64 lanes][16 B]
   const void* w3;        // packed second matrix of SWIGLU
   int batch, n, k;
+  int ksplit;            // workgroups per 16-row tile along K (1 except RESIDUAL)
   // QKV
   const float* cos_t;    // [ctx, dk/2] fp32
   const float* sin_t;
@@ -67,11 +69,7 @@ struct LinearArgs {
   void* v_cache;
   int heads, head_dim, cap, d_model;
   // RESIDUAL
-  const float* x;        // fp32 residual [B, N]
-  float* x_out;          // [B, N] (may alias x)
-  const void* gain_next; // optional [N] gain of the next normalized consumer
-  void* act_next;        // its input x_out * gain_next, [B, N] activation format
-  float* ss_next;        // its partial sums of x_out^2, [B, N/16]
+  float* x;              // fp32 residual [B, N], updated in place
   // SWIGLU
   void* h_out;           // [B, N] in the activation format
   // LOGITS
@@ -154,81 +152,128 @@ __device__ __forceinline__ f32x4 mfma_act<float>(const uint4& w, const ActChunk<
   return mfma_chunk<float>(w, b, acc);
 }
 
-// CPW: weight chunks each wave loads per round (one round when K/chunk_k <= kWaves*CPW);
-// chosen on the host from K so no wave issues more loads than it needs.
+// A normalized consumer's source: one lane's fp32 values of x for a chunk and
+// the matching gains (bf16 weights: 8 values, fp32: 4).
+template <typename T> struct NormChunk;
+template <> struct NormChunk<bf16_t> { float4 x0, x1; uint4 g; };
+template <> struct NormChunk<float> { float4 x; float4 g; };
+
+template <typename T>
+__device__ __forceinline__ NormChunk<T> load_norm(const float* x, const T* g);
+template <>
+__device__ __forceinline__ NormChunk<bf16_t> load_norm<bf16_t>(const float* x, const bf16_t* g) {
+  return {*reinterpret_cast<const float4*>(x), *reinterpret_cast<const float4*>(x + 4), load16(g)};
+}
+template <>
+__device__ __forceinline__ NormChunk<float> load_norm<float>(const float* x, const float* g) {
+  return {*reinterpret_cast<const float4*>(x), *reinterpret_cast<const float4*>(g)};
+}
+
+// x * g in the MFMA operand format (for bf16 weights split into hi + lo bf16
+// halves, as act_format.hpp defines), adding the lane's x^2 to ss.
+template <typename T>
+__device__ __forceinline__ ActChunk<T> norm_operand(const NormChunk<T>& s, float& ss);
+template <>
+__device__ __forceinline__ ActChunk<bf16_t> norm_operand<bf16_t>(const NormChunk<bf16_t>& s, float& ss) {
+  const float x[8] = {s.x0.x, s.x0.y, s.x0.z, s.x0.w, s.x1.x, s.x1.y, s.x1.z, s.x1.w};
+  const uint32_t gw[4] = {s.g.x, s.g.y, s.g.z, s.g.w};
+  uint32_t hb[8], lb[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    ss = fmaf(x[i], x[i], ss);
+    const float v = x[i] * ((i & 1) ? bf16_hi(gw[i / 2]) : bf16_lo(gw[i / 2]));
+    hb[i] = __float_as_uint(v) & 0xffff0000u;
+    lb[i] = __float_as_uint(v - __uint_as_float(hb[i])) & 0xffff0000u;
+  }
+  ActChunk<bf16_t> r;
+  r.hi = make_uint4((hb[0] >> 16) | hb[1], (hb[2] >> 16) | hb[3], (hb[4] >> 16) | hb[5], (hb[6] >> 16) | hb[7]);
+  r.lo = make_uint4((lb[0] >> 16) | lb[1], (lb[2] >> 16) | lb[3], (lb[4] >> 16) | lb[5], (lb[6] >> 16) | lb[7]);
+  return r;
+}
+template <>
+__device__ __forceinline__ ActChunk<float> norm_operand<float>(const NormChunk<float>& s, float& ss) {
+  ss = fmaf(s.x.x, s.x.x, ss);
+  ss = fmaf(s.x.y, s.x.y, ss);
+  ss = fmaf(s.x.z, s.x.z, ss);
+  ss = fmaf(s.x.w, s.x.w, ss);
+  ActChunk<float> r;
+  r.v = make_uint4(__float_as_uint(s.x.x * s.g.x), __float_as_uint(s.x.y * s.g.y),
+                   __float_as_uint(s.x.z * s.g.z), __float_as_uint(s.x.w * s.g.w));
+  return r;
+}
+
+template <bool kNorm, typename T> struct SrcOf { using type = ActChunk<T>; };
+template <typename T> struct SrcOf<true, T> { using type = NormChunk<T>; };
+
+// CPW: weight chunks each wave loads per round (one round when the workgroup's
+// chunks fit kWaves*CPW); chosen on the host so no wave issues more loads than
+// it needs. Workgroup blockIdx.x owns tile blockIdx.x % tiles and the K part
+// blockIdx.x / tiles (one part unless RESIDUAL splits K).
 template <typename T, int E, int CPW>
 __global__ __launch_bounds__(kWaves * kWave) void linear_kernel(LinearArgs a) {
-  constexpr int kChunkGroup = CPW;
   constexpr int KC = chunk_k<T>();
+  constexpr int EPL = vec_elems<T>();
   constexpr bool kTwo = (E == EPI_SWIGLU);
-  __shared__ float red[kWaves * kWave * (kTwo ? 8 : 4)];
+  constexpr bool kNorm = (E != EPI_RESIDUAL);
+  constexpr int RS = (kTwo ? 8 : 4) + (kNorm ? 1 : 0);  // floats per lane in the cross-wave reduction
+  using Src = typename SrcOf<kNorm, T>::type;
+  __shared__ float red[kWaves * kWave * RS];
   const int tid = threadIdx.x;
   const int wave = tid / kWave;
   const int lane = tid % kWave;
   const int K = a.k;
 
   constexpr int CB = act_chunk_bytes<T>();
-  const int n0 = blockIdx.x * kTileN;
+  const int tiles = (a.n + kTileN - 1) / kTileN;
+  const int tile = int(blockIdx.x % unsigned(tiles));
+  const int part = int(blockIdx.x / unsigned(tiles));
+  const int n0 = tile * kTileN;
   const int grp = lane / 16;
   const int b = lane % 16;
   const int nchunks = K / KC;
-  // This lane's 16 bytes of chunk c: w + c*1KB, act + c*CB (packed layouts).
-  const unsigned char* wl = static_cast<const unsigned char*>(a.w) + (long(blockIdx.x) * nchunks * kWave + lane) * 16;
+  const int per = (nchunks + a.ksplit - 1) / a.ksplit;
+  const int cb = part * per;
+  const int ce = min(nchunks, cb + per);
+  if (cb >= ce) return;  // an empty K part (whole workgroup)
+  // This lane's 16 bytes of chunk c: w + c*1KB (packed weights); its B operand
+  // from act + c*CB (activation format) or from row b of x and the gain.
+  const unsigned char* wl = static_cast<const unsigned char*>(a.w) + (long(tile) * nchunks * kWave + lane) * 16;
   const unsigned char* w3l =
-      kTwo ? static_cast<const unsigned char*>(a.w3) + (long(blockIdx.x) * nchunks * kWave + lane) * 16 : nullptr;
-  const unsigned char* al = static_cast<const unsigned char*>(a.act) + lane * 16;
+      kTwo ? static_cast<const unsigned char*>(a.w3) + (long(tile) * nchunks * kWave + lane) * 16 : nullptr;
   const bool live = b < a.batch;
+  const int row = min(b, a.batch - 1);
+  const unsigned char* al = kNorm ? nullptr : static_cast<const unsigned char*>(a.act) + lane * 16;
+  const float* xl = kNorm ? a.x_in + long(row) * K + grp * EPL : nullptr;
+  const T* gl = kNorm ? static_cast<const T*>(a.gain) + grp * EPL : nullptr;
 
-  // Issue the first group of weight and activation loads up front. Loads are
+  // Issue the first group of weight and operand loads up front. Loads are
   // unconditional, from clamped addresses, and masked where they are used: a
   // load whose value is consumed inside its own guard makes the compiler wait
   // for it on the spot, serialising the memory round trips.
-  uint4 wa[kChunkGroup], wb[kTwo ? kChunkGroup : 1];
-  ActChunk<T> af[kChunkGroup];
-  int c0 = wave;
-  const int last = nchunks - 1;
+  uint4 wa[CPW], wb[kTwo ? CPW : 1];
+  Src src[CPW];
+  int c0 = cb + wave;
+  const int last = ce - 1;
 #pragma unroll
-  for (int j = 0; j < kChunkGroup; ++j) {
+  for (int j = 0; j < CPW; ++j) {
     const long c = min(c0 + j * kWaves, last);
     wa[j] = load16(wl + c * kWave * 16);
     if constexpr (kTwo) wb[j] = load16(w3l + c * kWave * 16);
-    af[j] = load_act<T>(al + c * CB);
+    if constexpr (kNorm) src[j] = load_norm<T>(xl + c * KC, gl + c * KC);
+    else src[j] = load_act<T>(al + c * CB);
   }
 
   // Prefetch what wave 0's epilogue reads, so it overlaps the weight loads.
   const int n = n0 + 4 * grp;  // this lane's features n .. n+3 of batch row b
-  float4 pre_x = make_float4(0.f, 0.f, 0.f, 0.f), pre_g = make_float4(0.f, 0.f, 0.f, 0.f);
+  const int nl = min(n, a.n - 4);
+  float4 pre_x = make_float4(0.f, 0.f, 0.f, 0.f);
   float2 pre_c = make_float2(0.f, 0.f), pre_s = make_float2(0.f, 0.f);
   int pre_p = 0;
-  float ssum = 0.f;  // this lane's share of sum(x^2) of row b (normalized consumers)
-  const int ntiles = K / 16;
-  const int nl = min(n, a.n - 4);
   if (wave == 0) {
-    if (a.ss) {
-      const float* sr = a.ss + long(min(b, a.batch - 1)) * ntiles;
-      const int per = ntiles / 4;  // tiles summed by each of the 4 lanes of row b
-      if (a.ss_vec4) {  // per % 4 == 0 and 16-byte aligned rows: float4 loads
-        const float4* s4 = reinterpret_cast<const float4*>(sr + grp * per);
-        float4 part[kMaxSsTiles / 16];
-#pragma unroll
-        for (int t = 0; t < kMaxSsTiles / 16; ++t) part[t] = s4[min(t, per / 4 - 1)];
-#pragma unroll
-        for (int t = 0; t < kMaxSsTiles / 16; ++t)
-          if (t < per / 4) ssum += (part[t].x + part[t].y) + (part[t].z + part[t].w);
-      } else {
-        float part[kMaxSsTiles / 4];
-#pragma unroll
-        for (int t = 0; t < kMaxSsTiles / 4; ++t) part[t] = sr[grp * per + min(t, per - 1)];
-#pragma unroll
-        for (int t = 0; t < kMaxSsTiles / 4; ++t)
-          if (t < per) ssum += part[t];
-      }
-    }
     if constexpr (E == EPI_RESIDUAL) {
-      pre_x = *reinterpret_cast<const float4*>(a.x + long(min(b, a.batch - 1)) * a.n + nl);
-      if (a.gain_next) pre_g = load_gain4<T>(static_cast<const T*>(a.gain_next) + nl);
+      if (a.ksplit == 1) pre_x = *reinterpret_cast<const float4*>(a.x + long(row) * a.n + nl);
     } else if constexpr (E == EPI_QKV) {
-      pre_p = a.pos[min(b, a.batch - 1)];
+      pre_p = a.pos[row];
       const int half = a.head_dim / 2;
       const long at = long(pre_p) * half + (nl % a.d_model % a.head_dim) / 2;
       pre_c = *reinterpret_cast<const float2*>(a.cos_t + at);
@@ -238,49 +283,57 @@ __global__ __launch_bounds__(kWaves * kWave) void linear_kernel(LinearArgs a) {
 
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   f32x4 acc3 = {0.f, 0.f, 0.f, 0.f};
+  float ssum = 0.f;  // this lane's share of sum(x^2) of row b (normalized consumers)
   for (;;) {
 #pragma unroll
-    for (int j = 0; j < kChunkGroup; ++j) {
+    for (int j = 0; j < CPW; ++j) {
       const int c = c0 + j * kWaves;
-      if (c < nchunks) {
-        acc = mfma_act<T>(wa[j], af[j], live, acc);
-        if constexpr (kTwo) acc3 = mfma_act<T>(wb[j], af[j], live, acc3);
+      if (c < ce) {
+        ActChunk<T> op;
+        if constexpr (kNorm) op = norm_operand<T>(src[j], ssum);
+        else op = src[j];
+        acc = mfma_act<T>(wa[j], op, live, acc);
+        if constexpr (kTwo) acc3 = mfma_act<T>(wb[j], op, live, acc3);
       }
     }
-    c0 += kChunkGroup * kWaves;
-    if (c0 >= nchunks) break;
+    c0 += CPW * kWaves;
+    if (c0 >= ce) break;
 #pragma unroll
-    for (int j = 0; j < kChunkGroup; ++j) {
+    for (int j = 0; j < CPW; ++j) {
       const long c = min(c0 + j * kWaves, last);
       wa[j] = load16(wl + c * kWave * 16);
       if constexpr (kTwo) wb[j] = load16(w3l + c * kWave * 16);
-      af[j] = load_act<T>(al + c * CB);
+      if constexpr (kNorm) src[j] = load_norm<T>(xl + c * KC, gl + c * KC);
+      else src[j] = load_act<T>(al + c * CB);
     }
   }
 
-  // Sum the waves' partial tiles.
-  float* mine = red + (wave * kWave + lane) * (kTwo ? 8 : 4);
+  // Sum the waves' partial tiles (and partial sums of x^2).
+  float* mine = red + (wave * kWave + lane) * RS;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     mine[i] = acc[i];
     if constexpr (kTwo) mine[4 + i] = acc3[i];
   }
+  if constexpr (kNorm) mine[RS - 1] = ssum;
   __syncthreads();
   if (wave != 0) return;
   float v1[4] = {0.f, 0.f, 0.f, 0.f}, v3[4] = {0.f, 0.f, 0.f, 0.f};
+  float sq = 0.f;
   for (int w = 0; w < kWaves; ++w) {
-    const float* p = red + (w * kWave + lane) * (kTwo ? 8 : 4);
+    const float* p = red + (w * kWave + lane) * RS;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       v1[i] += p[i];
       if constexpr (kTwo) v3[i] += p[4 + i];
     }
+    if constexpr (kNorm) sq += p[RS - 1];
   }
-  if (a.ss) {
-    // sum(x^2) over the row in a fixed order: lane partials, then lane groups.
-    ssum += __shfl_xor(ssum, 16, kWave);
-    ssum += __shfl_xor(ssum, 32, kWave);
-    const float inv = 1.f / sqrtf(ssum / float(K) + kEps);
+  if constexpr (kNorm) {
+    // Lane (row b, group g) holds group g's sum over all of K: add the 4 groups.
+    sq += __shfl_xor(sq, 16, kWave);
+    sq += __shfl_xor(sq, 32, kWave);
+    const float inv = 1.f / sqrtf(sq / float(K) + kEps);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       v1[i] *= inv;
@@ -304,8 +357,8 @@ __global__ __launch_bounds__(kWaves * kWave) void linear_kernel(LinearArgs a) {
     }
     if (live) {
       if (grp == 0) {
-        a.best_val[long(blockIdx.x) * a.best_stride + b] = bv;
-        a.best_idx[long(blockIdx.x) * a.best_stride + b] = bi;
+        a.best_val[long(tile) * a.best_stride + b] = bv;
+        a.best_idx[long(tile) * a.best_stride + b] = bi;
       }
       if (a.logits && n < a.n) {
         float* dst = static_cast<float*>(a.logits) + b * a.logits_batch_stride + n;
@@ -317,25 +370,16 @@ __global__ __launch_bounds__(kWaves * kWave) void linear_kernel(LinearArgs a) {
     }
     return;
   }
-  if constexpr (E == EPI_RESIDUAL) {
-    const float xo[4] = {pre_x.x + v1[0], pre_x.y + v1[1], pre_x.z + v1[2], pre_x.w + v1[3]};
-    if (a.gain_next) {
-      // Partial sum of x^2 over this workgroup's 16 features (4 lanes of row b).
-      float sq = xo[0] * xo[0] + xo[1] * xo[1] + xo[2] * xo[2] + xo[3] * xo[3];
-      sq += __shfl_xor(sq, 16, kWave);
-      sq += __shfl_xor(sq, 32, kWave);
-      if (live && n < a.n) {
-        const float gx[4] = {xo[0] * pre_g.x, xo[1] * pre_g.y, xo[2] * pre_g.z, xo[3] * pre_g.w};
-        store_act4<T>(static_cast<unsigned char*>(a.act_next), b, n, a.n, gx);
-        if (grp == 0) a.ss_next[long(b) * (a.n / 16) + blockIdx.x] = sq;
-      }
-    }
-    if (live && n < a.n)
-      *reinterpret_cast<float4*>(a.x_out + long(b) * a.n + n) = make_float4(xo[0], xo[1], xo[2], xo[3]);
-    return;
-  }
   if (!live || n >= a.n) return;
-  if constexpr (E == EPI_SWIGLU) {
+  if constexpr (E == EPI_RESIDUAL) {
+    float* dst = a.x + long(b) * a.n + n;
+    if (a.ksplit == 1) {
+      *reinterpret_cast<float4*>(dst) = make_float4(pre_x.x + v1[0], pre_x.y + v1[1], pre_x.z + v1[2], pre_x.w + v1[3]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) unsafeAtomicAdd(dst + i, v1[i]);
+    }
+  } else if constexpr (E == EPI_SWIGLU) {
     float h[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) h[i] = v1[i] / (1.f + expf(-v1[i])) * v3[i];
@@ -370,13 +414,15 @@ __global__ __launch_bounds__(kWaves * kWave) void linear_kernel(LinearArgs a) {
 template <typename T, int E, int CPW>
 int launch_linear_cpw(const LinearArgs& a, hipStream_t stream, const char* what) {
   const unsigned tiles = unsigned((a.n + kTileN - 1) / kTileN);
-  hipLaunchKernelGGL((linear_kernel<T, E, CPW>), dim3(tiles), dim3(kWaves * kWave), 0, stream, a);
+  hipLaunchKernelGGL((linear_kernel<T, E, CPW>), dim3(tiles * unsigned(a.ksplit)), dim3(kWaves * kWave), 0,
+                     stream, a);
   return check_launch(what);
 }
 
 template <typename T, int E>
 int launch_linear(const LinearArgs& a, hipStream_t stream, const char* what) {
-  const int per_wave = (a.k / chunk_k<T>() + kWaves - 1) / kWaves;
+  const int per_part = (a.k / chunk_k<T>() + a.ksplit - 1) / a.ksplit;
+  const int per_wave = (per_part + kWaves - 1) / kWaves;
   if (per_wave <= 1) return launch_linear_cpw<T, E, 1>(a, stream, what);
   if (per_wave <= 2) return launch_linear_cpw<T, E, 2>(a, stream, what);
   if (per_wave <= 4) return launch_linear_cpw<T, E, 4>(a, stream, what);
@@ -398,17 +444,16 @@ int check_common(const char* what, int batch, int n, int k, int dtype, bool vec4
   return SFL_OK;
 }
 
-// Normalized inputs: K/16 tiles of partial sums, split evenly over 4 lanes.
-int check_normed(const char* what, int k) {
-  if (k % 64 || k / 16 > kMaxSsTiles)
-    return set_error(SFL_ERR_UNSUPPORTED, "%s: normalized inputs need d_model %% 64 == 0 and <= %d", what,
-                     kMaxSsTiles * 16);
+// Normalized inputs: x rows are read as float4 (16-byte aligned rows).
+int check_normed(const char* what, const float* x, const void* gain) {
+  if (reinterpret_cast<uintptr_t>(x) % 16 || reinterpret_cast<uintptr_t>(gain) % 16)
+    return set_error(SFL_ERR_INVALID, "%s: x and gain must be 16-byte aligned", what);
   return SFL_OK;
 }
 
 template <int E>
 int dispatch_linear(LinearArgs a, int dtype, hipStream_t s, const char* what) {
-  a.ss_vec4 = a.ss && a.k % 256 == 0 && reinterpret_cast<uintptr_t>(a.ss) % 16 == 0;
+  if (a.ksplit < 1) a.ksplit = 1;
   if (dtype == SFL_DTYPE_BF16) return launch_linear<bf16_t, E>(a, s, what);
   return launch_linear<float, E>(a, s, what);
 }
@@ -432,111 +477,78 @@ __global__ __launch_bounds__(256) void pack_weights_kernel(const T* __restrict__
   }
 }
 
-// act = x * g and the per-tile sums of x^2 for a normalized consumer, from x.
-template <typename T>
-__global__ __launch_bounds__(64) void norm_act_kernel(const float* x, const T* gain, unsigned char* act,
-                                                      float* ss, int d) {
-  const int b = blockIdx.x;
-  const float* xr = x + long(b) * d;
-  for (int t = threadIdx.x; t < d / 16; t += kWave) {
-    float v[16];
-#pragma unroll
-    for (int i = 0; i < 16; i += 4) {
-      const float4 q = *reinterpret_cast<const float4*>(xr + 16 * t + i);
-      v[i] = q.x; v[i + 1] = q.y; v[i + 2] = q.z; v[i + 3] = q.w;
-    }
-    emit_tile<T>(v, gain, t, nullptr, act, b, d, ss + long(b) * (d / 16));
-  }
-}
-
 }  // namespace
 }  // namespace sfl
 
 using namespace sfl;
 
-extern "C" int sfl_rmsnorm_qkv_rope_append(const void* act, const float* ss, const void* w_qkv,
+extern "C" int sfl_rmsnorm_qkv_rope_append(const float* x, const void* gain, const void* w_qkv,
                                            const float* cos_t, const float* sin_t,
                                            const int32_t* pos, void* q_out, void* k_cache,
                                            void* v_cache, int batch, int d_model, int heads,
                                            int capacity, int dtype, void* stream) {
   const char* what = "rmsnorm_qkv_rope_append";
-  if (!act || !ss || !w_qkv || !cos_t || !sin_t || !pos || !q_out || !k_cache || !v_cache)
+  if (!x || !gain || !w_qkv || !cos_t || !sin_t || !pos || !q_out || !k_cache || !v_cache)
     return set_error(SFL_ERR_INVALID, "%s: null pointer argument", what);
   if (heads < 1 || d_model % heads) return set_error(SFL_ERR_INVALID, "%s: d_model must be divisible by heads", what);
   const int dk = d_model / heads;
   if (dk % 16) return set_error(SFL_ERR_UNSUPPORTED, "%s: head dim must be a multiple of 16", what);
   if (capacity < 1) return set_error(SFL_ERR_INVALID, "%s: capacity must be positive", what);
   if (int rc = check_common(what, batch, 3 * d_model, d_model, dtype)) return rc;
-  if (int rc = check_normed(what, d_model)) return rc;
+  if (int rc = check_normed(what, x, gain)) return rc;
   LinearArgs a{};
-  a.act = act; a.ss = ss; a.w = w_qkv; a.batch = batch; a.n = 3 * d_model; a.k = d_model;
+  a.x_in = x; a.gain = gain; a.w = w_qkv; a.batch = batch; a.n = 3 * d_model; a.k = d_model;
   a.cos_t = cos_t; a.sin_t = sin_t; a.pos = pos; a.q_out = q_out; a.k_cache = k_cache;
   a.v_cache = v_cache; a.heads = heads; a.head_dim = dk; a.cap = capacity; a.d_model = d_model;
   return dispatch_linear<EPI_QKV>(a, dtype, static_cast<hipStream_t>(stream), what);
 }
 
-extern "C" int sfl_linear_residual(const void* act, const void* w, const float* x, float* x_out,
-                                   const void* gain_next, void* act_next, float* ss_next, int batch,
-                                   int n, int k, int dtype, void* stream) {
+extern "C" int sfl_linear_residual(const void* act, const void* w, float* x, int batch, int n, int k,
+                                   int ksplit, int dtype, void* stream) {
   const char* what = "linear_residual";
-  if (!act || !w || !x || !x_out) return set_error(SFL_ERR_INVALID, "%s: null pointer argument", what);
-  if (gain_next && (!act_next || !ss_next))
-    return set_error(SFL_ERR_INVALID, "%s: gain_next needs act_next and ss_next", what);
+  if (!act || !w || !x) return set_error(SFL_ERR_INVALID, "%s: null pointer argument", what);
   if (int rc = check_common(what, batch, n, k, dtype)) return rc;
-  if (gain_next && n % 16) return set_error(SFL_ERR_UNSUPPORTED, "%s: N must be a multiple of 16", what);
+  if (ksplit < 1 || ksplit > kMaxSplitK)
+    return set_error(SFL_ERR_INVALID, "%s: ksplit must be in [1, %d]", what, kMaxSplitK);
+  if (reinterpret_cast<uintptr_t>(x) % 16) return set_error(SFL_ERR_INVALID, "%s: x must be 16-byte aligned", what);
   LinearArgs a{};
-  a.act = act; a.w = w; a.x = x; a.x_out = x_out; a.batch = batch; a.n = n; a.k = k;
-  a.gain_next = gain_next; a.act_next = act_next; a.ss_next = ss_next;
+  a.act = act; a.w = w; a.x = x; a.batch = batch; a.n = n; a.k = k; a.ksplit = ksplit;
   return dispatch_linear<EPI_RESIDUAL>(a, dtype, static_cast<hipStream_t>(stream), what);
 }
 
-extern "C" int sfl_rmsnorm_swiglu(const void* act, const float* ss, const void* w1, const void* w3,
+extern "C" int sfl_rmsnorm_swiglu(const float* x, const void* gain, const void* w1, const void* w3,
                                   void* h_out, int batch, int d_model, int d_ff, int dtype,
                                   void* stream) {
   const char* what = "rmsnorm_swiglu";
-  if (!act || !ss || !w1 || !w3 || !h_out) return set_error(SFL_ERR_INVALID, "%s: null pointer argument", what);
+  if (!x || !gain || !w1 || !w3 || !h_out) return set_error(SFL_ERR_INVALID, "%s: null pointer argument", what);
   if (int rc = check_common(what, batch, d_ff, d_model, dtype)) return rc;
-  if (int rc = check_normed(what, d_model)) return rc;
+  if (int rc = check_normed(what, x, gain)) return rc;
+  const int kc = dtype == SFL_DTYPE_BF16 ? chunk_k<bf16_t>() : chunk_k<float>();
+  if (d_ff % kc)  // h is written in the activation layout, whole chunks per row
+    return set_error(SFL_ERR_UNSUPPORTED, "%s: d_ff=%d must be a multiple of %d", what, d_ff, kc);
   LinearArgs a{};
-  a.act = act; a.ss = ss; a.w = w1; a.w3 = w3; a.h_out = h_out; a.batch = batch; a.n = d_ff;
+  a.x_in = x; a.gain = gain; a.w = w1; a.w3 = w3; a.h_out = h_out; a.batch = batch; a.n = d_ff;
   a.k = d_model;
   return dispatch_linear<EPI_SWIGLU>(a, dtype, static_cast<hipStream_t>(stream), what);
 }
 
-extern "C" int sfl_rmsnorm_lm_head(const void* act, const float* ss, const void* w_head,
+extern "C" int sfl_rmsnorm_lm_head(const float* x, const void* gain, const void* w_head,
                                    void* logits, long logits_batch_stride, const int32_t* pos,
                                    long logits_pos_stride, float* best_val, int32_t* best_idx,
                                    int best_stride, int batch, int d_model, int vocab, int dtype,
                                    void* stream) {
   const char* what = "rmsnorm_lm_head";
-  if (!act || !ss || !w_head || !best_val || !best_idx)
+  if (!x || !gain || !w_head || !best_val || !best_idx)
     return set_error(SFL_ERR_INVALID, "%s: null pointer argument", what);
   if (int rc = check_common(what, batch, vocab, d_model, dtype, false)) return rc;
-  if (int rc = check_normed(what, d_model)) return rc;
+  if (int rc = check_normed(what, x, gain)) return rc;
   if (best_stride < batch) return set_error(SFL_ERR_INVALID, "%s: best_stride must be >= batch", what);
   LinearArgs a{};
-  a.act = act; a.ss = ss; a.w = w_head; a.logits = logits; a.logits_batch_stride = logits_batch_stride;
+  a.x_in = x; a.gain = gain; a.w = w_head; a.logits = logits; a.logits_batch_stride = logits_batch_stride;
   a.pos = pos; a.logits_pos_stride = logits_pos_stride; a.best_val = best_val; a.best_idx = best_idx;
   a.best_stride = best_stride;
   a.batch = batch; a.n = vocab; a.k = d_model;
   return dispatch_linear<EPI_LOGITS>(a, dtype, static_cast<hipStream_t>(stream), what);
-}
-
-extern "C" int sfl_norm_act(const float* x, const void* gain, void* act, float* ss, int batch, int d_model,
-                            int dtype, void* stream) {
-  const char* what = "norm_act";
-  if (!x || !gain || !act || !ss) return set_error(SFL_ERR_INVALID, "%s: null pointer argument", what);
-  if (batch < 1 || d_model < 16 || d_model % 16) return set_error(SFL_ERR_INVALID, "%s: d_model must be a multiple of 16", what);
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  if (dtype == SFL_DTYPE_BF16)
-    hipLaunchKernelGGL(norm_act_kernel<bf16_t>, dim3(batch), dim3(64), 0, s, x, static_cast<const bf16_t*>(gain),
-                       static_cast<unsigned char*>(act), ss, d_model);
-  else if (dtype == SFL_DTYPE_F32)
-    hipLaunchKernelGGL(norm_act_kernel<float>, dim3(batch), dim3(64), 0, s, x, static_cast<const float*>(gain),
-                       static_cast<unsigned char*>(act), ss, d_model);
-  else
-    return set_error(SFL_ERR_UNSUPPORTED, "%s: model dtype must be F32 or BF16", what);
-  return check_launch(what);
 }
 
 extern "C" int sfl_lm_head_tiles(int vocab) { return (vocab + kTileN - 1) / kTileN; }

@@ -30,15 +30,13 @@ __global__ __launch_bounds__(256) void embed_kernel(const int64_t* __restrict__ 
 // One wave per sequence: finish the argmax over the lm_head tiles (lowest
 // index on ties), record it, pick the next token (the given one while the
 // sequence is still inside its prompt, else the argmax), gather its
-// embedding into x, write the first layer's normalized-consumer input
-// (x * gain0 and the per-16-feature sums of x^2) and advance pos/lengths.
+// embedding into x (fp32) and advance pos/lengths.
 template <typename T>
 __global__ __launch_bounds__(64) void next_token_kernel(
     const float* __restrict__ best_val, const int32_t* __restrict__ best_idx, int tiles, int batch,
     int64_t* __restrict__ tokens, int64_t* __restrict__ predicted, long stride,
     const int32_t* __restrict__ prompt_len, int32_t* __restrict__ pos, int32_t* __restrict__ lengths,
-    const T* __restrict__ emb, float* __restrict__ x, const T* __restrict__ gain0,
-    unsigned char* __restrict__ act, float* __restrict__ ss, int d, int cap) {
+    const T* __restrict__ emb, float* __restrict__ x, int d, int cap) {
   const int b = blockIdx.x;
   const int lane = threadIdx.x;
   const int p = pos[b];
@@ -73,6 +71,7 @@ __global__ __launch_bounds__(64) void next_token_kernel(
   const long tok = forced ? given : long(bi);
   const T* src = emb + tok * d;
   constexpr int V = vec_elems<T>();
+  float* xr = x + long(b) * d;
   for (int t = lane; t < d / 16; t += kWave) {  // one 16-feature tile per lane per round
     uint4 r[16 / V];
 #pragma unroll
@@ -80,7 +79,9 @@ __global__ __launch_bounds__(64) void next_token_kernel(
     float v[16];
 #pragma unroll
     for (int j = 0; j < 16 / V; ++j) unpack16<T>(r[j], v + j * V);
-    emit_tile<T>(v, gain0, t, x + long(b) * d, act, b, d, ss + long(b) * (d / 16));
+#pragma unroll
+    for (int i = 0; i < 16; i += 4)
+      *reinterpret_cast<float4*>(xr + 16 * t + i) = make_float4(v[i], v[i + 1], v[i + 2], v[i + 3]);
   }
   if (lane == 0) {
     predicted[b * stride + np] = bi;
@@ -115,10 +116,9 @@ extern "C" int sfl_embedding_gather(const int64_t* tokens, long token_stride, co
 extern "C" int sfl_next_token(const float* best_val, const int32_t* best_idx, int tiles,
                               int64_t* tokens, int64_t* predicted, long token_stride,
                               const int32_t* prompt_len, int32_t* pos, int32_t* lengths,
-                              const void* emb, float* x, const void* gain0, void* act, float* ss,
-                              int batch, int d_model, int capacity, int dtype, void* stream) {
-  if (!best_val || !best_idx || !tokens || !predicted || !prompt_len || !pos || !lengths || !emb || !x ||
-      !gain0 || !act || !ss)
+                              const void* emb, float* x, int batch, int d_model, int capacity,
+                              int dtype, void* stream) {
+  if (!best_val || !best_idx || !tokens || !predicted || !prompt_len || !pos || !lengths || !emb || !x)
     return set_error(SFL_ERR_INVALID, "next_token: null pointer argument");
   if (batch < 1 || tiles < 1 || d_model < 1 || capacity < 1)
     return set_error(SFL_ERR_INVALID, "next_token: sizes must be positive");
@@ -129,13 +129,11 @@ extern "C" int sfl_next_token(const float* best_val, const int32_t* best_idx, in
   if (dtype == SFL_DTYPE_BF16)
     hipLaunchKernelGGL(next_token_kernel<bf16_t>, dim3(batch), dim3(64), 0, s, best_val, best_idx, tiles,
                        batch, tokens, predicted, token_stride, prompt_len, pos, lengths,
-                       static_cast<const bf16_t*>(emb), x, static_cast<const bf16_t*>(gain0),
-                       static_cast<unsigned char*>(act), ss, d_model, capacity);
+                       static_cast<const bf16_t*>(emb), x, d_model, capacity);
   else if (dtype == SFL_DTYPE_F32)
     hipLaunchKernelGGL(next_token_kernel<float>, dim3(batch), dim3(64), 0, s, best_val, best_idx, tiles,
                        batch, tokens, predicted, token_stride, prompt_len, pos, lengths,
-                       static_cast<const float*>(emb), x, static_cast<const float*>(gain0),
-                       static_cast<unsigned char*>(act), ss, d_model, capacity);
+                       static_cast<const float*>(emb), x, d_model, capacity);
   else
     return set_error(SFL_ERR_UNSUPPORTED, "next_token: model dtype must be F32 or BF16");
   return check_launch("next_token");

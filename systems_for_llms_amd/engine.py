@@ -5,15 +5,18 @@ the KV cache ``[L, B, H, cap, dk]`` in the model dtype, the fp32 residual
 stream, scratch, and the token/position/length state -- and issues one step as
 a fixed sequence of C-ABI launches on the current stream:
 
-    per layer:  rmsnorm_qkv_rope_append -> decode_attention (split-KV + merge)
-                -> linear_residual (output_proj) -> rmsnorm_swiglu
-                -> linear_residual (w2)
+    per layer:  rmsnorm_qkv_rope_append -> decode_attention_out_proj
+                -> rmsnorm_swiglu -> linear_residual (w2)
     then:       rmsnorm_lm_head (+ tile argmax) -> next_token
 
-RMSNorm is folded into its consumer: whichever launch produces x (a residual
-GEMV or next_token) also writes ``act = x * g`` for the next norm's gain ``g``
-and the per-16-feature sums of x^2 (``ss``); the consumer scales its sums by
-the inverse RMS.
+With more than one KV split the attention and output_proj run as
+decode_attention (split-KV + merge) and linear_residual instead.
+
+RMSNorm is folded into its consumer: x stays a plain fp32 tensor, and the
+q/k/v, w1/w3 and lm_head GEMVs read it with their norm's gain, forming x * g
+and the sum of x^2 as they go. The producers of x only add to it, so the
+output projection is accumulated by the attention workgroups and w2 is split
+along K over several workgroups, both with fp32 atomics.
 
 All step state lives in device memory and is advanced by ``next_token``, so a
 step has no host inputs: it is captured once into a HIP graph and replayed.
@@ -35,6 +38,15 @@ from .decode import auto_splits
 ROWS_PER_LAUNCH = 16  # batch rows per decode-step GEMV launch
 
 
+def residual_ksplit(n: int, target_groups: int = 256) -> int:
+    """Workgroups per 16-row tile along K for a residual GEMV with ``n`` outputs.
+
+    ``n / 16`` tiles cover few of the 256 CUs at these model widths (64 at
+    d_model 1024); the K parts add their partial sums into x with atomics.
+    """
+    return max(1, min(16, target_groups // max(1, n // 16)))
+
+
 class DecodeSession:
     def __init__(self, model, batch: int, capacity: int | None = None, *, splits: int | None = None,
                  record_logits: bool = False):
@@ -47,8 +59,8 @@ class DecodeSession:
         cap = capacity or model.context_length
         if not 0 < cap <= model.context_length:
             raise ValueError("capacity must be in [1, context_length]")
-        if model.d_model % 64 or model.d_model > 2048:
-            raise ValueError("the decode step needs d_model % 64 == 0 and d_model <= 2048")
+        if model.d_model % 32 or model.d_ff % 32:
+            raise ValueError("the decode step needs d_model and d_ff to be multiples of 32")
         self.model = model
         self.device = param.device
         self.dtype = param.dtype
@@ -80,14 +92,12 @@ class DecodeSession:
         # fp32 for fp32 models, the split-bf16 (hi, lo) format for bf16 models.
         self.q = torch.zeros((batch, h, self.dk), device=dev, dtype=torch.float32)
         # GEMV inputs in the activation layout: whole blocks of 16 rows, 4 bytes per
-        # value (viewed here as fp32 words): the attention output, the SwiGLU hidden
-        # state, and x * g for the next RMSNorm consumer with the sums of x^2 over
-        # each 16-feature tile (ss).
+        # value (viewed here as fp32 words): the attention output (only when the
+        # attention is not fused with output_proj) and the SwiGLU hidden state.
+        # The normalized consumers read x itself with their RMSNorm gain.
         blocks = -(-batch // ROWS_PER_LAUNCH)
         self.attn = torch.zeros((blocks, ROWS_PER_LAUNCH * d), device=dev, dtype=torch.float32)
         self.hidden = torch.zeros((blocks, ROWS_PER_LAUNCH * f), device=dev, dtype=torch.float32)
-        self.act = torch.zeros((blocks, ROWS_PER_LAUNCH * d), device=dev, dtype=torch.float32)
-        self.ss = torch.zeros((batch, d // 16), device=dev, dtype=torch.float32)
         self.act_code = _lib.DTYPE_BF16X2 if dt == torch.bfloat16 else _lib.DTYPE_F32X
         self.splits = splits or auto_splits(batch, h, cap)
         self.pmax = torch.empty((batch, h, self.splits), device=dev, dtype=torch.float32)
@@ -103,6 +113,9 @@ class DecodeSession:
         self.prompt_len = torch.ones(batch, device=dev, dtype=torch.int32)
         self.logits = (torch.zeros((batch, cap, v), device=dev, dtype=torch.float32)
                        if record_logits else None)
+        # One split: the attention kernel also applies output_proj and adds it to x.
+        self.fused_out_proj = self.splits == 1 and self.dk % (32 if dt == torch.bfloat16 else 16) == 0 \
+            and self.dk <= 128 and self.dk & (self.dk - 1) == 0
         self.graph = None
         self._calls = self._plan()
 
@@ -116,42 +129,46 @@ class DecodeSession:
         scale = float(dk) ** -0.5
         row_chunks = [(r, min(ROWS_PER_LAUNCH, self.batch - r)) for r in range(0, self.batch, ROWS_PER_LAUNCH)]
         self._row_chunks = row_chunks
-        gains = [blk.attn_norm.weight for blk in m.layers[1:]] + [m.ln_final.weight]
         for layer, blk in enumerate(m.layers):
             kc, vc = self.k_cache[layer], self.v_cache[layer]
             for r, rows in row_chunks:
                 calls.append((lib.sfl_rmsnorm_qkv_rope_append, (
-                    self.act[r // ROWS_PER_LAUNCH].data_ptr(), self.ss[r].data_ptr(), self.p_qkv[layer].data_ptr(),
+                    self.x[r].data_ptr(), blk.attn_norm.weight.data_ptr(), self.p_qkv[layer].data_ptr(),
                     self.cos.data_ptr(), self.sin.data_ptr(), self.pos[r:].data_ptr(),
                     self.q[r].data_ptr(), kc[r].data_ptr(), vc[r].data_ptr(), rows, d, h, cap, code)))
-            calls.append((lib.sfl_decode_attention, (
-                self.q.data_ptr(), kc.data_ptr(), vc.data_ptr(), self.lengths.data_ptr(),
-                self.pmax.data_ptr(), self.psum.data_ptr(), self.pout.data_ptr(), self.attn.data_ptr(),
-                self.batch, h, h, cap, dk, self.splits, scale, code, _lib.DTYPE_CODES[torch.float32],
-                self.act_code)))
+            if self.fused_out_proj:
+                calls.append((lib.sfl_decode_attention_out_proj, (
+                    self.q.data_ptr(), kc.data_ptr(), vc.data_ptr(), self.lengths.data_ptr(),
+                    self.p_out[layer].data_ptr(), self.x.data_ptr(), self.batch, h, cap, dk, scale, code)))
+            else:
+                calls.append((lib.sfl_decode_attention, (
+                    self.q.data_ptr(), kc.data_ptr(), vc.data_ptr(), self.lengths.data_ptr(),
+                    self.pmax.data_ptr(), self.psum.data_ptr(), self.pout.data_ptr(), self.attn.data_ptr(),
+                    self.batch, h, h, cap, dk, self.splits, scale, code, _lib.DTYPE_CODES[torch.float32],
+                    self.act_code)))
             for r, rows in row_chunks:
                 j = r // ROWS_PER_LAUNCH
-                x, act, ss = self.x[r].data_ptr(), self.act[j].data_ptr(), self.ss[r].data_ptr()
-                calls.append((lib.sfl_linear_residual, (
-                    self.attn[j].data_ptr(), self.p_out[layer].data_ptr(), x, x,
-                    blk.ffn_norm.weight.data_ptr(), act, ss, rows, d, d, code)))
+                x = self.x[r].data_ptr()
+                if not self.fused_out_proj:
+                    calls.append((lib.sfl_linear_residual, (
+                        self.attn[j].data_ptr(), self.p_out[layer].data_ptr(), x, rows, d, d,
+                        residual_ksplit(d), code)))
                 calls.append((lib.sfl_rmsnorm_swiglu, (
-                    act, ss, self.p_w1[layer].data_ptr(), self.p_w3[layer].data_ptr(),
+                    x, blk.ffn_norm.weight.data_ptr(), self.p_w1[layer].data_ptr(), self.p_w3[layer].data_ptr(),
                     self.hidden[j].data_ptr(), rows, d, f, code)))
                 calls.append((lib.sfl_linear_residual, (
-                    self.hidden[j].data_ptr(), self.p_w2[layer].data_ptr(), x, x,
-                    gains[layer].data_ptr(), act, ss, rows, d, f, code)))
+                    self.hidden[j].data_ptr(), self.p_w2[layer].data_ptr(), x, rows, d, f,
+                    residual_ksplit(d), code)))
         for r, rows in row_chunks:
             logits = self.logits[r].data_ptr() if self.logits is not None else None
             calls.append((lib.sfl_rmsnorm_lm_head, (
-                self.act[r // ROWS_PER_LAUNCH].data_ptr(), self.ss[r].data_ptr(), self.p_head.data_ptr(),
+                self.x[r].data_ptr(), m.ln_final.weight.data_ptr(), self.p_head.data_ptr(),
                 logits, cap * v, self.pos[r:].data_ptr(), v, self.best_val[:, r:].data_ptr(),
                 self.best_idx[:, r:].data_ptr(), self.batch, rows, d, v, code)))
         calls.append((lib.sfl_next_token, (
             self.best_val.data_ptr(), self.best_idx.data_ptr(), self.tiles, self.tokens.data_ptr(),
             self.predicted.data_ptr(), cap, self.prompt_len.data_ptr(), self.pos.data_ptr(),
             self.lengths.data_ptr(), m.token_embeddings.weight.data_ptr(), self.x.data_ptr(),
-            m.layers[0].attn_norm.weight.data_ptr(), self.act.data_ptr(), self.ss.data_ptr(),
             self.batch, d, cap, code)))
         return calls
 
@@ -177,16 +194,11 @@ class DecodeSession:
         self._embed_current()
 
     def _embed_current(self) -> None:
-        """x = embedding of each row's token at pos, plus the first layer's normalized input."""
+        """x = embedding of each row's token at pos."""
         stream = _lib.stream_handle(self.device)
         _lib.call("sfl_embedding_gather", self.tokens.data_ptr(), self.cap, self.pos.data_ptr(),
                   self.model.token_embeddings.weight.data_ptr(), self.x.data_ptr(), self.batch,
                   self.d, self.code, stream)
-        self._norm_input(self.model.layers[0].attn_norm.weight, stream)
-
-    def _norm_input(self, gain, stream) -> None:
-        _lib.call("sfl_norm_act", self.x.data_ptr(), gain.data_ptr(), self.act.data_ptr(), self.ss.data_ptr(),
-                  self.batch, self.d, self.code, stream)
 
     # -- prefill ------------------------------------------------------------
     def _prefill_weights(self):
@@ -264,7 +276,6 @@ class DecodeSession:
             logits = logits.view(b, t, v)
         # Hand the last position to the decode head: pick token T and advance.
         self.x.copy_(x.view(b, t, d)[:, t - 1])
-        self._norm_input(self.model.ln_final.weight, st)
         self.pos.fill_(t - 1)
         self.lengths.fill_(t)
         for fn, args in self._calls[-(len(self._row_chunks) + 1):]:

@@ -70,6 +70,21 @@ def test_config1_fp32_greedy_sequence_identical(golden):
         assert torch.equal(ids, expected), f"graph={use_graph} first mismatch {mismatch[:1].tolist()}"
 
 
+def test_config1_from_reference_checkpoint_greedy_identical(golden, tmp_path):
+    """A reference-format training checkpoint loads into the GPU model and decodes the golden ids."""
+    from test_model_api import reference_style_checkpoint
+
+    meta, arrays = golden
+    c1 = meta["c1"]
+    cfg = load_model_config("pilot-22m-s256")
+    path = tmp_path / "checkpoint.pt"
+    reference_style_checkpoint(path, cfg, seeded_state_dict(cfg, c1["seed"]))
+    model = TransformerLM.from_checkpoint(path, device="cuda").eval()
+    prompt = seeded_prompt(cfg.vocab_size, 1, c1["prompt_length"], c1["prompt_seed"]).cuda()
+    ids = model.generate(prompt, c1["steps"]).cpu()
+    assert torch.equal(ids, torch.from_numpy(arrays["c1_ids"]))
+
+
 def bf16_gate(name, got, ref, floor, targets=None):
     """Judge bf16 logits against the fp32 reference and against the bf16-storage floor.
 
