@@ -246,10 +246,16 @@ __global__ __launch_bounds__(kWaves * kWave) void linear_kernel(LinearArgs a) {
   const float* xl = kNorm ? a.x_in + long(row) * K + grp * EPL : nullptr;
   const T* gl = kNorm ? static_cast<const T*>(a.gain) + grp * EPL : nullptr;
 
-  // Issue the first group of weight and operand loads up front. Loads are
+  // Issue the first group of operand and weight loads up front. Loads are
   // unconditional, from clamped addresses, and masked where they are used: a
   // load whose value is consumed inside its own guard makes the compiler wait
-  // for it on the spot, serialising the memory round trips.
+  // for it on the spot, serialising the memory round trips. The operand loads
+  // (cache hits) go first, so a normalized consumer forms x * g while the
+  // weights are still on their way from HBM.
+  // QKV: load the position before anything else; the RoPE table loads of the
+  // epilogue depend on it and are issued right after the weight loads.
+  int pre_p = 0;
+  if constexpr (E == EPI_QKV) pre_p = a.pos[row];
   uint4 wa[CPW], wb[kTwo ? CPW : 1];
   Src src[CPW];
   int c0 = cb + wave;
@@ -257,10 +263,15 @@ __global__ __launch_bounds__(kWaves * kWave) void linear_kernel(LinearArgs a) {
 #pragma unroll
   for (int j = 0; j < CPW; ++j) {
     const long c = min(c0 + j * kWaves, last);
-    wa[j] = load16(wl + c * kWave * 16);
-    if constexpr (kTwo) wb[j] = load16(w3l + c * kWave * 16);
     if constexpr (kNorm) src[j] = load_norm<T>(xl + c * KC, gl + c * KC);
     else src[j] = load_act<T>(al + c * CB);
+  }
+  __builtin_amdgcn_sched_barrier(0);  // keep the operand loads ahead of the weight loads
+#pragma unroll
+  for (int j = 0; j < CPW; ++j) {
+    const long c = min(c0 + j * kWaves, last);
+    wa[j] = load16(wl + c * kWave * 16);
+    if constexpr (kTwo) wb[j] = load16(w3l + c * kWave * 16);
   }
 
   // Prefetch what wave 0's epilogue reads, so it overlaps the weight loads.
@@ -268,12 +279,10 @@ __global__ __launch_bounds__(kWaves * kWave) void linear_kernel(LinearArgs a) {
   const int nl = min(n, a.n - 4);
   float4 pre_x = make_float4(0.f, 0.f, 0.f, 0.f);
   float2 pre_c = make_float2(0.f, 0.f), pre_s = make_float2(0.f, 0.f);
-  int pre_p = 0;
   if (wave == 0) {
     if constexpr (E == EPI_RESIDUAL) {
       if (a.ksplit == 1) pre_x = *reinterpret_cast<const float4*>(a.x + long(row) * a.n + nl);
     } else if constexpr (E == EPI_QKV) {
-      pre_p = a.pos[row];
       const int half = a.head_dim / 2;
       const long at = long(pre_p) * half + (nl % a.d_model % a.head_dim) / 2;
       pre_c = *reinterpret_cast<const float2*>(a.cos_t + at);
@@ -285,26 +294,42 @@ __global__ __launch_bounds__(kWaves * kWave) void linear_kernel(LinearArgs a) {
   f32x4 acc3 = {0.f, 0.f, 0.f, 0.f};
   float ssum = 0.f;  // this lane's share of sum(x^2) of row b (normalized consumers)
   for (;;) {
+    // Operands first (they do not wait for the weights), then the MFMAs. Both
+    // are unconditional, with chunks past the part masked to zero, so no load
+    // is sunk into a branch behind the others.
+    ActChunk<T> op[CPW];
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int j = 0; j < CPW; ++j) {
-      const int c = c0 + j * kWaves;
-      if (c < ce) {
-        ActChunk<T> op;
-        if constexpr (kNorm) op = norm_operand<T>(src[j], ssum);
-        else op = src[j];
-        acc = mfma_act<T>(wa[j], op, live, acc);
-        if constexpr (kTwo) acc3 = mfma_act<T>(wb[j], op, live, acc3);
+      if constexpr (kNorm) {
+        float part = 0.f;
+        op[j] = norm_operand<T>(src[j], part);
+        ssum += (c0 + j * kWaves < ce) ? part : 0.f;
+      } else {
+        op[j] = src[j];
       }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < CPW; ++j) {
+      const bool use = live && c0 + j * kWaves < ce;
+      acc = mfma_act<T>(wa[j], op[j], use, acc);
+      if constexpr (kTwo) acc3 = mfma_act<T>(wb[j], op[j], use, acc3);
     }
     c0 += CPW * kWaves;
     if (c0 >= ce) break;
 #pragma unroll
     for (int j = 0; j < CPW; ++j) {
       const long c = min(c0 + j * kWaves, last);
-      wa[j] = load16(wl + c * kWave * 16);
-      if constexpr (kTwo) wb[j] = load16(w3l + c * kWave * 16);
       if constexpr (kNorm) src[j] = load_norm<T>(xl + c * KC, gl + c * KC);
       else src[j] = load_act<T>(al + c * CB);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < CPW; ++j) {
+      const long c = min(c0 + j * kWaves, last);
+      wa[j] = load16(wl + c * kWave * 16);
+      if constexpr (kTwo) wb[j] = load16(w3l + c * kWave * 16);
     }
   }
 
