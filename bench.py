@@ -11,9 +11,11 @@ steps always cover positions 3072 .. 3072+K-1 (attention lengths 3073 ..
 3072+K); the default K = 1023 generates tokens 3073 .. 4095.
 
 Printed JSON (one line): decode tok/s; ``roofline`` for the dominant kernel,
-split-KV decode attention, timed with HIP events on its launch stream at the
-mean decode context of the timed region, rotating over the 24 layers' caches so
-that every call streams from HBM as it does inside the decode loop; ``prefill``
+decode attention fused with the output projection (the model path's kernel),
+timed with HIP events on its launch stream at the mean decode context of the
+timed region, rotating over the 24 layers' caches so that every call streams
+from HBM as it does inside the decode loop; ``decode_attention_operator``: the
+same measurement for the standalone split-KV attention operator; ``prefill``
 (the prompt pass, MFMA TFLOP/s against the bf16 dense peak);
 ``decode_attention_config4`` and ``masked_attention_config5`` (BASELINE
 configs 4 and 5 as operator microbenchmarks); ``cpu_baseline``: the CPU
@@ -52,6 +54,12 @@ def log(msg: str) -> None:
 def attention_bytes(lengths, heads, dim, elem=2, q_elem=4):
     """Algorithmic decode-attention bytes: K+V rows up to each length, plus q read and out write."""
     return sum(int(n) for n in lengths) * heads * dim * 2 * elem + len(lengths) * heads * dim * 2 * q_elem
+
+
+def fused_attention_bytes(lengths, heads, dim, d_model, w_elem=2):
+    """Algorithmic bytes of attention + output projection: K+V rows, q (fp32), W_o, x read and write."""
+    kv = sum(int(n) for n in lengths) * heads * dim * 2 * w_elem
+    return kv + len(lengths) * heads * dim * 4 + d_model * d_model * w_elem + 2 * len(lengths) * d_model * 4
 
 
 def step_bytes(cfg, batch, length):
@@ -135,38 +143,39 @@ def cpu_reference_semantics(cfg, length=PROMPT):
 
 
 def profile_target_attention(reps: int = 24) -> int:
-    """Counter-collection target: the roofline's decode-attention launches plus a calibration copy.
+    """Counter-collection target: the roofline's fused attention launches plus a calibration copy.
 
     Same shapes as the ``roofline`` measurement (324M cache layout, B=16, H=16,
-    D=64, length 3584, one call per layer cache so nothing is re-read from the
-    last-level cache), with random cache contents, followed by one device copy
-    of 256 MiB whose HBM traffic is known (256 MiB read + 256 MiB written).
-    Run it under ``rocprofv3 --pmc FETCH_SIZE`` and ``--pmc WRITE_SIZE``.
+    D=64, d_model 1024, length 3584, one call per layer cache so nothing is
+    re-read from the last-level cache), with random cache contents and weights,
+    followed by one device copy of 256 MiB whose HBM traffic is known (256 MiB
+    read + 256 MiB written). Run it under ``rocprofv3 --pmc FETCH_SIZE`` and
+    ``--pmc WRITE_SIZE``.
     """
     import torch
 
     from systems_for_llms_amd import _lib
-    from systems_for_llms_amd.decode import auto_splits
 
     layers, heads, dim, length = 24, 16, 64, PROMPT + 512  # the timed region's mean length, 3584
+    d_model = heads * dim
     k = torch.randn((layers, BATCH, heads, CONTEXT, dim), device="cuda", dtype=torch.bfloat16)
     v = torch.randn_like(k)
+    w_out = [_lib.pack_gemv(torch.randn((d_model, d_model), device="cuda", dtype=torch.bfloat16) * 0.02)
+             for _ in range(layers)]
     q = torch.randn((BATCH, heads, dim), device="cuda", dtype=torch.float32)
-    out = torch.empty((BATCH, heads, dim), device="cuda", dtype=torch.float32)
+    x = torch.zeros((BATCH, d_model), device="cuda", dtype=torch.float32)
     lengths = torch.full((BATCH,), length, device="cuda", dtype=torch.int32)
-    splits = auto_splits(BATCH, heads, CONTEXT)
-    scratch = torch.empty((BATCH, heads, splits, dim + 2), device="cuda", dtype=torch.float32)
     for i in range(reps):
-        _lib.call("sfl_decode_attention", q.data_ptr(), k[i % layers].data_ptr(), v[i % layers].data_ptr(),
-                  lengths.data_ptr(), scratch.data_ptr(), scratch.data_ptr(), scratch.data_ptr(), out.data_ptr(),
-                  BATCH, heads, heads, CONTEXT, dim, splits, dim ** -0.5, 1, 0, _lib.DTYPE_BF16X2,
-                  _lib.stream_handle())
+        _lib.call("sfl_decode_attention_out_proj", q.data_ptr(), k[i % layers].data_ptr(), v[i % layers].data_ptr(),
+                  lengths.data_ptr(), w_out[i % layers].data_ptr(), x.data_ptr(), BATCH, heads, CONTEXT, dim,
+                  dim ** -0.5, 1, _lib.stream_handle())
     src = torch.ones(256 << 20, device="cuda", dtype=torch.uint8)
     dst = torch.empty_like(src)
     dst.copy_(src)
     torch.cuda.synchronize()
-    log(f"profile target: {reps} decode-attention launches (length {length}, "
-        f"{attention_bytes([length] * BATCH, heads, dim)} algorithmic bytes each) + one 256 MiB copy")
+    log(f"profile target: {reps} fused attention + output_proj launches (length {length}, "
+        f"{fused_attention_bytes([length] * BATCH, heads, dim, d_model)} algorithmic bytes each) "
+        f"+ one 256 MiB copy")
     return 0
 
 
@@ -233,17 +242,27 @@ def main() -> int:
     assert bool((generated >= 0).all()) and bool((generated < cfg.vocab_size).all())
     log(f"decode {args.steps} steps: {ms_per_step:.3f} ms/step, {tokens_per_s:.0f} tok/s")
 
-    # Dominant kernel: decode attention at the timed region's mean attention length.
+    # Dominant kernel: decode attention fused with output_proj, at the timed
+    # region's mean attention length.
     mean_len = first + 1 + (args.steps - 1) / 2
     length = int(round(mean_len))
     lengths = torch.full((BATCH,), length, device="cuda", dtype=torch.int32)
     q = torch.randn((BATCH, cfg.num_heads, cfg.head_dim), device="cuda", dtype=torch.float32)
+    x_scratch = torch.zeros((BATCH, cfg.d_model), device="cuda", dtype=torch.float32)
     from systems_for_llms_amd import _lib
 
     # Rotate over the 24 layers' caches (5.6 GB in all) so no call re-reads
     # data another left in the 256 MB last-level cache: this is HBM streaming,
     # as in the decode loop.
     layer = [0]
+    stream = _lib.stream_handle()
+
+    def fused_call():
+        layer[0] = (layer[0] + 1) % cfg.num_layers
+        k_l, v_l = session.k_cache[layer[0]], session.v_cache[layer[0]]
+        _lib.call("sfl_decode_attention_out_proj", q.data_ptr(), k_l.data_ptr(), v_l.data_ptr(), lengths.data_ptr(),
+                  session.p_out[layer[0]].data_ptr(), x_scratch.data_ptr(), BATCH, cfg.num_heads, CONTEXT,
+                  cfg.head_dim, cfg.head_dim ** -0.5, 1, stream)
 
     def attention_call():
         layer[0] = (layer[0] + 1) % cfg.num_layers
@@ -251,14 +270,21 @@ def main() -> int:
         _lib.call("sfl_decode_attention", q.data_ptr(), k_l.data_ptr(), v_l.data_ptr(), lengths.data_ptr(),
                   session.pmax.data_ptr(), session.psum.data_ptr(), session.pout.data_ptr(),
                   session.attn.data_ptr(), BATCH, cfg.num_heads, cfg.num_heads, CONTEXT, cfg.head_dim,
-                  session.splits, cfg.head_dim ** -0.5, 1, 0, session.act_code, _lib.stream_handle())
+                  session.splits, cfg.head_dim ** -0.5, 1, 0, session.act_code, stream)
 
+    assert session.fused_out_proj, "the 324M decode step runs the fused attention + output_proj kernel"
+    for _ in range(3):
+        fused_call()
+    attn_ms = time_events(fused_call, args.attention_reps)
+    attn_bytes = fused_attention_bytes([length] * BATCH, cfg.num_heads, cfg.head_dim, cfg.d_model)
+    achieved = attn_bytes / (attn_ms * 1e-3) / 1e9
+    log(f"decode attention + output_proj at length {length}: {attn_ms * 1000:.1f} us, {achieved:.0f} GB/s")
     for _ in range(3):
         attention_call()
-    attn_ms = time_events(attention_call, args.attention_reps)
-    attn_bytes = attention_bytes([length] * BATCH, cfg.num_heads, cfg.head_dim)
-    achieved = attn_bytes / (attn_ms * 1e-3) / 1e9
-    log(f"decode attention at length {length}: {attn_ms * 1000:.1f} us, {achieved:.0f} GB/s")
+    op_ms = time_events(attention_call, args.attention_reps)
+    op_bytes = attention_bytes([length] * BATCH, cfg.num_heads, cfg.head_dim)
+    op_gbs = op_bytes / (op_ms * 1e-3) / 1e9
+    log(f"decode attention operator at length {length}: {op_ms * 1000:.1f} us, {op_gbs:.0f} GB/s")
 
     # BASELINE config 4 decode-attention microbench (ragged 1K..16K, B=64, H=16, D=64).
     g = torch.Generator(device="cuda").manual_seed(4)
@@ -298,7 +324,7 @@ def main() -> int:
     # HBM traffic per launch from the committed PMC record of the same launch
     # shape (FETCH_SIZE + WRITE_SIZE, calibrated on a copy of known size).
     traffic = None
-    pmc = ROOT / "profiles" / "decode_attention_324m_b16_len3584_pmc.json"
+    pmc = ROOT / "profiles" / "decode_attention_out_proj_324m_b16_len3584_pmc.json"
     if pmc.exists() and length == 3584:
         traffic = json.loads(pmc.read_text())["traffic_bytes"]
 
@@ -330,12 +356,17 @@ def main() -> int:
                    "d_model": cfg.d_model, "num_layers": cfg.num_layers, "num_heads": cfg.num_heads,
                    "d_ff": cfg.d_ff, "vocab_size": cfg.vocab_size, "global_batch": BATCH,
                    "prompt": PROMPT, "context": CONTEXT, "parallelism": "single GPU"},
-        "roofline": {"bound": "hbm", "kernel": "decode_attn_kernel (split-KV decode attention, one launch)",
+        "roofline": {"bound": "hbm",
+                     "kernel": "decode_attn_kernel<resid_t> (decode attention + output_proj + residual, one launch)",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "traffic_source": "profiles/decode_attention_324m_b16_len3584_pmc.json" if traffic else None,
+                     "traffic_source": f"profiles/{pmc.name}" if traffic else None,
                      "bytes_per_launch": attn_bytes, "us_per_launch": round(attn_ms * 1000, 2),
-                     "shape": f"B={BATCH} H={cfg.num_heads} D={cfg.head_dim} length={length} (mean of timed region)"},
+                     "shape": f"B={BATCH} H={cfg.num_heads} D={cfg.head_dim} d_model={cfg.d_model} "
+                              f"length={length} (mean of timed region)"},
+        "decode_attention_operator": {"us": round(op_ms * 1000, 2), "achieved_gbs": round(op_gbs, 1),
+                                      "frac": round(op_gbs / HBM_PEAK_GBS, 4), "bytes": op_bytes,
+                                      "shape": f"sfl_decode_attention, same shape and caches, BF16X2 output"},
         "e2e": {"bytes_per_step": int(e2e_bytes), "achieved_gbs": round(e2e_gbs, 1),
                 "frac_of_hbm_peak": round(e2e_gbs / HBM_PEAK_GBS, 4),
                 "roofline_tok_s": round(BATCH / (e2e_bytes / (HBM_PEAK_GBS * 1e9)), 1),
