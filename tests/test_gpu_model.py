@@ -178,3 +178,30 @@ def test_config2_bf16_teacher_forced_against_cpu_oracle():
     torch.cuda.synchronize()
     got = session.logits[:, prompt_len - 1:].float().cpu()
     bf16_gate("config2", got, ref, floor)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_split_cache_path_matches_fused_path(dtype):
+    """With more than one KV split the step runs attention + output_proj as two
+    launches (no atomics in the projection); both paths give the same logits."""
+    cfg = ModelConfig(vocab_size=500, context_length=96, d_model=256, num_layers=2, num_heads=4,
+                      d_ff=512, rope_theta=10000.0)
+    sd = seeded_state_dict(cfg, 31)
+    model = gpu_model(cfg, sd, dtype)
+    ids = seeded_prompt(cfg.vocab_size, 3, 96, 32).cuda()
+    runs = {}
+    for splits in (1, 3):
+        session = DecodeSession(model, batch=3, capacity=96, splits=splits, record_logits=True)
+        assert session.fused_out_proj == (splits == 1)
+        session.start(ids)
+        session.run(95, use_graph=True)
+        runs[splits] = session.logits.clone().cpu()
+    fused, split = runs[1][:, :95], runs[3][:, :95]  # logits of positions 0..94
+    err = (fused - split).abs().max().item()
+    print(f"{dtype}: fused vs split-cache path max-abs {err:.2e}")
+    assert err < (2e-5 if dtype == torch.float32 else 2e-3)
+    if dtype == torch.float32:
+        torch.testing.assert_close(fused, om.forward(sd, cfg, ids.cpu())[:, :95], atol=2e-5, rtol=1e-4)
+    else:  # against the oracle with the kernels' storage formats (bf16 weights and KV)
+        floor = om.forward(om.round_weights(sd), cfg, ids.cpu(), kv_dtype=torch.bfloat16)[:, :95]
+        assert (fused - floor).abs().max().item() <= 1e-2
