@@ -19,7 +19,7 @@
 // operand is exactly the probabilities the lane already holds (the product is
 // a sum over keys, so any order both operands share is exact), and V^T rows
 // come from LDS as 8-byte runs.
-#include "common.hpp"
+#include "lds_dma.hpp"
 
 namespace sfl {
 namespace {
@@ -80,7 +80,7 @@ struct AttnArgs {
   void* o;
   float* lse;
   long qs[3], ks[3], vs[3], os[3];  // strides (elements) of batch, head, sequence
-  int heads, n;
+  int batch, heads, n;
   float scale_log2;
   MaskArgs m;
   Sched s;
@@ -105,6 +105,23 @@ __device__ __forceinline__ bool allowed_flat(const MaskArgs& m, int q, int k, in
   const bool left_ok = (m.left < 0) | (q - k <= m.left);
   const bool right_ok = (m.right < 0) | (k - q <= m.right);
   return in & causal_ok & doc_ok & ((k < m.prefix) | (left_ok & right_ok));
+}
+
+// Workgroup -> (query tile, batch * head) of a 1-D grid, XCD-aware. Workgroups
+// are dealt to the 8 XCDs round-robin and each XCD has its own 4 MB L2, so XCD
+// x takes a contiguous range of the head-major tile order: the ~100
+// workgroups an XCD runs at once then share the K/V of 2-3 heads (0.8 MB per
+// head at 3072 x 64 bf16) instead of every XCD streaming every head's K/V.
+// Within a head the query tiles run last-first, so the longest causal rows
+// start first.
+constexpr int kXcds = 8;
+__device__ __forceinline__ int2 attn_tile(int nqt, int nbh) {
+  const int total = nqt * nbh;
+  const int blk = int(blockIdx.x);
+  const int x = blk % kXcds, idx = blk / kXcds;
+  const int base = total / kXcds, extra = total % kXcds;
+  const int t = x * base + min(x, extra) + idx;
+  return make_int2(nqt - 1 - t % nqt, t / nqt);
 }
 
 // Tile geometry of one query tile, as masks.py/_tile_geometry derives it.
@@ -155,8 +172,9 @@ __global__ __launch_bounds__(kThreads) void masked_attention_kernel(AttnArgs a) 
   const int tid = threadIdx.x;
   const int wave = tid / kWave, lane = tid % kWave;
   const int col = lane % 16, grp = lane / 16;
-  const int qt = blockIdx.x;
-  const int bh = blockIdx.y;
+  const int2 tile = attn_tile((a.n + BQ - 1) / BQ, a.batch * a.heads);
+  const int qt = tile.x;
+  const int bh = tile.y;
   const int b = bh / a.heads, h = bh % a.heads;
   const int n = a.n;
   const int q0 = qt * BQ;
@@ -415,8 +433,9 @@ __global__ __launch_bounds__(kPairWaves * kWave) __attribute__((amdgpu_waves_per
   const int wave = tid / kWave, lane = tid % kWave;
   const int col = lane % 16, grp = lane / 16;
   const int n = a.n;
-  const int qt = blockIdx.x;
-  const int bh = blockIdx.y;
+  const int2 tile = attn_tile((a.n + BQ - 1) / BQ, a.batch * a.heads);
+  const int qt = tile.x;
+  const int bh = tile.y;
   const int b = bh / a.heads, h = bh % a.heads;
   const int q0 = qt * BQ;
   const int q1 = min(q0 + BQ, n) - 1;
@@ -562,13 +581,273 @@ __global__ __launch_bounds__(kPairWaves * kWave) __attribute__((amdgpu_waves_per
   }
 }
 
+// Head dim 64 on 32x32x16 MFMAs (twice the rate of 16x16x32 on gfx950). A
+// workgroup of 2 waves owns a 64-query tile; a wave owns 32 queries, one per
+// lane pair (lanes c and c + 32). S^T = K Q^T per 32-key block: lane
+// (c, h = lane/32) ends with 16 scores of query q0 + 32*wave + c, keys
+// 8*(j/4) + 4h + j%4 of the block, so the row max needs one exchange with
+// the partner lane and the rescale factor is per lane. The head dim is split
+// between the lane halves in both K and Q (h takes dims 32h .. 32h+31; a
+// contraction is exact in any order both operands share), so a lane reads 64
+// contiguous bytes of its key or query row. K tiles go global -> LDS by
+// buffer loads that write LDS directly (no registers), rows stored with their
+// 16-byte slots XOR-swizzled by the row so that the 32 rows an operand read
+// touches hit distinct banks; rows past the sequence read as zeros through the
+// buffer range check. O^T = V^T P^T: for the 16-key
+// step s the P^T operand of lane (c, h) is its own probabilities j = 8(s%2)
+// .. +7 of block s/2 (keys 16s + 4h + {0..3} and 16s + 8 + 4h + {0..3}), so
+// V^T is stored in LDS with the middle two key quads of every 16 swapped and
+// each V^T operand is one 16-byte read. The row sum comes from the packed
+// probabilities with dot2 (the sum of exactly the values the P V product
+// weights), kept per lane and added with the partner's at the end.
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x2_v __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_v __attribute__((ext_vector_type(2)));
+
+template <typename T>
+__device__ __forceinline__ f32x16 mfma32(const u32x4& a, const u32x4& b, f32x16 c);
+template <>
+__device__ __forceinline__ f32x16 mfma32<bf16_t>(const u32x4& a, const u32x4& b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+template <>
+__device__ __forceinline__ f32x16 mfma32<f16_t>(const u32x4& a, const u32x4& b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+
+// acc + lo + hi of a packed pair (v_dot2 with (1, 1)).
+template <typename T> __device__ __forceinline__ float add_pair(uint32_t pk, float acc);
+template <> __device__ __forceinline__ float add_pair<bf16_t>(uint32_t pk, float acc) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_v, pk), __builtin_bit_cast(bf16x2_v, 0x3f803f80u),
+                                         acc, false);
+}
+template <> __device__ __forceinline__ float add_pair<f16_t>(uint32_t pk, float acc) {
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_v, pk), __builtin_bit_cast(f16x2_v, 0x3c003c00u), acc, false);
+}
+
+constexpr int kA32Waves = 2;
+
+template <typename T>
+__global__ __launch_bounds__(kA32Waves * kWave) __attribute__((amdgpu_waves_per_eu(2))) void masked_attention32_kernel(AttnArgs a) {
+  constexpr int D = 64;
+  constexpr int LDV = BK + kPadK;  // V^T row stride (elements)
+  __shared__ __align__(16) uint16_t vt_s[2][D * LDV];
+  __shared__ __align__(16) uint4 k_s[2][BK][8];  // [key][16-byte slot s at s ^ (key & 7)]
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave), lane = tid % kWave;
+  const int c = lane % 32, h = lane / 32;
+  const int n = a.n;
+  // Tile indices, schedule entries and key offsets are wave-uniform; keeping
+  // them in scalar registers keeps their loads off the vector memory counter,
+  // which would otherwise make the math wait for the next tile's prefetch.
+  const int2 tile = attn_tile((a.n + BQ - 1) / BQ, a.batch * a.heads);
+  const int qt = __builtin_amdgcn_readfirstlane(tile.x);
+  const int bh = __builtin_amdgcn_readfirstlane(tile.y);
+  const int b = bh / a.heads, hd = bh % a.heads;
+  const int q0 = qt * BQ;
+  const int q1 = min(q0 + BQ, n) - 1;
+  const int qrow = q0 + 32 * wave + c;  // this lane's query
+
+  const uint16_t* qp = static_cast<const uint16_t*>(a.q) + b * a.qs[0] + hd * a.qs[1];
+  const uint16_t* kp = static_cast<const uint16_t*>(a.k) + b * a.ks[0] + hd * a.ks[1];
+  const uint16_t* vp = static_cast<const uint16_t*>(a.v) + b * a.vs[0] + hd * a.vs[1];
+
+  // Q^T operand of k-step ks: Q[qrow][32h + 8ks .. +8].
+  u32x4 qreg[4];
+  {
+    const uint16_t* qr = qp + long(min(qrow, n - 1)) * a.qs[2] + 32 * h;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const uint4 r = load16(qr + 8 * ks);
+      qreg[ks] = u32x4{r.x, r.y, r.z, r.w};
+    }
+  }
+
+  float m_run = -INFINITY, l_run = 0.f;
+  f32x16 oacc[2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int j = 0; j < 16; ++j) oacc[t][j] = 0.f;
+
+  const TileBounds tb = tile_bounds(a.m, n, q0, q1);
+  int count, base = 0;
+  if (a.s.mode == 1) {
+    base = __builtin_amdgcn_readfirstlane(a.s.row_ptr[qt]);
+    count = __builtin_amdgcn_readfirstlane(a.s.row_ptr[qt + 1]) - base;
+  } else {
+    const int lowg = min(tb.gend, tb.begin);
+    count = lowg + max(0, max(tb.end, tb.gend) - tb.begin);
+  }
+  const int lowg = min(tb.gend, tb.begin);
+
+  // K tile: 8 loads of 8 rows (1 KB) per tile, 4 per wave; lane i moves row
+  // 8ch + i/8, logical slot (i%8) ^ (i/8) into physical slot i%8. The buffer
+  // covers this head's rows [0, n): rows past n read as zeros.
+  const unsigned krow_bytes = unsigned(a.ks[2]) * 2u;
+  const i32x4_t krsrc = buffer_rsrc(kp, unsigned((long(n - 1) * a.ks[2] + D) * 2));
+  const unsigned kvoff = unsigned(lane / 8) * krow_bytes + 16u * unsigned((lane % 8) ^ (lane / 8));
+  // V share of this thread: keys vr0 .. vr0+3, dims vd0 .. vd0+7 (128 threads
+  // cover 64 keys x 64 dims); its V^T column is vr0 with quads 1 and 2 of each
+  // 16 keys swapped.
+  const int vr0 = 4 * (tid % 16), vd0 = 8 * (tid / 16);
+  const int vquad = (vr0 >> 2) & 3;
+  const int vcol = (vr0 & ~15) | ((vquad == 1 ? 2 : vquad == 2 ? 1 : vquad) << 2);
+  uint4 vreg[4];
+#define SFL_A32_LOAD(kb, kbuf)                                                              \
+  {                                                                                         \
+    const int k0_ = (kb) * BK;                                                              \
+    _Pragma("unroll") for (int cw = 0; cw < BK / 8 / kA32Waves; ++cw) {                     \
+      const int ch_ = cw * kA32Waves + wave;                                                \
+      lds_load16(krsrc, lds_offset(&k_s[kbuf][8 * ch_][0]), kvoff,                          \
+                 unsigned(k0_ + 8 * ch_) * krow_bytes);                                     \
+    }                                                                                       \
+    _Pragma("unroll") for (int u = 0; u < 4; ++u)                                           \
+      vreg[u] = load16(vp + long(min(k0_ + vr0 + u, n - 1)) * a.vs[2] + vd0);               \
+  }
+#define SFL_A32_TILE_AT(it, kb_, fl_)                                                       \
+  if (a.s.mode == 1) {                                                                      \
+    kb_ = __builtin_amdgcn_readfirstlane(a.s.col_idx[base + (it)]);                         \
+    fl_ = __builtin_amdgcn_readfirstlane(int(a.s.full[base + (it)])) != 0;                  \
+  } else {                                                                                  \
+    kb_ = (it) < lowg ? (it) : tb.begin + ((it) - lowg);                                    \
+    fl_ = !a.m.docs && covered(tb, kb_ * BK, min(kb_ * BK + BK, n) - 1);                    \
+  }
+#define SFL_A32_STORE_VT(buf)                                                               \
+  {                                                                                         \
+    const uint32_t w0_[4] = {vreg[0].x, vreg[0].y, vreg[0].z, vreg[0].w};                  \
+    const uint32_t w1_[4] = {vreg[1].x, vreg[1].y, vreg[1].z, vreg[1].w};                  \
+    const uint32_t w2_[4] = {vreg[2].x, vreg[2].y, vreg[2].z, vreg[2].w};                  \
+    const uint32_t w3_[4] = {vreg[3].x, vreg[3].y, vreg[3].z, vreg[3].w};                  \
+    _Pragma("unroll") for (int e = 0; e < 8; ++e) {                                         \
+      const uint32_t sel_ = (e & 1) ? 0x07060302u : 0x05040100u;                             \
+      const uint32_t k01_ = __builtin_amdgcn_perm(w1_[e / 2], w0_[e / 2], sel_);             \
+      const uint32_t k23_ = __builtin_amdgcn_perm(w3_[e / 2], w2_[e / 2], sel_);             \
+      *reinterpret_cast<uint2*>(&vt_s[buf][(vd0 + e) * LDV + vcol]) = make_uint2(k01_, k23_); \
+    }                                                                                       \
+  }
+  // One key tile: S^T, masked online softmax, O^T += V^T P^T.
+#define SFL_A32_MATH(buf, k0, full)                                                         \
+  {                                                                                         \
+    f32x16 sacc[2];                                                                         \
+    _Pragma("unroll") for (int kb2 = 0; kb2 < 2; ++kb2) {                                   \
+      _Pragma("unroll") for (int j = 0; j < 16; ++j) sacc[kb2][j] = 0.f;                    \
+      _Pragma("unroll") for (int ks = 0; ks < 4; ++ks) {                                    \
+        const uint4 kr_ = k_s[buf][32 * kb2 + c][(4 * h + ks) ^ (c & 7)];                   \
+        sacc[kb2] = mfma32<T>(u32x4{kr_.x, kr_.y, kr_.z, kr_.w}, qreg[ks], sacc[kb2]);      \
+      }                                                                                     \
+    }                                                                                       \
+    if (!((full) && (k0) + BK <= n)) { /* mask in place */                                \
+      const int64_t dq_ = a.m.docs ? a.m.docs[min(qrow, n - 1)] : 0;                        \
+      _Pragma("unroll") for (int i = 0; i < 32; ++i) {                                      \
+        const int j_ = i % 16;                                                              \
+        const int key_ = (k0) + 32 * (i / 16) + 8 * (j_ / 4) + 4 * h + j_ % 4;             \
+        const int64_t dk_ = a.m.docs ? a.m.docs[min(key_, n - 1)] : 0;                      \
+        const bool ok_ = (full) ? (key_ < n) & (qrow < n)                                   \
+                                : allowed_flat(a.m, qrow, key_, n, dq_, dk_);              \
+        if (!ok_) sacc[i / 16][j_] = -INFINITY;                                             \
+      }                                                                                     \
+    }                                                                                       \
+    float mx_ = fmaxf(sacc[0][0], sacc[0][1]);                                              \
+    _Pragma("unroll") for (int i = 2; i < 32; i += 2)                                       \
+      mx_ = fmaxf(fmaxf(mx_, sacc[i / 16][i % 16]), sacc[i / 16][i % 16 + 1]);              \
+    mx_ = fmaxf(mx_, __shfl_xor(mx_, 32, kWave));                                           \
+    const float cs_ = a.scale_log2;                                                         \
+    const float m_new_ = fmaxf(m_run, mx_ * cs_);                                           \
+    const float ms_ = m_new_ == -INFINITY ? 0.f : m_new_;                                   \
+    const float alpha_ = __builtin_amdgcn_exp2f(m_run - ms_);                               \
+    m_run = m_new_;                                                                         \
+    u32x4 pop_[4];                                                                          \
+    float psum_ = 0.f;                                                                      \
+    _Pragma("unroll") for (int s2 = 0; s2 < 4; ++s2) {                                      \
+      uint32_t pk_[4];                                                                      \
+      _Pragma("unroll") for (int e = 0; e < 4; ++e) {                                       \
+        const int i0_ = 16 * (s2 / 2) + 8 * (s2 % 2) + 2 * e;                               \
+        pk_[e] = pack2<T>(__builtin_amdgcn_exp2f(fmaf(sacc[i0_ / 16][i0_ % 16], cs_, -ms_)),     \
+                          __builtin_amdgcn_exp2f(fmaf(sacc[i0_ / 16][i0_ % 16 + 1], cs_, -ms_))); \
+        psum_ = add_pair<T>(pk_[e], psum_);                                                 \
+      }                                                                                     \
+      pop_[s2] = u32x4{pk_[0], pk_[1], pk_[2], pk_[3]};                                     \
+    }                                                                                       \
+    l_run = l_run * alpha_ + psum_;                                                         \
+    if (__ballot(alpha_ != 1.f)) {                                                          \
+      _Pragma("unroll") for (int t = 0; t < 2; ++t) oacc[t] *= alpha_;                     \
+    }                                                                                       \
+    _Pragma("unroll") for (int s2 = 0; s2 < 4; ++s2) {                                      \
+      _Pragma("unroll") for (int t = 0; t < 2; ++t) {                                       \
+        const u32x4 vop_ = *reinterpret_cast<const u32x4*>(                                 \
+            &vt_s[buf][(32 * t + c) * LDV + 16 * s2 + 8 * h]);                              \
+        oacc[t] = mfma32<T>(vop_, pop_[s2], oacc[t]);                                       \
+      }                                                                                     \
+    }                                                                                       \
+  }
+
+  if (count > 0) {
+    int kb0;
+    bool f0;
+    SFL_A32_TILE_AT(0, kb0, f0)
+    (void)f0;
+    SFL_A32_LOAD(kb0, 0)
+    SFL_A32_STORE_VT(0)
+  }
+  __builtin_amdgcn_s_waitcnt(sfl_vmcnt(0));
+  __syncthreads();
+#define SFL_A32_STEP(it)                                                                    \
+  {                                                                                         \
+    int kb;                                                                                 \
+    bool full;                                                                              \
+    SFL_A32_TILE_AT(it, kb, full)                                                           \
+    full = full && a.s.use_full;                                                            \
+    const int k0 = kb * BK;                                                                 \
+    const int buf = (it) & 1;                                                               \
+    const bool more = (it) + 1 < count;                                                     \
+    if (more) {                                                                             \
+      int kbn;                                                                              \
+      bool fn;                                                                              \
+      SFL_A32_TILE_AT((it) + 1, kbn, fn)                                                    \
+      (void)fn;                                                                             \
+      SFL_A32_LOAD(kbn, buf ^ 1)                                                            \
+    }                                                                                       \
+    SFL_A32_MATH(buf, k0, full)                                                             \
+    if (more) SFL_A32_STORE_VT(buf ^ 1)                                                     \
+    __builtin_amdgcn_s_waitcnt(sfl_vmcnt(0)); /* the next K tile has landed */              \
+    __syncthreads();                                                                        \
+  }
+  for (int it = 0; it < count; ++it) SFL_A32_STEP(it)
+#undef SFL_A32_STEP
+#undef SFL_A32_MATH
+#undef SFL_A32_STORE_VT
+#undef SFL_A32_TILE_AT
+#undef SFL_A32_LOAD
+
+  const float l_tot = l_run + __shfl_xor(l_run, 32, kWave);
+  if (qrow >= n) return;
+  const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+  uint16_t* op = static_cast<uint16_t*>(a.o) + b * a.os[0] + hd * a.os[1] + long(qrow) * a.os[2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int jq = 0; jq < 4; ++jq)
+      *reinterpret_cast<uint2*>(op + 32 * t + 8 * jq + 4 * h) =
+          make_uint2(pack2<T>(oacc[t][4 * jq] * inv, oacc[t][4 * jq + 1] * inv),
+                     pack2<T>(oacc[t][4 * jq + 2] * inv, oacc[t][4 * jq + 3] * inv));
+  if (a.lse && h == 0) {
+    const float lse = l_tot > 0.f ? (m_run + log2f(l_tot)) * 0.6931471805599453f : -INFINITY;
+    a.lse[(long(b) * a.heads + hd) * n + qrow] = lse;
+  }
+}
+
 template <typename T>
 int launch_masked(const AttnArgs& a, int batch, int dim, hipStream_t stream) {
-  dim3 grid((a.n + BQ - 1) / BQ, batch * a.heads);
+  dim3 grid(unsigned((a.n + BQ - 1) / BQ) * unsigned(batch * a.heads));
   switch (dim) {
     case 32: hipLaunchKernelGGL((masked_attention_kernel<T, 32>), grid, dim3(kThreads), 0, stream, a); break;
     case 64:
-      hipLaunchKernelGGL((masked_attention_pair_kernel<T>), grid, dim3(kPairWaves * kWave), 0, stream, a);
+      // The 32x32 kernel addresses K with 32-bit buffer offsets.
+      if (long(a.n) * a.ks[2] * 2 < (1L << 31))
+        hipLaunchKernelGGL((masked_attention32_kernel<T>), grid, dim3(kA32Waves * kWave), 0, stream, a);
+      else
+        hipLaunchKernelGGL((masked_attention_pair_kernel<T>), grid, dim3(kPairWaves * kWave), 0, stream, a);
       break;
     case 128: hipLaunchKernelGGL((masked_attention_kernel<T, 128>), grid, dim3(kThreads), 0, stream, a); break;
     default: return set_error(SFL_ERR_UNSUPPORTED, "masked_attention: head dim must be 32, 64 or 128");
@@ -612,7 +891,9 @@ extern "C" int sfl_masked_attention(const void* q, const void* k, const void* v,
   for (int i = 0; i < 3; ++i) {
     a.qs[i] = q_strides[i]; a.ks[i] = k_strides[i]; a.vs[i] = v_strides[i]; a.os[i] = o_strides[i];
   }
-  a.heads = heads; a.n = n; a.scale_log2 = scale * kLog2e;
+  a.batch = batch; a.heads = heads; a.n = n; a.scale_log2 = scale * kLog2e;
+  if (long((n + BQ - 1) / BQ) * batch * heads > (1L << 31) - 1)
+    return set_error(SFL_ERR_UNSUPPORTED, "%s: too many query tiles", what);
   a.m = MaskArgs{causal, window_left, window_right, global_prefix, document_ids};
   a.s = Sched{schedule_mode, use_full_blocks, row_ptr, col_idx, full_blocks};
   hipStream_t s = static_cast<hipStream_t>(stream);
