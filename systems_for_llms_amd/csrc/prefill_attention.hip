@@ -581,6 +581,29 @@ __global__ __launch_bounds__(kPairWaves * kWave) __attribute__((amdgpu_waves_per
   }
 }
 
+// The keys one query may attend, without document labels, as two intervals:
+// the window [lo, hi] (causality and the sequence end folded in) and the
+// global prefix [0, phi]; allowed_flat() is "key in either". Returned relative
+// to `base` for an unsigned range test per key offset c:
+//   allowed(base + c) == (unsigned(c + r.a) <= unsigned(r.w)) | (c <= r.p).
+struct KeyRanges { int a, w, p; };
+__device__ __forceinline__ KeyRanges key_ranges(const MaskArgs& m, int q, int n, int base, bool all) {
+  int lo = 0, hi = n - 1, phi = -1;
+  if (!all) {
+    if (m.left >= 0) lo = max(0, q - min(m.left, n));
+    if (m.right >= 0) hi = min(hi, q + min(m.right, n));
+    if (m.causal) hi = min(hi, q);
+    phi = min(m.prefix, n) - 1;
+    if (m.causal) phi = min(phi, q);
+  }
+  if (q >= n) { lo = 1; hi = 0; phi = -1; }
+  KeyRanges r;
+  if (hi < lo) { r.a = 1 << 30; r.w = 0; }  // empty window: no c + a fits in [0, 0]
+  else { r.a = base - lo; r.w = hi - lo; }
+  r.p = phi - base;
+  return r;
+}
+
 // Head dim 64 on 32x32x16 MFMAs (twice the rate of 16x16x32 on gfx950). A
 // workgroup of 2 waves owns a 64-query tile; a wave owns 32 queries, one per
 // lane pair (lanes c and c + 32). S^T = K Q^T per 32-key block: lane
@@ -693,7 +716,11 @@ __global__ __launch_bounds__(kA32Waves * kWave) __attribute__((amdgpu_waves_per_
   const int vr0 = 4 * (tid % 16), vd0 = 8 * (tid / 16);
   const int vquad = (vr0 >> 2) & 3;
   const int vcol = (vr0 & ~15) | ((vquad == 1 ? 2 : vquad == 2 ? 1 : vquad) << 2);
-  uint4 vreg[4];
+  const unsigned vrow_bytes = unsigned(a.vs[2]) * 2u;
+  const __amdgpu_buffer_rsrc_t vrsrc =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(vp), 0, int((long(n - 1) * a.vs[2] + D) * 2), 0x00020000);
+  const unsigned vvoff = unsigned(vr0) * vrow_bytes + unsigned(vd0) * 2u;
+  u32x4 vreg[4];
 #define SFL_A32_LOAD(kb, kbuf)                                                              \
   {                                                                                         \
     const int k0_ = (kb) * BK;                                                              \
@@ -702,8 +729,9 @@ __global__ __launch_bounds__(kA32Waves * kWave) __attribute__((amdgpu_waves_per_
       lds_load16(krsrc, lds_offset(&k_s[kbuf][8 * ch_][0]), kvoff,                          \
                  unsigned(k0_ + 8 * ch_) * krow_bytes);                                     \
     }                                                                                       \
-    _Pragma("unroll") for (int u = 0; u < 4; ++u)                                           \
-      vreg[u] = load16(vp + long(min(k0_ + vr0 + u, n - 1)) * a.vs[2] + vd0);               \
+    _Pragma("unroll") for (int u = 0; u < 4; ++u) /* rows past n read as zeros */           \
+      vreg[u] = __builtin_amdgcn_raw_buffer_load_b128(vrsrc, int(vvoff + unsigned(u) * vrow_bytes), \
+                                                      int(unsigned(k0_) * vrow_bytes), 0);  \
   }
 #define SFL_A32_TILE_AT(it, kb_, fl_)                                                       \
   if (a.s.mode == 1) {                                                                      \
@@ -737,15 +765,25 @@ __global__ __launch_bounds__(kA32Waves * kWave) __attribute__((amdgpu_waves_per_
         sacc[kb2] = mfma32<T>(u32x4{kr_.x, kr_.y, kr_.z, kr_.w}, qreg[ks], sacc[kb2]);      \
       }                                                                                     \
     }                                                                                       \
-    if (!((full) && (k0) + BK <= n)) { /* mask in place */                                \
-      const int64_t dq_ = a.m.docs ? a.m.docs[min(qrow, n - 1)] : 0;                        \
-      _Pragma("unroll") for (int i = 0; i < 32; ++i) {                                      \
-        const int j_ = i % 16;                                                              \
-        const int key_ = (k0) + 32 * (i / 16) + 8 * (j_ / 4) + 4 * h + j_ % 4;             \
-        const int64_t dk_ = a.m.docs ? a.m.docs[min(key_, n - 1)] : 0;                      \
-        const bool ok_ = (full) ? (key_ < n) & (qrow < n)                                   \
-                                : allowed_flat(a.m, qrow, key_, n, dq_, dk_);              \
-        if (!ok_) sacc[i / 16][j_] = -INFINITY;                                             \
+    if (!((full) && (k0) + BK <= n)) { /* mask in place, without branches per score */     \
+      if (!a.m.docs) {                                                                      \
+        const KeyRanges kr_ = key_ranges(a.m, qrow, n, (k0) + 4 * h, (full));               \
+        _Pragma("unroll") for (int i = 0; i < 32; ++i) {                                    \
+          const int j_ = i % 16;                                                            \
+          const int c_ = 32 * (i / 16) + 8 * (j_ / 4) + j_ % 4;                             \
+          const bool ok_ = (unsigned(c_ + kr_.a) <= unsigned(kr_.w)) | (c_ <= kr_.p);       \
+          sacc[i / 16][j_] = ok_ ? sacc[i / 16][j_] : -INFINITY;                            \
+        }                                                                                   \
+      } else {                                                                              \
+        const int64_t dq_ = a.m.docs[min(qrow, n - 1)];                                     \
+        _Pragma("unroll") for (int i = 0; i < 32; ++i) {                                    \
+          const int j_ = i % 16;                                                            \
+          const int key_ = (k0) + 32 * (i / 16) + 8 * (j_ / 4) + 4 * h + j_ % 4;           \
+          const int64_t dk_ = a.m.docs[min(key_, n - 1)];                                   \
+          const bool ok_ = (full) ? (key_ < n) & (qrow < n)                                 \
+                                  : allowed_flat(a.m, qrow, key_, n, dq_, dk_);            \
+          sacc[i / 16][j_] = ok_ ? sacc[i / 16][j_] : -INFINITY;                            \
+        }                                                                                   \
       }                                                                                     \
     }                                                                                       \
     float mx_ = fmaxf(sacc[0][0], sacc[0][1]);                                              \
@@ -843,8 +881,8 @@ int launch_masked(const AttnArgs& a, int batch, int dim, hipStream_t stream) {
   switch (dim) {
     case 32: hipLaunchKernelGGL((masked_attention_kernel<T, 32>), grid, dim3(kThreads), 0, stream, a); break;
     case 64:
-      // The 32x32 kernel addresses K with 32-bit buffer offsets.
-      if (long(a.n) * a.ks[2] * 2 < (1L << 31))
+      // The 32x32 kernel addresses K and V with 32-bit buffer offsets.
+      if (long(a.n) * a.ks[2] * 2 < (1L << 31) && long(a.n) * a.vs[2] * 2 < (1L << 31))
         hipLaunchKernelGGL((masked_attention32_kernel<T>), grid, dim3(kA32Waves * kWave), 0, stream, a);
       else
         hipLaunchKernelGGL((masked_attention_pair_kernel<T>), grid, dim3(kPairWaves * kWave), 0, stream, a);
