@@ -648,6 +648,84 @@ template <> __device__ __forceinline__ float add_pair<f16_t>(uint32_t pk, float 
   return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_v, pk), __builtin_bit_cast(f16x2_v, 0x3c003c00u), acc, false);
 }
 
+// One key tile of masked_attention32_kernel for this wave: S^T = K Q^T from the
+// swizzled K tile, the online softmax (masked when kMask), and O^T += V^T P^T.
+// Instantiated separately for full and masked tiles so each is straight-line
+// code.
+template <typename T, bool kMask, int LDV>
+__device__ __forceinline__ void attn32_tile(const AttnArgs& a, const uint4 (&kt)[BK][8], const uint16_t* vt,
+                                            const u32x4 (&qreg)[4], f32x16 (&oacc)[2], float& m_run,
+                                            float& l_run, int c, int h, int qrow, int k0, bool full) {
+  const int n = a.n;
+  f32x16 sacc[2];
+#pragma unroll
+  for (int kb2 = 0; kb2 < 2; ++kb2) {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) sacc[kb2][j] = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const uint4 kr = kt[32 * kb2 + c][(4 * h + ks) ^ (c & 7)];
+      sacc[kb2] = mfma32<T>(u32x4{kr.x, kr.y, kr.z, kr.w}, qreg[ks], sacc[kb2]);
+    }
+  }
+  if constexpr (kMask) {
+    if (!a.m.docs) {
+      const KeyRanges kr = key_ranges(a.m, qrow, n, k0 + 4 * h, full);
+#pragma unroll
+      for (int i = 0; i < 32; ++i) {
+        const int j = i % 16;
+        const int cc = 32 * (i / 16) + 8 * (j / 4) + j % 4;
+        const bool ok = (unsigned(cc + kr.a) <= unsigned(kr.w)) | (cc <= kr.p);
+        sacc[i / 16][j] = ok ? sacc[i / 16][j] : -INFINITY;
+      }
+    } else {
+      const int64_t dq = a.m.docs[min(qrow, n - 1)];
+#pragma unroll
+      for (int i = 0; i < 32; ++i) {
+        const int j = i % 16;
+        const int key = k0 + 32 * (i / 16) + 8 * (j / 4) + 4 * h + j % 4;
+        const int64_t dk = a.m.docs[min(key, n - 1)];
+        const bool ok = full ? (key < n) & (qrow < n) : allowed_flat(a.m, qrow, key, n, dq, dk);
+        sacc[i / 16][j] = ok ? sacc[i / 16][j] : -INFINITY;
+      }
+    }
+  }
+  float mx = fmaxf(sacc[0][0], sacc[0][1]);
+#pragma unroll
+  for (int i = 2; i < 32; i += 2) mx = fmaxf(fmaxf(mx, sacc[i / 16][i % 16]), sacc[i / 16][i % 16 + 1]);
+  mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+  const float cs = a.scale_log2;
+  const float m_new = fmaxf(m_run, mx * cs);
+  const float ms = m_new == -INFINITY ? 0.f : m_new;
+  const float alpha = __builtin_amdgcn_exp2f(m_run - ms);
+  m_run = m_new;
+  u32x4 pop[4];
+  float psum = 0.f;
+#pragma unroll
+  for (int s2 = 0; s2 < 4; ++s2) {
+    uint32_t pk[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int i0 = 16 * (s2 / 2) + 8 * (s2 % 2) + 2 * e;
+      pk[e] = pack2<T>(__builtin_amdgcn_exp2f(fmaf(sacc[i0 / 16][i0 % 16], cs, -ms)),
+                       __builtin_amdgcn_exp2f(fmaf(sacc[i0 / 16][i0 % 16 + 1], cs, -ms)));
+      psum = add_pair<T>(pk[e], psum);
+    }
+    pop[s2] = u32x4{pk[0], pk[1], pk[2], pk[3]};
+  }
+  l_run = l_run * alpha + psum;
+#pragma unroll
+  for (int t = 0; t < 2; ++t) oacc[t] *= alpha;
+#pragma unroll
+  for (int s2 = 0; s2 < 4; ++s2) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const u32x4 vop = *reinterpret_cast<const u32x4*>(&vt[(32 * t + c) * LDV + 16 * s2 + 8 * h]);
+      oacc[t] = mfma32<T>(vop, pop[s2], oacc[t]);
+    }
+  }
+}
+
 constexpr int kA32Waves = 2;
 
 template <typename T>
@@ -755,71 +833,6 @@ __global__ __launch_bounds__(kA32Waves * kWave) __attribute__((amdgpu_waves_per_
     }                                                                                       \
   }
   // One key tile: S^T, masked online softmax, O^T += V^T P^T.
-#define SFL_A32_MATH(buf, k0, full)                                                         \
-  {                                                                                         \
-    f32x16 sacc[2];                                                                         \
-    _Pragma("unroll") for (int kb2 = 0; kb2 < 2; ++kb2) {                                   \
-      _Pragma("unroll") for (int j = 0; j < 16; ++j) sacc[kb2][j] = 0.f;                    \
-      _Pragma("unroll") for (int ks = 0; ks < 4; ++ks) {                                    \
-        const uint4 kr_ = k_s[buf][32 * kb2 + c][(4 * h + ks) ^ (c & 7)];                   \
-        sacc[kb2] = mfma32<T>(u32x4{kr_.x, kr_.y, kr_.z, kr_.w}, qreg[ks], sacc[kb2]);      \
-      }                                                                                     \
-    }                                                                                       \
-    if (!((full) && (k0) + BK <= n)) { /* mask in place, without branches per score */     \
-      if (!a.m.docs) {                                                                      \
-        const KeyRanges kr_ = key_ranges(a.m, qrow, n, (k0) + 4 * h, (full));               \
-        _Pragma("unroll") for (int i = 0; i < 32; ++i) {                                    \
-          const int j_ = i % 16;                                                            \
-          const int c_ = 32 * (i / 16) + 8 * (j_ / 4) + j_ % 4;                             \
-          const bool ok_ = (unsigned(c_ + kr_.a) <= unsigned(kr_.w)) | (c_ <= kr_.p);       \
-          sacc[i / 16][j_] = ok_ ? sacc[i / 16][j_] : -INFINITY;                            \
-        }                                                                                   \
-      } else {                                                                              \
-        const int64_t dq_ = a.m.docs[min(qrow, n - 1)];                                     \
-        _Pragma("unroll") for (int i = 0; i < 32; ++i) {                                    \
-          const int j_ = i % 16;                                                            \
-          const int key_ = (k0) + 32 * (i / 16) + 8 * (j_ / 4) + 4 * h + j_ % 4;           \
-          const int64_t dk_ = a.m.docs[min(key_, n - 1)];                                   \
-          const bool ok_ = (full) ? (key_ < n) & (qrow < n)                                 \
-                                  : allowed_flat(a.m, qrow, key_, n, dq_, dk_);            \
-          sacc[i / 16][j_] = ok_ ? sacc[i / 16][j_] : -INFINITY;                            \
-        }                                                                                   \
-      }                                                                                     \
-    }                                                                                       \
-    float mx_ = fmaxf(sacc[0][0], sacc[0][1]);                                              \
-    _Pragma("unroll") for (int i = 2; i < 32; i += 2)                                       \
-      mx_ = fmaxf(fmaxf(mx_, sacc[i / 16][i % 16]), sacc[i / 16][i % 16 + 1]);              \
-    mx_ = fmaxf(mx_, __shfl_xor(mx_, 32, kWave));                                           \
-    const float cs_ = a.scale_log2;                                                         \
-    const float m_new_ = fmaxf(m_run, mx_ * cs_);                                           \
-    const float ms_ = m_new_ == -INFINITY ? 0.f : m_new_;                                   \
-    const float alpha_ = __builtin_amdgcn_exp2f(m_run - ms_);                               \
-    m_run = m_new_;                                                                         \
-    u32x4 pop_[4];                                                                          \
-    float psum_ = 0.f;                                                                      \
-    _Pragma("unroll") for (int s2 = 0; s2 < 4; ++s2) {                                      \
-      uint32_t pk_[4];                                                                      \
-      _Pragma("unroll") for (int e = 0; e < 4; ++e) {                                       \
-        const int i0_ = 16 * (s2 / 2) + 8 * (s2 % 2) + 2 * e;                               \
-        pk_[e] = pack2<T>(__builtin_amdgcn_exp2f(fmaf(sacc[i0_ / 16][i0_ % 16], cs_, -ms_)),     \
-                          __builtin_amdgcn_exp2f(fmaf(sacc[i0_ / 16][i0_ % 16 + 1], cs_, -ms_))); \
-        psum_ = add_pair<T>(pk_[e], psum_);                                                 \
-      }                                                                                     \
-      pop_[s2] = u32x4{pk_[0], pk_[1], pk_[2], pk_[3]};                                     \
-    }                                                                                       \
-    l_run = l_run * alpha_ + psum_;                                                         \
-    if (__ballot(alpha_ != 1.f)) {                                                          \
-      _Pragma("unroll") for (int t = 0; t < 2; ++t) oacc[t] *= alpha_;                     \
-    }                                                                                       \
-    _Pragma("unroll") for (int s2 = 0; s2 < 4; ++s2) {                                      \
-      _Pragma("unroll") for (int t = 0; t < 2; ++t) {                                       \
-        const u32x4 vop_ = *reinterpret_cast<const u32x4*>(                                 \
-            &vt_s[buf][(32 * t + c) * LDV + 16 * s2 + 8 * h]);                              \
-        oacc[t] = mfma32<T>(vop_, pop_[s2], oacc[t]);                                       \
-      }                                                                                     \
-    }                                                                                       \
-  }
-
   if (count > 0) {
     int kb0;
     bool f0;
@@ -846,14 +859,16 @@ __global__ __launch_bounds__(kA32Waves * kWave) __attribute__((amdgpu_waves_per_
       (void)fn;                                                                             \
       SFL_A32_LOAD(kbn, buf ^ 1)                                                            \
     }                                                                                       \
-    SFL_A32_MATH(buf, k0, full)                                                             \
+    if (full && k0 + BK <= n)                                                               \
+      attn32_tile<T, false, LDV>(a, k_s[buf], vt_s[buf], qreg, oacc, m_run, l_run, c, h, qrow, k0, full); \
+    else                                                                                    \
+      attn32_tile<T, true, LDV>(a, k_s[buf], vt_s[buf], qreg, oacc, m_run, l_run, c, h, qrow, k0, full);  \
     if (more) SFL_A32_STORE_VT(buf ^ 1)                                                     \
     __builtin_amdgcn_s_waitcnt(sfl_vmcnt(0)); /* the next K tile has landed */              \
     __syncthreads();                                                                        \
   }
   for (int it = 0; it < count; ++it) SFL_A32_STEP(it)
 #undef SFL_A32_STEP
-#undef SFL_A32_MATH
 #undef SFL_A32_STORE_VT
 #undef SFL_A32_TILE_AT
 #undef SFL_A32_LOAD
