@@ -618,9 +618,14 @@ __device__ __forceinline__ KeyRanges key_ranges(const MaskArgs& m, int q, int n,
 // touches hit distinct banks; rows past the sequence read as zeros through the
 // buffer range check. O^T = V^T P^T: for the 16-key
 // step s the P^T operand of lane (c, h) is its own probabilities j = 8(s%2)
-// .. +7 of block s/2 (keys 16s + 4h + {0..3} and 16s + 8 + 4h + {0..3}), so
-// V^T is stored in LDS with the middle two key quads of every 16 swapped and
-// each V^T operand is one 16-byte read. The row sum comes from the packed
+// .. +7 of block s/2 (keys 16s + 4h + {0..3} and 16s + 8 + 4h + {0..3}). V
+// also goes global -> LDS directly, row-major (key rows, 32-byte units
+// XOR-swizzled by the row), and each V^T operand is assembled by two LDS
+// transpose reads (ds_read_b64_tr_b16): within each 16 lanes, lane 16g + i
+// receives element i%4 of the 8-byte pieces addressed by lanes
+// 16g + i/4 + 4k, k = 0..3, so lane 16g + m addresses key 16s + 4(g/2) + m/4
+// (+8 for the second read) at dims 32t + 16(g%2) + 4(m%4), and lane l ends
+// with dim 32t + l%32 of the 8 keys its P^T partner slots hold. The row sum comes from the packed
 // probabilities with dot2 (the sum of exactly the values the P V product
 // weights), kept per lane and added with the partner's at the end.
 typedef float f32x16 __attribute__((ext_vector_type(16)));
@@ -652,10 +657,29 @@ template <> __device__ __forceinline__ float add_pair<f16_t>(uint32_t pk, float 
 // swizzled K tile, the online softmax (masked when kMask), and O^T += V^T P^T.
 // Instantiated separately for full and masked tiles so each is straight-line
 // code.
-template <typename T, bool kMask, int LDV>
-__device__ __forceinline__ void attn32_tile(const AttnArgs& a, const uint4 (&kt)[BK][8], const uint16_t* vt,
+// V tile layout: row-major [key][8 slots of 16 bytes]; logical slot sg (dims
+// 8sg .. 8sg+7) of key row r sits at physical slot 2((sg >> 1) ^ (r & 3)) +
+// (sg & 1), so the 4 rows one 16-lane transpose read touches use 4 different
+// 32-byte bank groups.
+__device__ __forceinline__ unsigned vt_slot(unsigned sg, unsigned r) { return 2u * ((sg >> 1) ^ (r & 3u)) + (sg & 1u); }
+// Byte offset, within a tile, of lane l's 8-byte piece for key step 0, dim
+// tile t, first key half: key row 4(g >> 1) + (m >> 2), dims 32t + 16(g & 1) +
+// 4(m & 3) .. +3, with g = l / 16 and m = l % 16.
+__device__ __forceinline__ unsigned vt_lane_offset(int lane, int t) {
+  const unsigned g = unsigned(lane) / 16u, m = unsigned(lane) % 16u;
+  const unsigned r = 4u * (g >> 1) + (m >> 2);
+  const unsigned dim = 32u * unsigned(t) + 16u * (g & 1u) + 4u * (m & 3u);
+  return r * 128u + 16u * vt_slot(dim / 8u, r) + 2u * (dim % 8u);
+}
+
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i16x4_t lds_i16x4_t;
+
+template <typename T, bool kMask>
+__device__ __forceinline__ void attn32_tile(const AttnArgs& a, const uint4 (&kt)[BK][8], const uint4 (&vt)[BK][8],
                                             const u32x4 (&qreg)[4], f32x16 (&oacc)[2], float& m_run,
-                                            float& l_run, int c, int h, int qrow, int k0, bool full) {
+                                            float& l_run, int c, int h, int qrow, int k0, bool full,
+                                            unsigned vlane0, unsigned vlane1) {
   const int n = a.n;
   f32x16 sacc[2];
 #pragma unroll
@@ -690,9 +714,16 @@ __device__ __forceinline__ void attn32_tile(const AttnArgs& a, const uint4 (&kt)
       }
     }
   }
-  float mx = fmaxf(sacc[0][0], sacc[0][1]);
+  // Row max as a tree (short dependency chains): 32 -> 11 -> 4 -> 1.
+  float m1[11];
 #pragma unroll
-  for (int i = 2; i < 32; i += 2) mx = fmaxf(fmaxf(mx, sacc[i / 16][i % 16]), sacc[i / 16][i % 16 + 1]);
+  for (int g = 0; g < 10; ++g)
+    m1[g] = fmaxf(fmaxf(sacc[(3 * g) / 16][(3 * g) % 16], sacc[(3 * g + 1) / 16][(3 * g + 1) % 16]),
+                  sacc[(3 * g + 2) / 16][(3 * g + 2) % 16]);
+  m1[10] = fmaxf(sacc[1][14], sacc[1][15]);
+  const float m2a = fmaxf(fmaxf(m1[0], m1[1]), m1[2]), m2b = fmaxf(fmaxf(m1[3], m1[4]), m1[5]);
+  const float m2c = fmaxf(fmaxf(m1[6], m1[7]), m1[8]), m2d = fmaxf(m1[9], m1[10]);
+  float mx = fmaxf(fmaxf(m2a, m2b), fmaxf(m2c, m2d));
   mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
   const float cs = a.scale_log2;
   const float m_new = fmaxf(m_run, mx * cs);
@@ -700,7 +731,7 @@ __device__ __forceinline__ void attn32_tile(const AttnArgs& a, const uint4 (&kt)
   const float alpha = __builtin_amdgcn_exp2f(m_run - ms);
   m_run = m_new;
   u32x4 pop[4];
-  float psum = 0.f;
+  float psum[4] = {0.f, 0.f, 0.f, 0.f};  // one accumulator per key step: short dot2 chains
 #pragma unroll
   for (int s2 = 0; s2 < 4; ++s2) {
     uint32_t pk[4];
@@ -709,19 +740,27 @@ __device__ __forceinline__ void attn32_tile(const AttnArgs& a, const uint4 (&kt)
       const int i0 = 16 * (s2 / 2) + 8 * (s2 % 2) + 2 * e;
       pk[e] = pack2<T>(__builtin_amdgcn_exp2f(fmaf(sacc[i0 / 16][i0 % 16], cs, -ms)),
                        __builtin_amdgcn_exp2f(fmaf(sacc[i0 / 16][i0 % 16 + 1], cs, -ms)));
-      psum = add_pair<T>(pk[e], psum);
+      psum[s2] = add_pair<T>(pk[e], psum[s2]);
     }
     pop[s2] = u32x4{pk[0], pk[1], pk[2], pk[3]};
   }
-  l_run = l_run * alpha + psum;
+  l_run = l_run * alpha + ((psum[0] + psum[1]) + (psum[2] + psum[3]));
+  if (__ballot(alpha != 1.f)) {  // wave-uniform: skip the rescale once the maxima settle
 #pragma unroll
-  for (int t = 0; t < 2; ++t) oacc[t] *= alpha;
+    for (int t = 0; t < 2; ++t) oacc[t] *= alpha;
+  }
+  // V^T operands: this lane's piece for step s2, dim tile t and key half is
+  // at byte vlane_t + 2048 s2 + 1024 half of the tile (vt_lane_offset).
+  const unsigned vbase = unsigned(size_t((__attribute__((address_space(3))) const char*)(&vt[0][0])));
 #pragma unroll
   for (int s2 = 0; s2 < 4; ++s2) {
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
-      const u32x4 vop = *reinterpret_cast<const u32x4*>(&vt[(32 * t + c) * LDV + 16 * s2 + 8 * h]);
-      oacc[t] = mfma32<T>(vop, pop[s2], oacc[t]);
+      const unsigned off = vbase + (t ? vlane1 : vlane0) + 2048u * s2;
+      const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(size_t)(off));
+      const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(size_t)(off + 1024u));
+      const uint2 l2 = __builtin_bit_cast(uint2, lo), h2 = __builtin_bit_cast(uint2, hi);
+      oacc[t] = mfma32<T>(u32x4{l2.x, l2.y, h2.x, h2.y}, pop[s2], oacc[t]);
     }
   }
 }
@@ -731,9 +770,8 @@ constexpr int kA32Waves = 2;
 template <typename T>
 __global__ __launch_bounds__(kA32Waves * kWave) __attribute__((amdgpu_waves_per_eu(2))) void masked_attention32_kernel(AttnArgs a) {
   constexpr int D = 64;
-  constexpr int LDV = BK + kPadK;  // V^T row stride (elements)
-  __shared__ __align__(16) uint16_t vt_s[2][D * LDV];
   __shared__ __align__(16) uint4 k_s[2][BK][8];  // [key][16-byte slot s at s ^ (key & 7)]
+  __shared__ __align__(16) uint4 v_s[2][BK][8];  // [key][16-byte slot, see vt_slot]
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave), lane = tid % kWave;
   const int c = lane % 32, h = lane / 32;
@@ -788,17 +826,13 @@ __global__ __launch_bounds__(kA32Waves * kWave) __attribute__((amdgpu_waves_per_
   const unsigned krow_bytes = unsigned(a.ks[2]) * 2u;
   const i32x4_t krsrc = buffer_rsrc(kp, unsigned((long(n - 1) * a.ks[2] + D) * 2));
   const unsigned kvoff = unsigned(lane / 8) * krow_bytes + 16u * unsigned((lane % 8) ^ (lane / 8));
-  // V share of this thread: keys vr0 .. vr0+3, dims vd0 .. vd0+7 (128 threads
-  // cover 64 keys x 64 dims); its V^T column is vr0 with quads 1 and 2 of each
-  // 16 keys swapped.
-  const int vr0 = 4 * (tid % 16), vd0 = 8 * (tid / 16);
-  const int vquad = (vr0 >> 2) & 3;
-  const int vcol = (vr0 & ~15) | ((vquad == 1 ? 2 : vquad == 2 ? 1 : vquad) << 2);
+  // V tile: the same 8 loads of 8 rows; lane i moves row 8ch + i/8, logical
+  // slot sg with vt_slot(sg, i/8) == i%8, into physical slot i%8.
   const unsigned vrow_bytes = unsigned(a.vs[2]) * 2u;
-  const __amdgpu_buffer_rsrc_t vrsrc =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(vp), 0, int((long(n - 1) * a.vs[2] + D) * 2), 0x00020000);
-  const unsigned vvoff = unsigned(vr0) * vrow_bytes + unsigned(vd0) * 2u;
-  u32x4 vreg[4];
+  const i32x4_t vrsrc = buffer_rsrc(vp, unsigned((long(n - 1) * a.vs[2] + D) * 2));
+  const unsigned vpp = unsigned(lane % 8), vrr = unsigned(lane / 8);
+  const unsigned vvoff = vrr * vrow_bytes + 16u * (2u * ((vpp >> 1) ^ (vrr & 3u)) + (vpp & 1u));
+  const unsigned vlane0 = vt_lane_offset(lane, 0), vlane1 = vt_lane_offset(lane, 1);
 #define SFL_A32_LOAD(kb, kbuf)                                                              \
   {                                                                                         \
     const int k0_ = (kb) * BK;                                                              \
@@ -806,10 +840,9 @@ __global__ __launch_bounds__(kA32Waves * kWave) __attribute__((amdgpu_waves_per_
       const int ch_ = cw * kA32Waves + wave;                                                \
       lds_load16(krsrc, lds_offset(&k_s[kbuf][8 * ch_][0]), kvoff,                          \
                  unsigned(k0_ + 8 * ch_) * krow_bytes);                                     \
+      lds_load16(vrsrc, lds_offset(&v_s[kbuf][8 * ch_][0]), vvoff,                          \
+                 unsigned(k0_ + 8 * ch_) * vrow_bytes);                                     \
     }                                                                                       \
-    _Pragma("unroll") for (int u = 0; u < 4; ++u) /* rows past n read as zeros */           \
-      vreg[u] = __builtin_amdgcn_raw_buffer_load_b128(vrsrc, int(vvoff + unsigned(u) * vrow_bytes), \
-                                                      int(unsigned(k0_) * vrow_bytes), 0);  \
   }
 #define SFL_A32_TILE_AT(it, kb_, fl_)                                                       \
   if (a.s.mode == 1) {                                                                      \
@@ -819,19 +852,6 @@ __global__ __launch_bounds__(kA32Waves * kWave) __attribute__((amdgpu_waves_per_
     kb_ = (it) < lowg ? (it) : tb.begin + ((it) - lowg);                                    \
     fl_ = !a.m.docs && covered(tb, kb_ * BK, min(kb_ * BK + BK, n) - 1);                    \
   }
-#define SFL_A32_STORE_VT(buf)                                                               \
-  {                                                                                         \
-    const uint32_t w0_[4] = {vreg[0].x, vreg[0].y, vreg[0].z, vreg[0].w};                  \
-    const uint32_t w1_[4] = {vreg[1].x, vreg[1].y, vreg[1].z, vreg[1].w};                  \
-    const uint32_t w2_[4] = {vreg[2].x, vreg[2].y, vreg[2].z, vreg[2].w};                  \
-    const uint32_t w3_[4] = {vreg[3].x, vreg[3].y, vreg[3].z, vreg[3].w};                  \
-    _Pragma("unroll") for (int e = 0; e < 8; ++e) {                                         \
-      const uint32_t sel_ = (e & 1) ? 0x07060302u : 0x05040100u;                             \
-      const uint32_t k01_ = __builtin_amdgcn_perm(w1_[e / 2], w0_[e / 2], sel_);             \
-      const uint32_t k23_ = __builtin_amdgcn_perm(w3_[e / 2], w2_[e / 2], sel_);             \
-      *reinterpret_cast<uint2*>(&vt_s[buf][(vd0 + e) * LDV + vcol]) = make_uint2(k01_, k23_); \
-    }                                                                                       \
-  }
   // One key tile: S^T, masked online softmax, O^T += V^T P^T.
   if (count > 0) {
     int kb0;
@@ -839,7 +859,6 @@ __global__ __launch_bounds__(kA32Waves * kWave) __attribute__((amdgpu_waves_per_
     SFL_A32_TILE_AT(0, kb0, f0)
     (void)f0;
     SFL_A32_LOAD(kb0, 0)
-    SFL_A32_STORE_VT(0)
   }
   __builtin_amdgcn_s_waitcnt(sfl_vmcnt(0));
   __syncthreads();
@@ -860,16 +879,16 @@ __global__ __launch_bounds__(kA32Waves * kWave) __attribute__((amdgpu_waves_per_
       SFL_A32_LOAD(kbn, buf ^ 1)                                                            \
     }                                                                                       \
     if (full && k0 + BK <= n)                                                               \
-      attn32_tile<T, false, LDV>(a, k_s[buf], vt_s[buf], qreg, oacc, m_run, l_run, c, h, qrow, k0, full); \
+      attn32_tile<T, false>(a, k_s[buf], v_s[buf], qreg, oacc, m_run, l_run, c, h, qrow, k0, full, \
+                            vlane0, vlane1);                                                \
     else                                                                                    \
-      attn32_tile<T, true, LDV>(a, k_s[buf], vt_s[buf], qreg, oacc, m_run, l_run, c, h, qrow, k0, full);  \
-    if (more) SFL_A32_STORE_VT(buf ^ 1)                                                     \
-    __builtin_amdgcn_s_waitcnt(sfl_vmcnt(0)); /* the next K tile has landed */              \
+      attn32_tile<T, true>(a, k_s[buf], v_s[buf], qreg, oacc, m_run, l_run, c, h, qrow, k0, full, \
+                           vlane0, vlane1);                                                 \
+    __builtin_amdgcn_s_waitcnt(sfl_vmcnt(0)); /* the next K and V tiles have landed */      \
     __syncthreads();                                                                        \
   }
   for (int it = 0; it < count; ++it) SFL_A32_STEP(it)
 #undef SFL_A32_STEP
-#undef SFL_A32_STORE_VT
 #undef SFL_A32_TILE_AT
 #undef SFL_A32_LOAD
 
