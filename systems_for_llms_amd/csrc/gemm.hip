@@ -253,17 +253,18 @@ __device__ __forceinline__ f32x16 mfma32_bf16(const u32x4& a, const u32x4& b, f3
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
 }
 
+template <int TN_, int TM_>
 struct Stage32 {
-  uint4 w[TB][8];  // [row][swizzled 16-byte slot]
-  uint4 a[TB][8];
+  uint4 w[TN_][8];  // [row][swizzled 16-byte slot]
+  uint4 a[TM_][8];
 };
 
 // Tile of workgroup b in a 1-D grid of tn x tm tiles, XCD-aware: workgroups
 // are dealt to the 8 XCDs round-robin (b % 8) and each XCD has its own L2, so
 // XCD x is given a contiguous range of the tile order, and that order walks
-// groups of kGroupM token tiles across the feature tiles. The ~32 workgroups
-// an XCD runs at once then cover about 4 token tiles x 8 feature tiles, whose
-// operands (~3 MB) stay in its 4 MB L2.
+// groups of kGroupM token tiles across the feature tiles. The workgroups an
+// XCD runs at once then cover about 4 token tiles x 8 feature tiles, whose
+// operands stay in (or near) its 4 MB L2.
 constexpr int kXcds = 8;
 constexpr int kGroupM = 4;
 
@@ -279,22 +280,32 @@ __device__ __forceinline__ int2 xcd_tile(int b, int tn, int tm) {
   return make_int2(r / gsize, gm0 + r % gsize);  // (feature tile, token tile)
 }
 
-template <int E>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) void gemm32_kernel(GemmArgs g) {
-  // Distinct LDS objects per stage; see lds_load16 for why the loads are counted by hand.
-  __shared__ Stage32 st0, st1;
+// TBN x TBM tiles (features x tokens) per workgroup of WN x WM waves; a wave
+// owns (TBN/WN) x (TBM/WM) as blocks of 32 x 32. 128 x 128 with 2 x 2 waves:
+// two workgroups per CU (64 KB of LDS each), 64 x 64 per wave. 256 x 256 with
+// 4 x 2 waves: one workgroup of 8 waves per CU (128 KB), 64 x 128 per wave,
+// which reads 3/4 of the LDS operand bytes per MFMA of the 64 x 64 wave tile
+// and stages half the bytes per MFMA through LDS.
+template <int E, int TBN, int TBM, int WN, int WM>
+__global__ __launch_bounds__(64 * WN * WM) __attribute__((amdgpu_waves_per_eu(2)))
+void gemm32_kernel(GemmArgs g) {
+  constexpr int NW = WN * WM;              // waves
+  constexpr int NBN = TBN / WN / 32;       // 32x32 blocks per wave along features
+  constexpr int NBM = TBM / WM / 32;       // and along tokens
+  // Two LDS stages; see lds_load16 for why the loads are counted by hand.
+  __shared__ Stage32<TBN, TBM> st[2];
   const int tid = threadIdx.x;
   // readfirstlane: the wave index is uniform, so the LDS destinations live in scalar registers.
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave), lane = tid % kWave;
-  const int wn = wave / 2, wm = wave % 2;
+  const int wn = wave / WM, wm = wave % WM;
   const int l32 = lane % 32, hf = lane / 32;
-  const int2 tile = xcd_tile(blockIdx.x, (g.n + TB - 1) / TB, (g.m + TB - 1) / TB);
-  const int n0 = tile.x * TB;
-  const int m0 = tile.y * TB;
+  const int2 tile = xcd_tile(blockIdx.x, (g.n + TBN - 1) / TBN, (g.m + TBM - 1) / TBM);
+  const int n0 = tile.x * TBN;
+  const int m0 = tile.y * TBM;
   const int ksteps = g.k / K2;
 
-  // Loads: the 2 x 128 rows of a step are 32 chunks of 8 rows; wave w takes
-  // chunks w, w + 4, ... Lane i of a chunk moves row 8c + i/8 into slot i%8,
+  // Loads: the TBN + TBM rows of a step are chunks of 8 rows; wave w takes
+  // chunks w, w + NW, ... Lane i of a chunk moves row 8c + i/8 into slot i%8,
   // i.e. column (i%8) ^ ((row >> 1) & 7); the swizzle depends on the chunk's
   // parity only, so two byte offsets per lane cover every chunk.
   const i32x4_t rw = buffer_rsrc(g.w, unsigned(g.n * g.k * 2));
@@ -303,18 +314,19 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
   unsigned voff[2];
 #pragma unroll
   for (int par = 0; par < 2; ++par) voff[par] = unsigned((rr * g.k + 8 * (pos ^ ((4 * par + rr / 2) & 7))) * 2);
-  constexpr int CH = TB / 8;  // chunks per operand
+  constexpr int CHN = TBN / 8, CHM = TBM / 8;  // chunks per operand
+  static_assert((CHN + CHM) % NW == 0 && CHN % 2 == 0, "chunks per wave");
 
 #define SFL_G32_ISSUE(stage, kt)                                                            \
   {                                                                                         \
-    _Pragma("unroll") for (int c0 = 0; c0 < 2 * CH; c0 += 4) {                              \
+    _Pragma("unroll") for (int c0 = 0; c0 < CHN + CHM; c0 += NW) {                          \
       const int c = c0 + wave;                                                              \
-      if (c < CH)                                                                           \
+      if (c < CHN)                                                                          \
         lds_load16(rw, lds_offset(&stage.w[8 * c][0]), voff[c & 1],                         \
                    unsigned(((n0 + 8 * c) * g.k + (kt) * K2) * 2));                         \
       else                                                                                  \
-        lds_load16(ra, lds_offset(&stage.a[8 * (c - CH)][0]), voff[(c - CH) & 1],           \
-                   unsigned(((m0 + 8 * (c - CH)) * g.k + (kt) * K2) * 2));                  \
+        lds_load16(ra, lds_offset(&stage.a[8 * (c - CHN)][0]), voff[(c - CHN) & 1],         \
+                   unsigned(((m0 + 8 * (c - CHN)) * g.k + (kt) * K2) * 2));                 \
     }                                                                                       \
   }
   // Operand reads: lane (l32, hf) takes row 32t + l32, column 2kk + hf.
@@ -322,53 +334,49 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) v
 #define SFL_G32_COMPUTE(stage)                                                              \
   _Pragma("unroll") for (int kk = 0; kk < 4; ++kk) {                                        \
     const int slot = (2 * kk + hf) ^ sw;                                                    \
-    u32x4 af[2], bfr[2];                                                                    \
-    _Pragma("unroll") for (int t = 0; t < 2; ++t) {                                         \
-      const uint4 ra_ = stage.w[32 * (2 * wn + t) + l32][slot];                             \
-      const uint4 rb_ = stage.a[32 * (2 * wm + t) + l32][slot];                             \
+    u32x4 af[NBN], bfr[NBM];                                                                \
+    _Pragma("unroll") for (int t = 0; t < NBN; ++t) {                                       \
+      const uint4 ra_ = stage.w[32 * (NBN * wn + t) + l32][slot];                           \
       af[t] = u32x4{ra_.x, ra_.y, ra_.z, ra_.w};                                            \
+    }                                                                                       \
+    _Pragma("unroll") for (int t = 0; t < NBM; ++t) {                                       \
+      const uint4 rb_ = stage.a[32 * (NBM * wm + t) + l32][slot];                           \
       bfr[t] = u32x4{rb_.x, rb_.y, rb_.z, rb_.w};                                           \
     }                                                                                       \
-    _Pragma("unroll") for (int i = 0; i < 2; ++i)                                           \
-      _Pragma("unroll") for (int j = 0; j < 2; ++j) acc[i][j] = mfma32_bf16(af[i], bfr[j], acc[i][j]); \
+    _Pragma("unroll") for (int i = 0; i < NBN; ++i)                                         \
+      _Pragma("unroll") for (int j = 0; j < NBM; ++j) acc[i][j] = mfma32_bf16(af[i], bfr[j], acc[i][j]); \
   }
 
-  f32x16 acc[2][2];
+  f32x16 acc[NBN][NBM];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < NBN; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < NBM; ++j)
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
-  // Two LDS stages (64 KB, two workgroups per CU): step kt computes from one
-  // stage while the loads of step kt+1 fill the other; unrolled twice so both
-  // stages are compile-time objects.
-  SFL_G32_ISSUE(st0, 0)
-#define SFL_G32_STEP(kt, cur, next)                                                         \
-  {                                                                                         \
-    __builtin_amdgcn_s_waitcnt(sfl_vmcnt(0));                                               \
-    __syncthreads(); /* every wave's loads of `cur` landed; `next` is no longer read */    \
-    if ((kt) + 1 < ksteps) SFL_G32_ISSUE(next, (kt) + 1)                                    \
-    SFL_G32_COMPUTE(cur)                                                                    \
+  // Two LDS stages: step kt computes from stage kt & 1 while the loads of
+  // step kt+1 fill the other. One loop body, so every accumulator keeps its
+  // registers across iterations.
+  SFL_G32_ISSUE(st[0], 0)
+  for (int kt = 0; kt < ksteps; ++kt) {
+    __builtin_amdgcn_s_waitcnt(sfl_vmcnt(0));
+    __syncthreads();  // every wave's loads of this stage landed; the other is no longer read
+    if (kt + 1 < ksteps) SFL_G32_ISSUE(st[(kt + 1) & 1], kt + 1)
+    SFL_G32_COMPUTE(st[kt & 1])
   }
-  for (int kt = 0; kt < ksteps; kt += 2) {
-    SFL_G32_STEP(kt, st0, st1)
-    if (kt + 1 >= ksteps) break;
-    SFL_G32_STEP(kt + 1, st1, st0)
-  }
-#undef SFL_G32_STEP
 #undef SFL_G32_COMPUTE
 #undef SFL_G32_ISSUE
 
-  // acc[i][j][4q + e] holds feature n0 + 64wn + 32i + 8q + 4hf + e of token m0 + 64wm + 32j + l32.
+  // acc[i][j][4q + e] holds feature n0 + (TBN/WN)wn + 32i + 8q + 4hf + e of
+  // token m0 + (TBM/WM)wm + 32j + l32.
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int m = m0 + 64 * wm + 32 * j + l32;
+  for (int j = 0; j < NBM; ++j) {
+    const int m = m0 + (TBM / WM) * wm + 32 * j + l32;
     const QkvTok tok = E == G_QKV ? qkv_tok(g, m) : QkvTok{};
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int nt = n0 + 64 * wn + 32 * i;
+    for (int i = 0; i < NBN; ++i) {
+      const int nt = n0 + (TBN / WN) * wn + 32 * i;
       if constexpr (E == G_SWIGLU) {
         // W1/W3 interleaved in blocks of 8 rows: groups q = 0, 2 are W1 features,
         // q + 1 the matching W3 features, all in this lane.
@@ -406,7 +414,12 @@ int launch_gemm(const GemmArgs& g, hipStream_t s, const char* what) {
   if (g.k % K2 == 0 && long(g.m) * g.k < (1L << 30) && long(g.n) * g.k < (1L << 30)) {
     const long tiles = long((g.n + TB - 1) / TB) * ((g.m + TB - 1) / TB);
     if (tiles > (1L << 31) - 1) return set_error(SFL_ERR_UNSUPPORTED, "%s: too many tiles", what);
-    hipLaunchKernelGGL((gemm32_kernel<E>), dim3(unsigned(tiles)), dim3(kThreads), 0, s, g);
+    // 256 x 256 tiles where they still give every CU several workgroups.
+    const long big = long((g.n + 255) / 256) * ((g.m + 255) / 256);
+    if (big >= 512)
+      hipLaunchKernelGGL((gemm32_kernel<E, 256, 256, 4, 2>), dim3(unsigned(big)), dim3(512), 0, s, g);
+    else
+      hipLaunchKernelGGL((gemm32_kernel<E, 128, 128, 2, 2>), dim3(unsigned(tiles)), dim3(kThreads), 0, s, g);
     return check_launch(what);
   }
   dim3 grid((g.n + TN - 1) / TN, (g.m + TM - 1) / TM);
