@@ -452,6 +452,41 @@ __global__ __launch_bounds__(256) void rmsnorm_rows_kernel(const float* x, const
   for (int i = threadIdx.x; i < d; i += 256) out[m * d + i] = f32_to_bf16_bits((xr[i] * inv) * load_scalar<T>(w + i));
 }
 
+// The same for rows of d % 4 == 0 and d <= 4 * 64 * kNormVec with one wave per
+// row: the row is read once with 16-byte loads and kept in registers, the sum
+// of squares is a wave reduction (no LDS, no barrier), and each lane stores
+// four bf16 values at a time.
+constexpr int kNormVec = 8;
+template <typename T>
+__global__ __launch_bounds__(256) void rmsnorm_rows_wave_kernel(const float* x, const T* w, uint16_t* out, int m,
+                                                               int d) {
+  const long row = long(blockIdx.x) * 4 + threadIdx.x / kWave;
+  const int lane = threadIdx.x % kWave;
+  if (row >= m) return;
+  const float* xr = x + row * d;
+  float4 v[kNormVec];
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < kNormVec; ++j) {
+    const int i = 4 * (j * kWave + lane);
+    v[j] = i < d ? *reinterpret_cast<const float4*>(xr + i) : make_float4(0.f, 0.f, 0.f, 0.f);
+    ss = fmaf(v[j].x, v[j].x, ss);
+    ss = fmaf(v[j].y, v[j].y, ss);
+    ss = fmaf(v[j].z, v[j].z, ss);
+    ss = fmaf(v[j].w, v[j].w, ss);
+  }
+  const float inv = 1.f / sqrtf(wave_sum(ss) / float(d) + 1e-5f);
+#pragma unroll
+  for (int j = 0; j < kNormVec; ++j) {
+    const int i = 4 * (j * kWave + lane);
+    if (i < d) {
+      const float y0 = (v[j].x * inv) * load_scalar<T>(w + i), y1 = (v[j].y * inv) * load_scalar<T>(w + i + 1);
+      const float y2 = (v[j].z * inv) * load_scalar<T>(w + i + 2), y3 = (v[j].w * inv) * load_scalar<T>(w + i + 3);
+      *reinterpret_cast<uint2*>(out + row * d + i) = make_uint2(pack_bf16(y0, y1), pack_bf16(y2, y3));
+    }
+  }
+}
+
 }  // namespace
 }  // namespace sfl
 
@@ -519,14 +554,26 @@ extern "C" int sfl_rmsnorm_rows(const float* x, const void* w, void* out_bf16, i
                                 void* stream) {
   if (!x || !w || !out_bf16) return set_error(SFL_ERR_INVALID, "rmsnorm_rows: null pointer argument");
   if (m < 1 || d_model < 1) return set_error(SFL_ERR_INVALID, "rmsnorm_rows: sizes must be positive");
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  if (dtype == SFL_DTYPE_BF16)
-    hipLaunchKernelGGL(rmsnorm_rows_kernel<bf16_t>, dim3(m), dim3(256), 0, s, x, static_cast<const bf16_t*>(w),
-                       static_cast<uint16_t*>(out_bf16), d_model);
-  else if (dtype == SFL_DTYPE_F32)
-    hipLaunchKernelGGL(rmsnorm_rows_kernel<float>, dim3(m), dim3(256), 0, s, x, static_cast<const float*>(w),
-                       static_cast<uint16_t*>(out_bf16), d_model);
-  else
+  if (dtype != SFL_DTYPE_BF16 && dtype != SFL_DTYPE_F32)
     return set_error(SFL_ERR_UNSUPPORTED, "rmsnorm_rows: dtype must be F32 or BF16");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  uint16_t* out = static_cast<uint16_t*>(out_bf16);
+  const bool wave_rows = d_model % 4 == 0 && d_model <= 4 * kWave * kNormVec &&
+                         reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(out) % 8 == 0;
+  if (wave_rows) {
+    const dim3 grid((m + 3) / 4);
+    if (dtype == SFL_DTYPE_BF16)
+      hipLaunchKernelGGL(rmsnorm_rows_wave_kernel<bf16_t>, grid, dim3(256), 0, s, x, static_cast<const bf16_t*>(w),
+                         out, m, d_model);
+    else
+      hipLaunchKernelGGL(rmsnorm_rows_wave_kernel<float>, grid, dim3(256), 0, s, x, static_cast<const float*>(w), out,
+                         m, d_model);
+  } else if (dtype == SFL_DTYPE_BF16) {
+    hipLaunchKernelGGL(rmsnorm_rows_kernel<bf16_t>, dim3(m), dim3(256), 0, s, x, static_cast<const bf16_t*>(w), out,
+                       d_model);
+  } else {
+    hipLaunchKernelGGL(rmsnorm_rows_kernel<float>, dim3(m), dim3(256), 0, s, x, static_cast<const float*>(w), out,
+                       d_model);
+  }
   return check_launch("rmsnorm_rows");
 }

@@ -34,6 +34,28 @@ def test_gemm_matches_fp32_matmul(m, n, k):
     torch.testing.assert_close(ob.float().cpu(), ref.bfloat16().float(), atol=1e-2, rtol=1e-2)
 
 
+# d % 4 == 0 and d <= 2048 take the one-wave-per-row kernel (m not a multiple
+# of its 4 rows per workgroup included); other widths the workgroup-per-row one.
+@pytest.mark.parametrize("m,d", [(1, 64), (7, 96), (130, 1024), (33, 2048), (5, 2052), (9, 1030)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_rmsnorm_rows_matches_reference(m, d, dtype):
+    g = torch.Generator().manual_seed(m * d)
+    x = torch.randn((m, d), generator=g) * 3
+    w = (1 + 0.5 * torch.randn(d, generator=g)).to(dtype)
+    xd, wd = x.cuda(), w.cuda()
+    out = torch.zeros((m + 1, d), device="cuda", dtype=torch.bfloat16)  # one guard row
+    _lib.call("sfl_rmsnorm_rows", xd.data_ptr(), wd.data_ptr(), out.data_ptr(), m, d, _lib.dtype_code(dtype),
+              _lib.stream_handle())
+    x64 = x.double()
+    ref = (x64 / torch.sqrt(x64.pow(2).mean(-1, keepdim=True) + 1e-5) * w.double()).float()
+    got = out[:m].float().cpu()
+    # One bf16 rounding of a value computed in fp32: half an ulp plus fp32 noise.
+    torch.testing.assert_close(got, ref, atol=1e-6, rtol=2 ** -8 + 1e-6)
+    # Nearly every value is exactly the bf16 rounding of the reference (the rest sit on a rounding tie).
+    assert (got == ref.bfloat16().float()).float().mean().item() > 0.99
+    assert not out[m].any(), "wrote past the last row"
+
+
 def gpu_model(cfg, sd):
     model = TransformerLM.from_config(cfg, device="cuda", dtype=torch.bfloat16)
     model.load_state_dict(sd)
