@@ -14,7 +14,7 @@ Differences, all documented widenings:
   supported by both implementations;
 * head dimension 32 is accepted besides 64 and 128;
 * ``num_warps`` and ``num_stages`` are validated as in the reference but do
-  not change the kernel (4 waves of 64 lanes, one key tile in flight);
+  not change the kernel (the launch shape is fixed per head dimension);
 * ``q``, ``k`` and ``v`` may be strided views whose last dimension is
   contiguous (the model passes K/V straight out of its KV cache).
 """
@@ -34,7 +34,27 @@ INT32_MAX = (1 << 31) - 1
 
 
 def _validated_schedule(schedule):
-    """Structural validation of a schedule (``triton_attention.py:60-97``)."""
+    """Structural validation of a schedule (``triton_attention.py:60-97``).
+
+    Returns ``(row_ptr, col_idx, full_blocks)`` as tuples. The check walks every
+    entry in Python (~0.2 ms for a 4096-token schedule), so its result is cached
+    on the schedule's contents together with the types of its entries (``True
+    == 1`` and both hash alike, so a cache on the values alone would let a bool
+    entry through); a schedule mutated in place is therefore checked again.
+    """
+    scalars = (schedule.length, schedule.block_q, schedule.block_k)
+    row_ptr, col_idx, full = tuple(schedule.row_ptr), tuple(schedule.col_idx), tuple(schedule.full_blocks)
+    key = (scalars, row_ptr, col_idx, full, tuple(map(type, scalars)), frozenset(map(type, row_ptr)),
+           frozenset(map(type, col_idx)), frozenset(map(type, full)))
+    try:
+        hash(key)
+    except TypeError:  # an unhashable entry: let the full check name it
+        return _check_schedule(*key)
+    return _checked_schedule(*key)
+
+
+def _check_schedule(scalars, row_ptr, col_idx, full, *_types):
+    length, block_q, block_k = scalars
 
     def integer(name, value, minimum=0):
         if isinstance(value, bool) or not isinstance(value, int):
@@ -42,21 +62,19 @@ def _validated_schedule(schedule):
         if value < minimum or value > INT32_MAX:
             raise ValueError(f"{name} must be in [{minimum}, {INT32_MAX}]")
 
-    integer("schedule.length", schedule.length, 1)
-    integer("schedule.block_q", schedule.block_q, 1)
-    integer("schedule.block_k", schedule.block_k, 1)
-    block_q, block_k = schedule.block_q, schedule.block_k
+    integer("schedule.length", length, 1)
+    integer("schedule.block_q", block_q, 1)
+    integer("schedule.block_k", block_k, 1)
     if block_q not in (16, 32, 64, 128) or block_k not in (16, 32, 64, 128):
         raise ValueError("block_q and block_k must each be one of 16, 32, 64, 128")
-    row_ptr, col_idx, full = tuple(schedule.row_ptr), tuple(schedule.col_idx), tuple(schedule.full_blocks)
     for value in row_ptr:
         integer("row_ptr entry", value)
     for value in col_idx:
         integer("col_idx entry", value)
     if any(not isinstance(flag, bool) for flag in full):
         raise TypeError("full_blocks entries must be bool values")
-    query_blocks = -(-schedule.length // block_q)
-    key_blocks = -(-schedule.length // block_k)
+    query_blocks = -(-length // block_q)
+    key_blocks = -(-length // block_k)
     if (len(row_ptr) != query_blocks + 1 or not row_ptr or row_ptr[0] != 0
             or row_ptr[-1] != len(col_idx) or len(full) != len(col_idx)
             or any(x > y for x, y in zip(row_ptr, row_ptr[1:]))
@@ -67,6 +85,9 @@ def _validated_schedule(schedule):
         if tuple(sorted(set(columns))) != columns:
             raise ValueError("CSR columns must be sorted and unique in each row")
     return row_ptr, col_idx, full
+
+
+_checked_schedule = lru_cache(maxsize=32)(_check_schedule)
 
 
 @lru_cache(maxsize=32)
@@ -166,8 +187,9 @@ def attention(q, k, v, schedule, spec, document_ids=None, num_warps=4, num_stage
 
     if implementation == "csr":
         sched = _kernel_schedule(schedule, spec, doc_list, length)
-        rows, cols, fulls = _upload_schedule(str(q.device), tuple(sched.row_ptr), tuple(sched.col_idx),
-                                             tuple(sched.full_blocks))
+        csr = (row_ptr, col_idx, full) if sched is schedule else \
+            (tuple(sched.row_ptr), tuple(sched.col_idx), tuple(sched.full_blocks))
+        rows, cols, fulls = _upload_schedule(str(q.device), *csr)
         mode, ptrs = 1, (rows.data_ptr(), cols.data_ptr(), fulls.data_ptr())
     else:
         mode, ptrs = 0, (None, None, None)

@@ -19,6 +19,8 @@
 // operand is exactly the probabilities the lane already holds (the product is
 // a sum over keys, so any order both operands share is exact), and V^T rows
 // come from LDS as 8-byte runs.
+#include <climits>
+
 #include "lds_dma.hpp"
 
 namespace sfl {
@@ -73,6 +75,27 @@ struct Sched {
   const int32_t* row_ptr;
   const int32_t* col_idx;
   const uint8_t* full;
+};
+
+// The CSR entries of one query tile's row, 64 at a time in one VGPR: lane l
+// holds entry first + l as 2 * column + full flag. A key tile's entry is then
+// a readlane instead of a memory round trip in front of every tile's loads;
+// the window moves (one load) every 64 tiles. `it` must be wave-uniform.
+struct RowSched {
+  const int32_t* col;
+  const uint8_t* full;
+  int count, first, reg;
+  __device__ __forceinline__ void fetch(int f) {
+    first = f;
+    const int i = f + int(threadIdx.x % kWave);
+    reg = i < count ? 2 * col[i] + int(full[i] != 0) : 0;
+  }
+  __device__ __forceinline__ void at(int it, int& kb, bool& fl) {
+    if ((it & ~63) != first) fetch(it & ~63);
+    const int e = __builtin_amdgcn_readlane(reg, it & 63);
+    kb = e >> 1;
+    fl = (e & 1) != 0;
+  }
 };
 
 struct AttnArgs {
@@ -211,13 +234,14 @@ __global__ __launch_bounds__(kThreads) void masked_attention_kernel(AttnArgs a) 
     count = lowg + max(0, max(tb.end, tb.gend) - tb.begin);
   }
   const int lowg = min(tb.gend, tb.begin);
+  RowSched rs{a.s.col_idx + base, a.s.full + base, count, 0, 0};
+  if (a.s.mode == 1) rs.fetch(0);
 
   for (int it = 0; it < count; ++it) {
     int kb;
     bool full;
     if (a.s.mode == 1) {
-      kb = a.s.col_idx[base + it];
-      full = a.s.full[base + it] != 0;
+      rs.at(it, kb, full);
     } else {
       kb = it < lowg ? it : tb.begin + (it - lowg);
       full = !a.m.docs && covered(tb, kb * BK, min(kb * BK + BK, n) - 1);
@@ -477,6 +501,8 @@ __global__ __launch_bounds__(kPairWaves * kWave) __attribute__((amdgpu_waves_per
     count = lowg + max(0, max(tb.end, tb.gend) - tb.begin);
   }
   const int lowg = min(tb.gend, tb.begin);
+  RowSched rs{a.s.col_idx + base, a.s.full + base, count, 0, 0};
+  if (a.s.mode == 1) rs.fetch(0);
 
   // Per tile at key block kb: K operands of key subtile j (keys 16j + col),
   // and this thread's share of V: rows 4*(tid % 16) + u (u < 4), dims
@@ -499,8 +525,7 @@ __global__ __launch_bounds__(kPairWaves * kWave) __attribute__((amdgpu_waves_per
   }
 #define SFL_TILE_AT(it, kb_, fl_)                                                           \
   if (a.s.mode == 1) {                                                                      \
-    kb_ = a.s.col_idx[base + (it)];                                                         \
-    fl_ = a.s.full[base + (it)] != 0;                                                       \
+    rs.at((it), kb_, fl_);                                                                  \
   } else {                                                                                  \
     kb_ = (it) < lowg ? (it) : tb.begin + ((it) - lowg);                                    \
     fl_ = !a.m.docs && covered(tb, kb_ * BK, min(kb_ * BK + BK, n) - 1);                    \
@@ -765,26 +790,93 @@ __device__ __forceinline__ void attn32_tile(const AttnArgs& a, const uint4 (&kt)
   }
 }
 
-constexpr int kA32Waves = 2;
+// The key tiles of one 64-query row of the schedule in increasing order: the
+// CSR row (mode 1) or the interval row (global blocks [0, lowg), then window
+// blocks [begin, end)). A row that starts past the sequence has none.
+struct TileRow {
+  RowSched rs;
+  TileBounds tb;
+  int lowg, count, i;
+  __device__ __forceinline__ void init(const AttnArgs& a, int row) {
+    const int n = a.n, q0 = row * BQ;
+    const bool live = q0 < n;
+    tb = tile_bounds(a.m, n, q0, min(q0 + BQ, n) - 1);
+    lowg = min(tb.gend, tb.begin);
+    int base = 0;
+    if (!live) {
+      count = 0;
+    } else if (a.s.mode == 1) {
+      base = __builtin_amdgcn_readfirstlane(a.s.row_ptr[row]);
+      count = __builtin_amdgcn_readfirstlane(a.s.row_ptr[row + 1]) - base;
+    } else {
+      count = lowg + max(0, max(tb.end, tb.gend) - tb.begin);
+    }
+    rs = RowSched{a.s.col_idx + base, a.s.full + base, count, 0, 0};
+    if (a.s.mode == 1 && live) rs.fetch(0);
+    i = 0;
+  }
+  // The next tile's key block (INT_MAX when the row is done) and full flag.
+  __device__ __forceinline__ int peek(const AttnArgs& a, bool& full) {
+    if (i >= count) {
+      full = false;
+      return INT_MAX;
+    }
+    int kb;
+    if (a.s.mode == 1) {
+      rs.at(i, kb, full);
+    } else {
+      kb = i < lowg ? i : tb.begin + (i - lowg);
+      full = !a.m.docs && covered(tb, kb * BK, min(kb * BK + BK, a.n) - 1);
+    }
+    return kb;
+  }
+};
 
+// One key tile of a 128-query workgroup: its block and, for each 64-query
+// half, whether the half's row lists it and whether it is fully admissible.
+struct MergedTile {
+  int kb;
+  bool in[2], full[2];
+};
+__device__ __forceinline__ MergedTile next_tile(const AttnArgs& a, TileRow (&rows)[2]) {
+  MergedTile t;
+  const int c0 = rows[0].peek(a, t.full[0]);
+  const int c1 = rows[1].peek(a, t.full[1]);
+  t.kb = min(c0, c1);
+  t.in[0] = c0 == t.kb && c0 != INT_MAX;
+  t.in[1] = c1 == t.kb && c1 != INT_MAX;
+  rows[0].i += t.in[0];
+  rows[1].i += t.in[1];
+  return t;
+}
+
+constexpr int kA32Waves = 4;
+
+// 4 waves, 128 queries (two 64-query rows of the schedule) per workgroup: the
+// waves share each K/V tile in LDS, so a tile's global -> LDS traffic serves
+// 128 queries, and the 32 KB of double-buffered tiles per 4 waves leaves the
+// register file, not LDS, to bound the waves per CU. The workgroup walks the
+// merge of its two rows' tile lists; a wave skips (but still synchronises on)
+// a tile its own row does not list, so each row processes exactly its own
+// tiles, as the 64-query tiling would.
 template <typename T>
-__global__ __launch_bounds__(kA32Waves * kWave) __attribute__((amdgpu_waves_per_eu(2))) void masked_attention32_kernel(AttnArgs a) {
-  constexpr int D = 64;
+__global__ __launch_bounds__(kA32Waves * kWave) __attribute__((amdgpu_waves_per_eu(3))) void masked_attention32_kernel(AttnArgs a) {
+  constexpr int D = 64, QB = 2 * BQ;
   __shared__ __align__(16) uint4 k_s[2][BK][8];  // [key][16-byte slot s at s ^ (key & 7)]
   __shared__ __align__(16) uint4 v_s[2][BK][8];  // [key][16-byte slot, see vt_slot]
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave), lane = tid % kWave;
+  const int half = wave / 2;
   const int c = lane % 32, h = lane / 32;
   const int n = a.n;
   // Tile indices, schedule entries and key offsets are wave-uniform; keeping
   // them in scalar registers keeps their loads off the vector memory counter,
   // which would otherwise make the math wait for the next tile's prefetch.
-  const int2 tile = attn_tile((a.n + BQ - 1) / BQ, a.batch * a.heads);
+  const int2 tile = attn_tile((a.n + QB - 1) / QB, a.batch * a.heads);
   const int qt = __builtin_amdgcn_readfirstlane(tile.x);
   const int bh = __builtin_amdgcn_readfirstlane(tile.y);
   const int b = bh / a.heads, hd = bh % a.heads;
-  const int q0 = qt * BQ;
-  const int q1 = min(q0 + BQ, n) - 1;
+  const int q0 = qt * QB;
   const int qrow = q0 + 32 * wave + c;  // this lane's query
 
   const uint16_t* qp = static_cast<const uint16_t*>(a.q) + b * a.qs[0] + hd * a.qs[1];
@@ -809,18 +901,11 @@ __global__ __launch_bounds__(kA32Waves * kWave) __attribute__((amdgpu_waves_per_
 #pragma unroll
     for (int j = 0; j < 16; ++j) oacc[t][j] = 0.f;
 
-  const TileBounds tb = tile_bounds(a.m, n, q0, q1);
-  int count, base = 0;
-  if (a.s.mode == 1) {
-    base = __builtin_amdgcn_readfirstlane(a.s.row_ptr[qt]);
-    count = __builtin_amdgcn_readfirstlane(a.s.row_ptr[qt + 1]) - base;
-  } else {
-    const int lowg = min(tb.gend, tb.begin);
-    count = lowg + max(0, max(tb.end, tb.gend) - tb.begin);
-  }
-  const int lowg = min(tb.gend, tb.begin);
+  TileRow rows[2];
+  rows[0].init(a, 2 * qt);
+  rows[1].init(a, 2 * qt + 1);
 
-  // K tile: 8 loads of 8 rows (1 KB) per tile, 4 per wave; lane i moves row
+  // K tile: 8 loads of 8 rows (1 KB) per tile, 2 per wave; lane i moves row
   // 8ch + i/8, logical slot (i%8) ^ (i/8) into physical slot i%8. The buffer
   // covers this head's rows [0, n): rows past n read as zeros.
   const unsigned krow_bytes = unsigned(a.ks[2]) * 2u;
@@ -844,52 +929,28 @@ __global__ __launch_bounds__(kA32Waves * kWave) __attribute__((amdgpu_waves_per_
                  unsigned(k0_ + 8 * ch_) * vrow_bytes);                                     \
     }                                                                                       \
   }
-#define SFL_A32_TILE_AT(it, kb_, fl_)                                                       \
-  if (a.s.mode == 1) {                                                                      \
-    kb_ = __builtin_amdgcn_readfirstlane(a.s.col_idx[base + (it)]);                         \
-    fl_ = __builtin_amdgcn_readfirstlane(int(a.s.full[base + (it)])) != 0;                  \
-  } else {                                                                                  \
-    kb_ = (it) < lowg ? (it) : tb.begin + ((it) - lowg);                                    \
-    fl_ = !a.m.docs && covered(tb, kb_ * BK, min(kb_ * BK + BK, n) - 1);                    \
-  }
   // One key tile: S^T, masked online softmax, O^T += V^T P^T.
-  if (count > 0) {
-    int kb0;
-    bool f0;
-    SFL_A32_TILE_AT(0, kb0, f0)
-    (void)f0;
-    SFL_A32_LOAD(kb0, 0)
-  }
+  MergedTile cur = next_tile(a, rows);
+  if (cur.kb != INT_MAX) SFL_A32_LOAD(cur.kb, 0)
   __builtin_amdgcn_s_waitcnt(sfl_vmcnt(0));
   __syncthreads();
-#define SFL_A32_STEP(it)                                                                    \
-  {                                                                                         \
-    int kb;                                                                                 \
-    bool full;                                                                              \
-    SFL_A32_TILE_AT(it, kb, full)                                                           \
-    full = full && a.s.use_full;                                                            \
-    const int k0 = kb * BK;                                                                 \
-    const int buf = (it) & 1;                                                               \
-    const bool more = (it) + 1 < count;                                                     \
-    if (more) {                                                                             \
-      int kbn;                                                                              \
-      bool fn;                                                                              \
-      SFL_A32_TILE_AT((it) + 1, kbn, fn)                                                    \
-      (void)fn;                                                                             \
-      SFL_A32_LOAD(kbn, buf ^ 1)                                                            \
-    }                                                                                       \
-    if (full && k0 + BK <= n)                                                               \
-      attn32_tile<T, false>(a, k_s[buf], v_s[buf], qreg, oacc, m_run, l_run, c, h, qrow, k0, full, \
-                            vlane0, vlane1);                                                \
-    else                                                                                    \
-      attn32_tile<T, true>(a, k_s[buf], v_s[buf], qreg, oacc, m_run, l_run, c, h, qrow, k0, full, \
-                           vlane0, vlane1);                                                 \
-    __builtin_amdgcn_s_waitcnt(sfl_vmcnt(0)); /* the next K and V tiles have landed */      \
-    __syncthreads();                                                                        \
+  for (int buf = 0; cur.kb != INT_MAX; buf ^= 1) {
+    const MergedTile nxt = next_tile(a, rows);
+    if (nxt.kb != INT_MAX) SFL_A32_LOAD(nxt.kb, buf ^ 1)
+    const int k0 = cur.kb * BK;
+    const bool full = (half ? cur.full[1] : cur.full[0]) && a.s.use_full;
+    if (half ? cur.in[1] : cur.in[0]) {
+      if (full && k0 + BK <= n)
+        attn32_tile<T, false>(a, k_s[buf], v_s[buf], qreg, oacc, m_run, l_run, c, h, qrow, k0, full, vlane0,
+                              vlane1);
+      else
+        attn32_tile<T, true>(a, k_s[buf], v_s[buf], qreg, oacc, m_run, l_run, c, h, qrow, k0, full, vlane0,
+                             vlane1);
+    }
+    __builtin_amdgcn_s_waitcnt(sfl_vmcnt(0));  // the next K and V tiles have landed
+    __syncthreads();
+    cur = nxt;
   }
-  for (int it = 0; it < count; ++it) SFL_A32_STEP(it)
-#undef SFL_A32_STEP
-#undef SFL_A32_TILE_AT
 #undef SFL_A32_LOAD
 
   const float l_tot = l_run + __shfl_xor(l_run, 32, kWave);
@@ -915,9 +976,11 @@ int launch_masked(const AttnArgs& a, int batch, int dim, hipStream_t stream) {
   switch (dim) {
     case 32: hipLaunchKernelGGL((masked_attention_kernel<T, 32>), grid, dim3(kThreads), 0, stream, a); break;
     case 64:
-      // The 32x32 kernel addresses K and V with 32-bit buffer offsets.
+      // The 32x32 kernel addresses K and V with 32-bit buffer offsets; its
+      // workgroups take two 64-query rows each.
       if (long(a.n) * a.ks[2] * 2 < (1L << 31) && long(a.n) * a.vs[2] * 2 < (1L << 31))
-        hipLaunchKernelGGL((masked_attention32_kernel<T>), grid, dim3(kA32Waves * kWave), 0, stream, a);
+        hipLaunchKernelGGL((masked_attention32_kernel<T>), dim3(unsigned((a.n + 2 * BQ - 1) / (2 * BQ)) *
+                           unsigned(batch * a.heads)), dim3(kA32Waves * kWave), 0, stream, a);
       else
         hipLaunchKernelGGL((masked_attention_pair_kernel<T>), grid, dim3(kPairWaves * kWave), 0, stream, a);
       break;
