@@ -639,8 +639,9 @@ __device__ __forceinline__ KeyRanges key_ranges(const MaskArgs& m, int q, int n,
 // contraction is exact in any order both operands share), so a lane reads 64
 // contiguous bytes of its key or query row. K tiles go global -> LDS by
 // buffer loads that write LDS directly (no registers), rows stored with their
-// 16-byte slots XOR-swizzled by the row so that the 32 rows an operand read
-// touches hit distinct banks; rows past the sequence read as zeros through the
+// 16-byte slots XOR-swizzled by (row >> 1) & 7 so that the 32 rows an operand
+// read touches hit distinct banks (with row & 7 the 128-bit reads measured
+// 2-way conflicts on gfx950); rows past the sequence read as zeros through the
 // buffer range check. O^T = V^T P^T: for the 16-key
 // step s the P^T operand of lane (c, h) is its own probabilities j = 8(s%2)
 // .. +7 of block s/2 (keys 16s + 4h + {0..3} and 16s + 8 + 4h + {0..3}). V
@@ -700,6 +701,8 @@ __device__ __forceinline__ unsigned vt_lane_offset(int lane, int t) {
 typedef short i16x4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) i16x4_t lds_i16x4_t;
 
+constexpr float kLazyMax = 8.f;
+
 template <typename T, bool kMask>
 __device__ __forceinline__ void attn32_tile(const AttnArgs& a, const uint4 (&kt)[BK][8], const uint4 (&vt)[BK][8],
                                             const u32x4 (&qreg)[4], f32x16 (&oacc)[2], float& m_run,
@@ -713,7 +716,7 @@ __device__ __forceinline__ void attn32_tile(const AttnArgs& a, const uint4 (&kt)
     for (int j = 0; j < 16; ++j) sacc[kb2][j] = 0.f;
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
-      const uint4 kr = kt[32 * kb2 + c][(4 * h + ks) ^ (c & 7)];
+      const uint4 kr = kt[32 * kb2 + c][(4 * h + ks) ^ ((c >> 1) & 7)];
       sacc[kb2] = mfma32<T>(u32x4{kr.x, kr.y, kr.z, kr.w}, qreg[ks], sacc[kb2]);
     }
   }
@@ -739,22 +742,32 @@ __device__ __forceinline__ void attn32_tile(const AttnArgs& a, const uint4 (&kt)
       }
     }
   }
-  // Row max as a tree (short dependency chains): 32 -> 11 -> 4 -> 1.
-  float m1[11];
+  // Row max: two interleaved chains of 3-input maxima over the lane's 32
+  // scores, then the partner lane's.
+  float ma = fmaxf(sacc[0][0], sacc[0][1]), mb = fmaxf(sacc[1][0], sacc[1][1]);
 #pragma unroll
-  for (int g = 0; g < 10; ++g)
-    m1[g] = fmaxf(fmaxf(sacc[(3 * g) / 16][(3 * g) % 16], sacc[(3 * g + 1) / 16][(3 * g + 1) % 16]),
-                  sacc[(3 * g + 2) / 16][(3 * g + 2) % 16]);
-  m1[10] = fmaxf(sacc[1][14], sacc[1][15]);
-  const float m2a = fmaxf(fmaxf(m1[0], m1[1]), m1[2]), m2b = fmaxf(fmaxf(m1[3], m1[4]), m1[5]);
-  const float m2c = fmaxf(fmaxf(m1[6], m1[7]), m1[8]), m2d = fmaxf(m1[9], m1[10]);
-  float mx = fmaxf(fmaxf(m2a, m2b), fmaxf(m2c, m2d));
+  for (int j = 2; j < 16; j += 2) {
+    ma = fmaxf(fmaxf(ma, sacc[0][j]), sacc[0][j + 1]);
+    mb = fmaxf(fmaxf(mb, sacc[1][j]), sacc[1][j + 1]);
+  }
+  float mx = fmaxf(ma, mb);
   mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
   const float cs = a.scale_log2;
-  const float m_new = fmaxf(m_run, mx * cs);
-  const float ms = m_new == -INFINITY ? 0.f : m_new;
-  const float alpha = __builtin_amdgcn_exp2f(m_run - ms);
-  m_run = m_new;
+  // Lazy maximum: the subtracted maximum m_run moves only when the tile's
+  // maximum exceeds it by more than kLazyMax (log2 units), so the probabilities
+  // stay below 2^kLazyMax and the O rescale runs only on the rare tiles where
+  // some query's maximum jumps. Any m_run that bounds the exponents gives the
+  // same O / l; it only has to keep them from overflowing.
+  const bool grow = mx * cs > m_run + kLazyMax;  // false for a fully masked row (mx = -inf)
+  float alpha = 1.f;
+  if (__ballot(grow)) {  // wave-uniform
+    const float m_new = grow ? mx * cs : m_run;
+    alpha = grow ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.f;  // 0 for the first admissible tile
+    m_run = m_new;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) oacc[t] *= alpha;
+  }
+  const float ms = m_run == -INFINITY ? 0.f : m_run;
   u32x4 pop[4];
   float psum[4] = {0.f, 0.f, 0.f, 0.f};  // one accumulator per key step: short dot2 chains
 #pragma unroll
@@ -770,10 +783,6 @@ __device__ __forceinline__ void attn32_tile(const AttnArgs& a, const uint4 (&kt)
     pop[s2] = u32x4{pk[0], pk[1], pk[2], pk[3]};
   }
   l_run = l_run * alpha + ((psum[0] + psum[1]) + (psum[2] + psum[3]));
-  if (__ballot(alpha != 1.f)) {  // wave-uniform: skip the rescale once the maxima settle
-#pragma unroll
-    for (int t = 0; t < 2; ++t) oacc[t] *= alpha;
-  }
   // V^T operands: this lane's piece for step s2, dim tile t and key half is
   // at byte vlane_t + 2048 s2 + 1024 half of the tile (vt_lane_offset).
   const unsigned vbase = unsigned(size_t((__attribute__((address_space(3))) const char*)(&vt[0][0])));
@@ -862,7 +871,7 @@ constexpr int kA32Waves = 4;
 template <typename T>
 __global__ __launch_bounds__(kA32Waves * kWave) __attribute__((amdgpu_waves_per_eu(3))) void masked_attention32_kernel(AttnArgs a) {
   constexpr int D = 64, QB = 2 * BQ;
-  __shared__ __align__(16) uint4 k_s[2][BK][8];  // [key][16-byte slot s at s ^ (key & 7)]
+  __shared__ __align__(16) uint4 k_s[2][BK][8];  // [key][16-byte slot s at s ^ ((key >> 1) & 7)]
   __shared__ __align__(16) uint4 v_s[2][BK][8];  // [key][16-byte slot, see vt_slot]
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave), lane = tid % kWave;
@@ -906,11 +915,16 @@ __global__ __launch_bounds__(kA32Waves * kWave) __attribute__((amdgpu_waves_per_
   rows[1].init(a, 2 * qt + 1);
 
   // K tile: 8 loads of 8 rows (1 KB) per tile, 2 per wave; lane i moves row
-  // 8ch + i/8, logical slot (i%8) ^ (i/8) into physical slot i%8. The buffer
+  // r = 8ch + i/8, logical slot (i%8) ^ ((r >> 1) & 7) into physical slot i%8
+  // (the swizzle under which the 128-bit operand reads, 32 rows by 2 slot
+  // groups, are free of LDS bank conflicts; measured). ch is 4 cw + wave, so
+  // (r >> 1) & 7 = 4 (wave & 1) + i/16 for every load of this wave. The buffer
   // covers this head's rows [0, n): rows past n read as zeros.
+  static_assert(kA32Waves % 2 == 0, "the K swizzle below assumes ch & 1 == wave & 1");
   const unsigned krow_bytes = unsigned(a.ks[2]) * 2u;
   const i32x4_t krsrc = buffer_rsrc(kp, unsigned((long(n - 1) * a.ks[2] + D) * 2));
-  const unsigned kvoff = unsigned(lane / 8) * krow_bytes + 16u * unsigned((lane % 8) ^ (lane / 8));
+  const unsigned kvoff =
+      unsigned(lane / 8) * krow_bytes + 16u * unsigned((lane % 8) ^ (4 * (wave & 1) + lane / 16));
   // V tile: the same 8 loads of 8 rows; lane i moves row 8ch + i/8, logical
   // slot sg with vt_slot(sg, i/8) == i%8, into physical slot i%8.
   const unsigned vrow_bytes = unsigned(a.vs[2]) * 2u;
