@@ -183,6 +183,9 @@ int sfl_lm_head_tiles(int vocab);
 
 /*
  * x[b] = emb[tokens[b*token_stride + pos[b]]] in fp32 (Embedding.forward, layers.py:68-70).
+ * Token ids must lie in [0, vocab): the library does not know vocab and does
+ * not check them (the Python layer rejects out-of-range ids, as the
+ * reference's nn.Embedding lookup raises).
  */
 int sfl_embedding_gather(const int64_t* tokens, long token_stride, const int32_t* pos,
                          const void* emb, float* x, int batch, int d_model, int dtype,
@@ -234,8 +237,10 @@ int sfl_masked_attention(const void* q, const void* k, const void* v, void* o, f
 int sfl_masked_attention_block(void);
 
 /* ---- prefill (bf16 weights) -------------------------------------------------
- * C^T = W A^T on MFMA 16x16x32 bf16 tiles of 128 features x 128 tokens;
- * A [M, K] bf16 row-major (one row per token), W [N, K] bf16; K % 8 == 0.
+ * C^T = W A^T on bf16 MFMAs; A [M, K] bf16 row-major (one row per token),
+ * W [N, K] bf16; K % 8 == 0. K % 64 == 0 runs 32x32x16 MFMA tiles of 256 x 256
+ * (grids of >= 512 such tiles) or 128 x 128 features x tokens, other K the
+ * 16x16x32 kernel on 128 x 128 tiles.
  * Replace, for a whole prompt, the Linear layers of one TransformerBlock and
  * the lm_head (src/llmlab/model/layers.py:34-35, attention.py:160-162,199-203,
  * layers.py:114-115, transformer.py:137-138).
@@ -257,7 +262,8 @@ int sfl_gemm_qkv_rope(const void* a, const void* w_qkv, int m, int seq, int d_mo
 int sfl_gemm_swiglu(const void* a, const void* w13_interleaved, void* h_out, int m, int d_ff, int k,
                     void* stream);
 
-/* x[r] = emb[ids[r]] in fp32 for r < m (Embedding.forward, layers.py:68-70). */
+/* x[r] = emb[ids[r]] in fp32 for r < m (Embedding.forward, layers.py:68-70);
+ * ids in [0, vocab), unchecked as for sfl_embedding_gather. */
 int sfl_embed_rows(const int64_t* ids, const void* emb, float* x, int m, int d_model, int dtype,
                    void* stream);
 
