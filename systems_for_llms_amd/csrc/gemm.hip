@@ -253,11 +253,22 @@ __device__ __forceinline__ f32x16 mfma32_bf16(const u32x4& a, const u32x4& b, f3
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
 }
 
-template <int TN_, int TM_>
+template <int TN_, int TM_, int SL_>
 struct Stage32 {
-  uint4 w[TN_][8];  // [row][swizzled 16-byte slot]
-  uint4 a[TM_][8];
+  uint4 w[TN_][SL_];  // [row][swizzled 16-byte slot]
+  uint4 a[TM_][SL_];
 };
+
+// Physical 16-byte slot offset of row r in a stage of SL slots per row: the
+// XOR under which the MFMA operand reads (16 consecutive lanes reading rows r
+// .. r+15 at one logical slot, 256 bytes per LDS cycle) touch every bank
+// once. Rows of 128 bytes already alternate bank halves, rows of 64 bytes
+// cycle through bank quarters, so the swizzle only has to separate rows that
+// share a half / quarter.
+template <int SL>
+__device__ __forceinline__ int stage_swizzle(int r) {
+  return SL == 8 ? (r >> 1) & 7 : (r >> 2) & 3;
+}
 
 // Tile of workgroup b in a 1-D grid of tn x tm tiles, XCD-aware: workgroups
 // are dealt to the 8 XCDs round-robin (b % 8) and each XCD has its own L2, so
@@ -286,14 +297,17 @@ __device__ __forceinline__ int2 xcd_tile(int b, int tn, int tm) {
 // 4 x 2 waves: one workgroup of 8 waves per CU (128 KB), 64 x 128 per wave,
 // which reads 3/4 of the LDS operand bytes per MFMA of the 64 x 64 wave tile
 // and stages half the bytes per MFMA through LDS.
-template <int E, int TBN, int TBM, int WN, int WM>
+template <int E, int TBN, int TBM, int WN, int WM, int KS, int NS>
 __global__ __launch_bounds__(64 * WN * WM) __attribute__((amdgpu_waves_per_eu(2)))
 void gemm32_kernel(GemmArgs g) {
   constexpr int NW = WN * WM;              // waves
   constexpr int NBN = TBN / WN / 32;       // 32x32 blocks per wave along features
   constexpr int NBM = TBM / WM / 32;       // and along tokens
-  // Two LDS stages; see lds_load16 for why the loads are counted by hand.
-  __shared__ Stage32<TBN, TBM> st[2];
+  constexpr int SL = KS / 8;               // 16-byte slots per row of a stage
+  constexpr int RPL = kWave / SL;          // rows one 1 KB load instruction moves
+  // NS LDS stages of KS k values each; see lds_load16 for why the loads are
+  // counted by hand.
+  __shared__ Stage32<TBN, TBM, SL> st[NS];
   const int tid = threadIdx.x;
   // readfirstlane: the wave index is uniform, so the LDS destinations live in scalar registers.
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave), lane = tid % kWave;
@@ -302,19 +316,21 @@ void gemm32_kernel(GemmArgs g) {
   const int2 tile = xcd_tile(blockIdx.x, (g.n + TBN - 1) / TBN, (g.m + TBM - 1) / TBM);
   const int n0 = tile.x * TBN;
   const int m0 = tile.y * TBM;
-  const int ksteps = g.k / K2;
+  const int ksteps = g.k / KS;
 
-  // Loads: the TBN + TBM rows of a step are chunks of 8 rows; wave w takes
-  // chunks w, w + NW, ... Lane i of a chunk moves row 8c + i/8 into slot i%8,
-  // i.e. column (i%8) ^ ((row >> 1) & 7); the swizzle depends on the chunk's
-  // parity only, so two byte offsets per lane cover every chunk.
+  // Loads: the TBN + TBM rows of a step are chunks of RPL rows; wave w takes
+  // chunks w, w + NW, ... Lane i of a chunk moves row RPL c + i/SL into slot
+  // i%SL, i.e. column (i%SL) ^ stage_swizzle(row); the swizzle depends on the
+  // chunk's parity at most, so two byte offsets per lane cover every chunk.
   const i32x4_t rw = buffer_rsrc(g.w, unsigned(g.n * g.k * 2));
   const i32x4_t ra = buffer_rsrc(g.a, unsigned(g.m * g.k * 2));
-  const int rr = lane / 8, pos = lane % 8;
+  const int rr = lane / SL, pos = lane % SL;
   unsigned voff[2];
 #pragma unroll
-  for (int par = 0; par < 2; ++par) voff[par] = unsigned((rr * g.k + 8 * (pos ^ ((4 * par + rr / 2) & 7))) * 2);
-  constexpr int CHN = TBN / 8, CHM = TBM / 8;  // chunks per operand
+  for (int par = 0; par < 2; ++par)
+    voff[par] = unsigned((rr * g.k + 8 * (pos ^ stage_swizzle<SL>(RPL * par + rr))) * 2);
+  constexpr int CHN = TBN / RPL, CHM = TBM / RPL;  // chunks per operand
+  constexpr int CPW = (CHN + CHM) / NW;            // load instructions per wave and stage
   static_assert((CHN + CHM) % NW == 0 && CHN % 2 == 0, "chunks per wave");
 
 #define SFL_G32_ISSUE(stage, kt)                                                            \
@@ -322,17 +338,17 @@ void gemm32_kernel(GemmArgs g) {
     _Pragma("unroll") for (int c0 = 0; c0 < CHN + CHM; c0 += NW) {                          \
       const int c = c0 + wave;                                                              \
       if (c < CHN)                                                                          \
-        lds_load16(rw, lds_offset(&stage.w[8 * c][0]), voff[c & 1],                         \
-                   unsigned(((n0 + 8 * c) * g.k + (kt) * K2) * 2));                         \
+        lds_load16(rw, lds_offset(&stage.w[RPL * c][0]), voff[c & 1],                       \
+                   unsigned(((n0 + RPL * c) * g.k + (kt) * KS) * 2));                       \
       else                                                                                  \
-        lds_load16(ra, lds_offset(&stage.a[8 * (c - CHN)][0]), voff[(c - CHN) & 1],         \
-                   unsigned(((m0 + 8 * (c - CHN)) * g.k + (kt) * K2) * 2));                 \
+        lds_load16(ra, lds_offset(&stage.a[RPL * (c - CHN)][0]), voff[(c - CHN) & 1],       \
+                   unsigned(((m0 + RPL * (c - CHN)) * g.k + (kt) * KS) * 2));               \
     }                                                                                       \
   }
   // Operand reads: lane (l32, hf) takes row 32t + l32, column 2kk + hf.
-  const int sw = (l32 >> 1) & 7;
+  const int sw = stage_swizzle<SL>(l32);
 #define SFL_G32_COMPUTE(stage)                                                              \
-  _Pragma("unroll") for (int kk = 0; kk < 4; ++kk) {                                        \
+  _Pragma("unroll") for (int kk = 0; kk < KS / 16; ++kk) {                                  \
     const int slot = (2 * kk + hf) ^ sw;                                                    \
     u32x4 af[NBN], bfr[NBM];                                                                \
     _Pragma("unroll") for (int t = 0; t < NBN; ++t) {                                       \
@@ -355,15 +371,23 @@ void gemm32_kernel(GemmArgs g) {
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
-  // Two LDS stages: step kt computes from stage kt & 1 while the loads of
-  // step kt+1 fill the other. One loop body, so every accumulator keeps its
-  // registers across iterations.
-  SFL_G32_ISSUE(st[0], 0)
+  // NS LDS stages in a ring: step kt computes from stage kt % NS while the
+  // loads of the next NS - 1 steps are in flight. At step kt the wave waits
+  // only for stage kt's loads (the younger stages' CPW each may stay
+  // outstanding), the barrier then covers every wave's share, and stage
+  // (kt - 1) % NS, last read before that barrier, is refilled with step
+  // kt + NS - 1. One loop body, so every accumulator keeps its registers.
+#pragma unroll
+  for (int p = 0; p < NS - 1; ++p)
+    if (p < ksteps) SFL_G32_ISSUE(st[p], p)
   for (int kt = 0; kt < ksteps; ++kt) {
-    __builtin_amdgcn_s_waitcnt(sfl_vmcnt(0));
-    __syncthreads();  // every wave's loads of this stage landed; the other is no longer read
-    if (kt + 1 < ksteps) SFL_G32_ISSUE(st[(kt + 1) & 1], kt + 1)
-    SFL_G32_COMPUTE(st[kt & 1])
+    const int younger = min(NS - 2, ksteps - 1 - kt);  // stages issued after stage kt
+    if (NS > 3 && younger >= 2) __builtin_amdgcn_s_waitcnt(sfl_vmcnt(NS > 3 ? 2 * CPW : 0));
+    else if (NS > 2 && younger >= 1) __builtin_amdgcn_s_waitcnt(sfl_vmcnt(NS > 2 ? CPW : 0));
+    else __builtin_amdgcn_s_waitcnt(sfl_vmcnt(0));
+    __syncthreads();  // every wave's loads of this stage landed; stage (kt - 1) % NS is no longer read
+    if (kt + NS - 1 < ksteps) SFL_G32_ISSUE(st[(kt + NS - 1) % NS], kt + NS - 1)
+    SFL_G32_COMPUTE(st[kt % NS])
   }
 #undef SFL_G32_COMPUTE
 #undef SFL_G32_ISSUE
@@ -417,9 +441,11 @@ int launch_gemm(const GemmArgs& g, hipStream_t s, const char* what) {
     // 256 x 256 tiles where they still give every CU several workgroups.
     const long big = long((g.n + 255) / 256) * ((g.m + 255) / 256);
     if (big >= 512)
-      hipLaunchKernelGGL((gemm32_kernel<E, 256, 256, 4, 2>), dim3(unsigned(big)), dim3(512), 0, s, g);
+      // (A ring of 4 stages of K = 32 in the same 128 KB measured 6% slower:
+      // the deeper prefetch does not pay for twice the steps and barriers.)
+      hipLaunchKernelGGL((gemm32_kernel<E, 256, 256, 4, 2, 64, 2>), dim3(unsigned(big)), dim3(512), 0, s, g);
     else
-      hipLaunchKernelGGL((gemm32_kernel<E, 128, 128, 2, 2>), dim3(unsigned(tiles)), dim3(kThreads), 0, s, g);
+      hipLaunchKernelGGL((gemm32_kernel<E, 128, 128, 2, 2, 64, 2>), dim3(unsigned(tiles)), dim3(kThreads), 0, s, g);
     return check_launch(what);
   }
   dim3 grid((g.n + TN - 1) / TN, (g.m + TM - 1) / TM);

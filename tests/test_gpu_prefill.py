@@ -34,6 +34,22 @@ def test_gemm_matches_fp32_matmul(m, n, k):
     torch.testing.assert_close(ob.float().cpu(), ref.bfloat16().float(), atol=1e-2, rtol=1e-2)
 
 
+# Grids of >= 512 tiles of 256 x 256 take the 256 x 256 kernel with its ring
+# of LDS stages: K of 64 (fewer steps than stages), 192 and 2752 (the model's
+# d_ff), ragged M and N. Sampled token rows keep the CPU reference small.
+@pytest.mark.parametrize("m,n,k", [(4100, 8200, 64), (4100, 8200, 192), (2304, 14400, 2752)])
+def test_gemm_large_grid_matches_fp32_matmul(m, n, k):
+    g = torch.Generator().manual_seed(m + n + k)
+    a = torch.randn((m, k), generator=g).bfloat16()
+    w = torch.randn((n, k), generator=g).bfloat16()
+    rows = torch.cat([torch.arange(0, 40), torch.randint(0, m, (200,), generator=g), torch.arange(m - 40, m)])
+    ref = a[rows].float() @ w.float().t()
+    ga, gw = a.cuda(), w.cuda()
+    out = torch.zeros((m, n), device="cuda")
+    _lib.call("sfl_gemm_bf16", ga.data_ptr(), gw.data_ptr(), out.data_ptr(), m, n, k, 0, 0, _lib.stream_handle())
+    torch.testing.assert_close(out[rows.cuda()].cpu(), ref, atol=1e-3 * k ** 0.5, rtol=1e-4)
+
+
 # d % 4 == 0 and d <= 2048 take the one-wave-per-row kernel (m not a multiple
 # of its 4 rows per workgroup included); other widths the workgroup-per-row one.
 @pytest.mark.parametrize("m,d", [(1, 64), (7, 96), (130, 1024), (33, 2048), (5, 2052), (9, 1030)])
