@@ -101,9 +101,12 @@ int sfl_decode_attention_out_proj(const float* q, const void* k, const void* v,
 
 
 /* ---- decode step of the llmlab decoder (model dtype F32 or BF16) ----------
- * One step processes one token per sequence for `batch` <= 16 sequences per
- * launch. x is the fp32 residual stream [batch, d_model]; weights are the
- * reference's [out, in] matrices in the model dtype.
+ * One step processes one token per sequence for `batch` <= 65536 sequences.
+ * The GEMVs run one workgroup per 16 output features and block of 16 batch
+ * rows; the blocks of one weight tile share an XCD, so the weights stream
+ * from HBM once per launch whatever the batch. x is the fp32 residual stream
+ * [batch, d_model]; weights are the reference's [out, in] matrices in the
+ * model dtype.
  */
 
 /*

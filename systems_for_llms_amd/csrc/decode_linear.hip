@@ -1,7 +1,8 @@
 // Decode-step projections as MFMA GEMVs with fused prologues and epilogues.
 //
 // Every kernel computes out[b, n] = sum_k act[b, k] * W[n, k] for a batch of
-// at most 16 rows (one decode token per sequence). W is the reference's [N, K]
+// rows (one decode token per sequence), 16 rows -- the MFMA's columns -- per
+// workgroup. W is the reference's [N, K]
 // Linear weight (src/llmlab/model/layers.py:34-35) repacked once by
 // sfl_pack_gemv_weights into the load order of the kernel: for every tile of
 // 16 output rows and every K chunk, the 64 lanes' 16-byte A operands are
@@ -48,7 +49,9 @@ enum Epi { EPI_QKV = 0, EPI_RESIDUAL = 1, EPI_SWIGLU = 2, EPI_LOGITS = 3 };
 
 constexpr int kWaves = 8;       // waves per workgroup (K split)
 constexpr int kTileN = 16;      // output features per workgroup
-constexpr int kMaxRows = 16;    // batch rows per launch
+constexpr int kBlockRows = 16;  // batch rows per MFMA column block (one workgroup)
+constexpr int kMaxRows = 1 << 16;  // batch rows per launch
+constexpr int kXcds = 8;        // workgroups are dealt to the XCDs round-robin
 constexpr float kEps = 1e-5f;
 constexpr int kMaxSplitK = 16;  // workgroups per tile along K (RESIDUAL)
 
@@ -207,8 +210,12 @@ template <typename T> struct SrcOf<true, T> { using type = NormChunk<T>; };
 
 // CPW: weight chunks each wave loads per round (one round when the workgroup's
 // chunks fit kWaves*CPW); chosen on the host so no wave issues more loads than
-// it needs. Workgroup blockIdx.x owns tile blockIdx.x % tiles and the K part
-// blockIdx.x / tiles (one part unless RESIDUAL splits K).
+// it needs. A workgroup owns one (tile, K part) item -- tile = item % tiles,
+// part = item / tiles (one part unless RESIDUAL splits K) -- for one block of
+// 16 batch rows. With one block, workgroup w owns item w. With several, the
+// blocks of one item go to workgroups w = 8 (g * blocks + blk) + x for item
+// 8 g + x: the same XCD (w % 8 == x), so the item's weights come from HBM
+// once and from that XCD's L2 for the other blocks.
 template <typename T, int E, int CPW>
 __global__ __launch_bounds__(kWaves * kWave) void linear_kernel(LinearArgs a) {
   constexpr int KC = chunk_k<T>();
@@ -225,11 +232,19 @@ __global__ __launch_bounds__(kWaves * kWave) void linear_kernel(LinearArgs a) {
 
   constexpr int CB = act_chunk_bytes<T>();
   const int tiles = (a.n + kTileN - 1) / kTileN;
-  const int tile = int(blockIdx.x % unsigned(tiles));
-  const int part = int(blockIdx.x / unsigned(tiles));
+  const int blocks = (a.batch + kBlockRows - 1) / kBlockRows;
+  int item = int(blockIdx.x), blk = 0;
+  if (blocks > 1) {
+    const int w = int(blockIdx.x), x = w % kXcds, r = w / kXcds;
+    blk = r % blocks;
+    item = (r / blocks) * kXcds + x;
+    if (item >= tiles * a.ksplit) return;  // padding of the last group of 8 items
+  }
+  const int tile = item % tiles;
+  const int part = item / tiles;
   const int n0 = tile * kTileN;
   const int grp = lane / 16;
-  const int b = lane % 16;
+  const int b = blk * kBlockRows + lane % 16;  // this lane's batch row
   const int nchunks = K / KC;
   const int per = (nchunks + a.ksplit - 1) / a.ksplit;
   const int cb = part * per;
@@ -242,7 +257,8 @@ __global__ __launch_bounds__(kWaves * kWave) void linear_kernel(LinearArgs a) {
       kTwo ? static_cast<const unsigned char*>(a.w3) + (long(tile) * nchunks * kWave + lane) * 16 : nullptr;
   const bool live = b < a.batch;
   const int row = min(b, a.batch - 1);
-  const unsigned char* al = kNorm ? nullptr : static_cast<const unsigned char*>(a.act) + lane * 16;
+  const unsigned char* al =
+      kNorm ? nullptr : static_cast<const unsigned char*>(a.act) + long(blk) * nchunks * CB + lane * 16;
   const float* xl = kNorm ? a.x_in + long(row) * K + grp * EPL : nullptr;
   const T* gl = kNorm ? static_cast<const T*>(a.gain) + grp * EPL : nullptr;
 
@@ -438,9 +454,11 @@ __global__ __launch_bounds__(kWaves * kWave) void linear_kernel(LinearArgs a) {
 
 template <typename T, int E, int CPW>
 int launch_linear_cpw(const LinearArgs& a, hipStream_t stream, const char* what) {
-  const unsigned tiles = unsigned((a.n + kTileN - 1) / kTileN);
-  hipLaunchKernelGGL((linear_kernel<T, E, CPW>), dim3(tiles * unsigned(a.ksplit)), dim3(kWaves * kWave), 0,
-                     stream, a);
+  const long items = long((a.n + kTileN - 1) / kTileN) * a.ksplit;
+  const long blocks = (a.batch + kBlockRows - 1) / kBlockRows;
+  const long grid = blocks == 1 ? items : (items + kXcds - 1) / kXcds * kXcds * blocks;
+  if (grid > (1L << 31) - 1) return set_error(SFL_ERR_UNSUPPORTED, "%s: too many workgroups", what);
+  hipLaunchKernelGGL((linear_kernel<T, E, CPW>), dim3(unsigned(grid)), dim3(kWaves * kWave), 0, stream, a);
   return check_launch(what);
 }
 
@@ -459,7 +477,7 @@ int launch_linear(const LinearArgs& a, hipStream_t stream, const char* what) {
 // vec4: the epilogue moves 4 consecutive features per lane (all but LOGITS).
 int check_common(const char* what, int batch, int n, int k, int dtype, bool vec4 = true) {
   if (batch < 1 || batch > kMaxRows)
-    return set_error(SFL_ERR_INVALID, "%s: batch must be in [1, %d] per launch", what, kMaxRows);
+    return set_error(SFL_ERR_INVALID, "%s: batch must be in [1, %d]", what, kMaxRows);
   if (n < 1 || k < 1) return set_error(SFL_ERR_INVALID, "%s: sizes must be positive", what);
   if (vec4 && n % 4) return set_error(SFL_ERR_UNSUPPORTED, "%s: N must be a multiple of 4", what);
   if (dtype != SFL_DTYPE_F32 && dtype != SFL_DTYPE_BF16)

@@ -35,7 +35,7 @@ import torch
 from . import _lib
 from .decode import auto_splits
 
-ROWS_PER_LAUNCH = 16  # batch rows per decode-step GEMV launch
+ROW_BLOCK = 16  # batch rows per GEMV workgroup (the activation layout's block)
 
 
 def residual_ksplit(n: int, target_groups: int = 256) -> int:
@@ -95,9 +95,9 @@ class DecodeSession:
         # value (viewed here as fp32 words): the attention output (only when the
         # attention is not fused with output_proj) and the SwiGLU hidden state.
         # The normalized consumers read x itself with their RMSNorm gain.
-        blocks = -(-batch // ROWS_PER_LAUNCH)
-        self.attn = torch.zeros((blocks, ROWS_PER_LAUNCH * d), device=dev, dtype=torch.float32)
-        self.hidden = torch.zeros((blocks, ROWS_PER_LAUNCH * f), device=dev, dtype=torch.float32)
+        blocks = -(-batch // ROW_BLOCK)
+        self.attn = torch.zeros((blocks, ROW_BLOCK * d), device=dev, dtype=torch.float32)
+        self.hidden = torch.zeros((blocks, ROW_BLOCK * f), device=dev, dtype=torch.float32)
         self.act_code = _lib.DTYPE_BF16X2 if dt == torch.bfloat16 else _lib.DTYPE_F32X
         self.splits = splits or auto_splits(batch, h, cap)
         self.pmax = torch.empty((batch, h, self.splits), device=dev, dtype=torch.float32)
@@ -127,15 +127,13 @@ class DecodeSession:
         m = self.model
         calls = []
         scale = float(dk) ** -0.5
-        row_chunks = [(r, min(ROWS_PER_LAUNCH, self.batch - r)) for r in range(0, self.batch, ROWS_PER_LAUNCH)]
-        self._row_chunks = row_chunks
+        rows = self.batch  # every GEMV launch covers all rows, 16 per workgroup
         for layer, blk in enumerate(m.layers):
             kc, vc = self.k_cache[layer], self.v_cache[layer]
-            for r, rows in row_chunks:
-                calls.append((lib.sfl_rmsnorm_qkv_rope_append, (
-                    self.x[r].data_ptr(), blk.attn_norm.weight.data_ptr(), self.p_qkv[layer].data_ptr(),
-                    self.cos.data_ptr(), self.sin.data_ptr(), self.pos[r:].data_ptr(),
-                    self.q[r].data_ptr(), kc[r].data_ptr(), vc[r].data_ptr(), rows, d, h, cap, code)))
+            calls.append((lib.sfl_rmsnorm_qkv_rope_append, (
+                self.x.data_ptr(), blk.attn_norm.weight.data_ptr(), self.p_qkv[layer].data_ptr(),
+                self.cos.data_ptr(), self.sin.data_ptr(), self.pos.data_ptr(),
+                self.q.data_ptr(), kc.data_ptr(), vc.data_ptr(), rows, d, h, cap, code)))
             if self.fused_out_proj:
                 calls.append((lib.sfl_decode_attention_out_proj, (
                     self.q.data_ptr(), kc.data_ptr(), vc.data_ptr(), self.lengths.data_ptr(),
@@ -146,25 +144,20 @@ class DecodeSession:
                     self.pmax.data_ptr(), self.psum.data_ptr(), self.pout.data_ptr(), self.attn.data_ptr(),
                     self.batch, h, h, cap, dk, self.splits, scale, code, _lib.DTYPE_CODES[torch.float32],
                     self.act_code)))
-            for r, rows in row_chunks:
-                j = r // ROWS_PER_LAUNCH
-                x = self.x[r].data_ptr()
-                if not self.fused_out_proj:
-                    calls.append((lib.sfl_linear_residual, (
-                        self.attn[j].data_ptr(), self.p_out[layer].data_ptr(), x, rows, d, d,
-                        residual_ksplit(d), code)))
-                calls.append((lib.sfl_rmsnorm_swiglu, (
-                    x, blk.ffn_norm.weight.data_ptr(), self.p_w1[layer].data_ptr(), self.p_w3[layer].data_ptr(),
-                    self.hidden[j].data_ptr(), rows, d, f, code)))
                 calls.append((lib.sfl_linear_residual, (
-                    self.hidden[j].data_ptr(), self.p_w2[layer].data_ptr(), x, rows, d, f,
+                    self.attn.data_ptr(), self.p_out[layer].data_ptr(), self.x.data_ptr(), rows, d, d,
                     residual_ksplit(d), code)))
-        for r, rows in row_chunks:
-            logits = self.logits[r].data_ptr() if self.logits is not None else None
-            calls.append((lib.sfl_rmsnorm_lm_head, (
-                self.x[r].data_ptr(), m.ln_final.weight.data_ptr(), self.p_head.data_ptr(),
-                logits, cap * v, self.pos[r:].data_ptr(), v, self.best_val[:, r:].data_ptr(),
-                self.best_idx[:, r:].data_ptr(), self.batch, rows, d, v, code)))
+            calls.append((lib.sfl_rmsnorm_swiglu, (
+                self.x.data_ptr(), blk.ffn_norm.weight.data_ptr(), self.p_w1[layer].data_ptr(),
+                self.p_w3[layer].data_ptr(), self.hidden.data_ptr(), rows, d, f, code)))
+            calls.append((lib.sfl_linear_residual, (
+                self.hidden.data_ptr(), self.p_w2[layer].data_ptr(), self.x.data_ptr(), rows, d, f,
+                residual_ksplit(d), code)))
+        logits = self.logits.data_ptr() if self.logits is not None else None
+        calls.append((lib.sfl_rmsnorm_lm_head, (
+            self.x.data_ptr(), m.ln_final.weight.data_ptr(), self.p_head.data_ptr(),
+            logits, cap * v, self.pos.data_ptr(), v, self.best_val.data_ptr(),
+            self.best_idx.data_ptr(), self.batch, rows, d, v, code)))
         calls.append((lib.sfl_next_token, (
             self.best_val.data_ptr(), self.best_idx.data_ptr(), self.tiles, self.tokens.data_ptr(),
             self.predicted.data_ptr(), cap, self.prompt_len.data_ptr(), self.pos.data_ptr(),
@@ -278,7 +271,7 @@ class DecodeSession:
         self.x.copy_(x.view(b, t, d)[:, t - 1])
         self.pos.fill_(t - 1)
         self.lengths.fill_(t)
-        for fn, args in self._calls[-(len(self._row_chunks) + 1):]:
+        for fn, args in self._calls[-2:]:  # the lm_head and the token step
             status = fn(*args, st)
             if status != 0:
                 raise RuntimeError(f"{fn.__name__} failed ({status}): "

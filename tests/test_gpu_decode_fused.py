@@ -44,7 +44,7 @@ def rms_normalize(x, g):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-@pytest.mark.parametrize("batch", [3, 16])
+@pytest.mark.parametrize("batch", [3, 16, 37])  # 37: three 16-row blocks in one launch
 @pytest.mark.parametrize("ksplit", [1, 2, 3, 16])
 def test_linear_residual_split_k(dtype, batch, ksplit):
     code = _lib.DTYPE_BF16X2 if dtype == torch.bfloat16 else _lib.DTYPE_F32X
@@ -125,12 +125,12 @@ def test_attention_out_proj_rejects_unsupported_shapes():
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-@pytest.mark.parametrize("d_model", [96, 1024])
-def test_normalized_consumers_read_raw_x(dtype, d_model):
+@pytest.mark.parametrize("d_model,batch", [(96, 7), (1024, 7), (96, 40)])  # 40: three row blocks
+def test_normalized_consumers_read_raw_x(dtype, d_model, batch):
     """SwiGLU and lm_head scale by the inverse RMS of x and apply the gain themselves."""
     code = _lib.DTYPE_BF16X2 if dtype == torch.bfloat16 else _lib.DTYPE_F32X
-    g = torch.Generator().manual_seed(d_model)
-    batch, d_ff, vocab = 7, 96, 203
+    g = torch.Generator().manual_seed(d_model + batch)
+    d_ff, vocab = 96, 203
     x = torch.randn(batch, d_model, generator=g) * 3
     gain = (1 + 0.5 * torch.randn(d_model, generator=g)).to(dtype)
     w1 = torch.randn(d_ff, d_model, generator=g).to(dtype)
@@ -138,7 +138,7 @@ def test_normalized_consumers_read_raw_x(dtype, d_model):
     wh = torch.randn(vocab, d_model, generator=g).to(dtype)
     xd, gd = x.cuda(), gain.cuda()
     w1d, w3d, whd = _lib.pack_gemv(w1.cuda()), _lib.pack_gemv(w3.cuda()), _lib.pack_gemv(wh.cuda())
-    h = torch.zeros(16 * d_ff, device="cuda")
+    h = torch.zeros(-(-batch // 16) * 16 * d_ff, device="cuda")
     st, dc = _lib.stream_handle(), _lib.dtype_code(dtype)
     _lib.call("sfl_rmsnorm_swiglu", xd.data_ptr(), gd.data_ptr(), w1d.data_ptr(), w3d.data_ptr(), h.data_ptr(),
               batch, d_model, d_ff, dc, st)

@@ -48,11 +48,13 @@ def test_tiny_bf16_forward_within_tolerance(golden):
     assert err <= BF16_ATOL
 
 
-def test_batch_above_one_launch_chunk_matches_oracle():
+@pytest.mark.parametrize("batch", [20, 41])
+def test_batch_of_several_row_blocks_matches_oracle(batch):
+    """More than 16 sequences: every GEMV launch covers 2 or 3 blocks of 16 rows."""
     cfg = ModelConfig(vocab_size=300, context_length=24, d_model=128, num_layers=2, num_heads=4,
                       d_ff=256, rope_theta=10000.0)
     sd = seeded_state_dict(cfg, 77)
-    ids = seeded_prompt(cfg.vocab_size, 20, 24, 78)
+    ids = seeded_prompt(cfg.vocab_size, batch, 24, 78)
     logits = gpu_model(cfg, sd, torch.float32)(ids.cuda()).cpu()
     torch.testing.assert_close(logits, om.forward(sd, cfg, ids), atol=2e-5, rtol=1e-4)
 
