@@ -21,12 +21,12 @@ Differences, all documented widenings:
 
 from __future__ import annotations
 
-import ctypes
 from functools import lru_cache
 
 import torch
 
 from . import _lib
+from . import ops  # noqa: F401  (registers torch.ops.sfl)
 from .masks import BlockSchedule, MaskSpec, compile_mask, interval_regions  # noqa: F401
 
 TILE = 64
@@ -110,10 +110,6 @@ def _kernel_schedule(schedule, spec, document_ids, length):
     return compile_mask(length, spec, TILE, TILE, docs)
 
 
-def _strides(t):
-    return (ctypes.c_long * 3)(t.stride(0), t.stride(1), t.stride(2))
-
-
 def attention(q, k, v, schedule, spec, document_ids=None, num_warps=4, num_stages=2,
               implementation="csr", use_full_blocks=True, launch_metadata=None, return_lse=False,
               out=None):
@@ -177,7 +173,7 @@ def attention(q, k, v, schedule, spec, document_ids=None, num_warps=4, num_stage
     else:
         doc_list = None
 
-    lib = _lib.lib()
+    _lib.lib()  # fail here, before allocating, if the library is not built
     if out is None:
         out = torch.empty_like(q)
     elif (out.shape != q.shape or out.dtype != q.dtype or out.device != q.device or out.stride(-1) != 1
@@ -190,16 +186,13 @@ def attention(q, k, v, schedule, spec, document_ids=None, num_warps=4, num_stage
         csr = (row_ptr, col_idx, full) if sched is schedule else \
             (tuple(sched.row_ptr), tuple(sched.col_idx), tuple(sched.full_blocks))
         rows, cols, fulls = _upload_schedule(str(q.device), *csr)
-        mode, ptrs = 1, (rows.data_ptr(), cols.data_ptr(), fulls.data_ptr())
     else:
-        mode, ptrs = 0, (None, None, None)
-    _lib.call("sfl_masked_attention", q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
-              None if lse is None else lse.data_ptr(), batch, heads, length, dimension,
-              _strides(q), _strides(k), _strides(v), _strides(out), float(dimension ** -0.5),
-              int(spec.causal), -1 if spec.window_left is None else spec.window_left,
-              -1 if spec.window_right is None else spec.window_right, spec.global_prefix or 0,
-              None if docs_gpu is None else docs_gpu.data_ptr(), mode, *ptrs, int(use_full_blocks),
-              _lib.dtype_code(q.dtype), _lib.stream_handle(q.device))
+        rows = cols = fulls = None
+    torch.ops.sfl.masked_attention(
+        q, k, v, out, lse, float(dimension ** -0.5), bool(spec.causal),
+        -1 if spec.window_left is None else spec.window_left,
+        -1 if spec.window_right is None else spec.window_right, spec.global_prefix or 0, docs_gpu,
+        rows, cols, fulls, use_full_blocks)
     if launch_metadata is not None:
         launch_metadata.update({"kernel_name": "masked_attention_kernel", "block_q": TILE, "block_k": TILE,
                                 "threads": 256, "implementation": implementation,
@@ -214,9 +207,6 @@ def causal_prefill(q, k, v, out):
     contiguous last dimension (``k``/``v`` straight out of the KV cache);
     launches on the current stream without any host synchronisation.
     """
-    b, h, t, d = q.shape
-    _lib.call("sfl_masked_attention", q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), None,
-              b, h, t, d, _strides(q), _strides(k), _strides(v), _strides(out), float(d ** -0.5),
-              1, -1, -1, 0, None, 0, None, None, None, 1, _lib.dtype_code(q.dtype),
-              _lib.stream_handle(q.device))
+    torch.ops.sfl.masked_attention(q, k, v, out, None, float(q.shape[-1] ** -0.5), True, -1, -1, 0, None,
+                                   None, None, None, True)
     return out

@@ -26,6 +26,7 @@ from dataclasses import dataclass
 import torch
 
 from . import _lib
+from . import ops  # noqa: F401  (registers torch.ops.sfl)
 
 SUPPORTED_DIMS = (16, 32, 64, 128)
 SUPPORTED_GROUPS = (1, 2, 4, 8)
@@ -88,14 +89,9 @@ class PreparedDecode:
     variant: str
 
     def __call__(self) -> torch.Tensor:
-        batch, heads, dim = self.q.shape
-        kv_heads, capacity = self.k.shape[1:3]
-        _lib.call("sfl_decode_attention", self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(),
-                  self.lengths.data_ptr(), self.partial_max.data_ptr(), self.partial_sum.data_ptr(),
-                  self.partial_output.data_ptr(), self.output.data_ptr(), batch, heads, kv_heads,
-                  capacity, dim, self.splits, self.scale, _lib.dtype_code(self.q.dtype),
-                  _lib.dtype_code(self.q.dtype), _lib.dtype_code(self.q.dtype),
-                  _lib.stream_handle(self.q.device))
+        torch.ops.sfl.decode_attention(self.q, self.k, self.v, self.lengths, self.partial_max,
+                                       self.partial_sum, self.partial_output, self.output, self.splits,
+                                       self.scale)
         return self.output
 
     @property
