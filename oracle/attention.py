@@ -9,6 +9,12 @@
 * ``masked_attention`` is softmax attention under a dense mask with the
   reference's empty-row convention (output 0, LSE ``-inf``,
   ``attention_lab/triton_attention.py:191-197``); LSE is the natural log.
+* ``scheduled_attention`` interprets a block schedule as the kernels must
+  (``attention_lab/validate.py:31-55``): a query tile attends only the key
+  tiles its CSR row lists; a tile flagged full is taken whole, any other tile
+  through the token mask. For a schedule the compiler made from the same spec
+  it equals ``masked_attention`` under ``spec_mask``; for a hand-edited one it
+  is the reference of what the kernels compute.
 """
 
 from __future__ import annotations
@@ -67,3 +73,19 @@ def masked_attention(q, k, v, mask, *, scale=None, dtype=torch.float64):
     weights = torch.softmax(scores, dim=-1).nan_to_num(0.0)
     out = torch.matmul(weights, v.to(dtype))
     return out, lse
+
+
+def scheduled_attention(q, k, v, schedule, spec, documents=None, *, use_full_blocks=True,
+                        dtype=torch.float64):
+    """Output ``[..., N, D]`` of ``schedule`` over q/k/v ``[..., N, D]`` (``validate.py:31-55``)."""
+    n = schedule.length
+    allowed = spec_mask(n, spec, documents)
+    mask = torch.zeros((n, n), dtype=torch.bool)
+    for r in range(len(schedule.row_ptr) - 1):
+        q0, q1 = r * schedule.block_q, min((r + 1) * schedule.block_q, n)
+        for j in range(schedule.row_ptr[r], schedule.row_ptr[r + 1]):
+            k0 = schedule.col_idx[j] * schedule.block_k
+            k1 = min(k0 + schedule.block_k, n)
+            whole = use_full_blocks and schedule.full_blocks[j]
+            mask[q0:q1, k0:k1] = True if whole else allowed[q0:q1, k0:k1]
+    return masked_attention(q, k, v, mask, dtype=dtype)[0]

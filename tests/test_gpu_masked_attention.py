@@ -107,3 +107,31 @@ def test_config5_shape_sampled_heads():
             torch.testing.assert_close(out[bi, hi].float().cpu(), ref_out, atol=2e-2, rtol=2e-2)
             torch.testing.assert_close(lse[bi, hi].cpu(), ref_lse, atol=1e-2, rtol=1e-2)
     torch.testing.assert_close(outs["interval"][0], outs["csr"][0], atol=0, rtol=0)
+
+
+@pytest.mark.parametrize("use_full", [True, False])
+def test_kernel_follows_a_hand_edited_schedule(use_full):
+    """The kernel walks the CSR it is given (validate.py:31-55 semantics), not the mask behind it:
+    a dropped tile is skipped, a partial tile flagged full is taken whole (unless use_full_blocks
+    is off, when every tile goes through the token mask)."""
+    from oracle.attention import scheduled_attention
+
+    n = 300
+    spec = MaskSpec(causal=True, window_left=70)
+    schedule = compile_mask(n, spec, 64, 64)
+    # Row 3: drop its first tile. Row 2: flag its diagonal (partial) tile as full.
+    first = schedule.row_ptr[3]
+    assert schedule.row_ptr[4] - first >= 2
+    schedule.col_idx.pop(first)
+    schedule.full_blocks.pop(first)
+    schedule.row_ptr[4:] = [p - 1 for p in schedule.row_ptr[4:]]
+    diag = schedule.row_ptr[3] - 1
+    assert schedule.col_idx[diag] == 2 and not schedule.full_blocks[diag]
+    schedule.full_blocks[diag] = True
+    q, k, v = inputs(2, 3, n, 64, torch.bfloat16, 41)
+    out = attention(q.cuda(), k.cuda(), v.cuda(), schedule, spec, implementation="csr",
+                    use_full_blocks=use_full)
+    ref = scheduled_attention(q, k, v, schedule, spec, use_full_blocks=use_full)
+    torch.testing.assert_close(out.float().cpu(), ref.float(), atol=2e-2, rtol=2e-2)
+    unedited = masked_attention(q, k, v, spec_mask(n, spec))[0]
+    assert (ref - unedited).abs().max() > 0.1  # the edits matter

@@ -133,3 +133,38 @@ def test_masked_attention_matches_sdpa_fp64_and_empty_rows():
     empty = torch.zeros(n, n, dtype=torch.bool)
     out, lse = masked_attention(q, k, v, empty)
     assert torch.equal(out, torch.zeros_like(out)) and torch.isneginf(lse).all()
+
+
+def test_scheduled_attention_equals_dense_oracle_for_compiled_schedules():
+    """The schedule interpreter (validate.py:31-55) on compiler output is the dense-mask oracle,
+    and a hand-edited schedule changes it exactly where the edit says."""
+    from oracle.attention import scheduled_attention, spec_mask
+    from systems_for_llms_amd.masks import MaskSpec, compile_mask
+
+    g = torch.Generator().manual_seed(11)
+    n = 150
+    q, k, v = (torch.randn(2, n, 16, dtype=torch.float64, generator=g) for _ in range(3))
+    docs = [i // 37 for i in range(n)]
+    for spec, documents, block in ((MaskSpec(causal=True), None, 32),
+                                   (MaskSpec(causal=True, window_left=40), None, 64),
+                                   (MaskSpec(window_left=20, window_right=9), None, 16),
+                                   (MaskSpec(causal=True, same_document=True), docs, 32)):
+        schedule = compile_mask(n, spec, block, block, documents)
+        ref = masked_attention(q, k, v, spec_mask(n, spec, documents))[0]
+        for use_full in (True, False):
+            got = scheduled_attention(q, k, v, schedule, spec, documents, use_full_blocks=use_full)
+            torch.testing.assert_close(got, ref, atol=1e-12, rtol=1e-12)
+    # Flag the diagonal (partial) tile of query tile 1 as full: its queries then see future keys.
+    spec = MaskSpec(causal=True)
+    schedule = compile_mask(n, spec, 32, 32)
+    j = schedule.row_ptr[2] - 1
+    assert schedule.col_idx[j] == 1 and not schedule.full_blocks[j]
+    schedule.full_blocks[j] = True
+    edited = masked_attention(q, k, v, spec_mask(n, spec) | _tile(n, 32, 1, 1))[0]
+    torch.testing.assert_close(scheduled_attention(q, k, v, schedule, spec), edited, atol=1e-12, rtol=1e-12)
+
+
+def _tile(n, block, row, col):
+    mask = torch.zeros((n, n), dtype=torch.bool)
+    mask[row * block:(row + 1) * block, col * block:(col + 1) * block] = True
+    return mask
