@@ -212,11 +212,11 @@ template <typename T> struct SrcOf<true, T> { using type = NormChunk<T>; };
 // chunks fit kWaves*CPW); chosen on the host so no wave issues more loads than
 // it needs. A workgroup owns one (tile, K part) item -- tile = item % tiles,
 // part = item / tiles (one part unless RESIDUAL splits K) -- for one block of
-// 16 batch rows. With one block, workgroup w owns item w. With several, the
-// blocks of one item go to workgroups w = 8 (g * blocks + blk) + x for item
-// 8 g + x: the same XCD (w % 8 == x), so the item's weights come from HBM
-// once and from that XCD's L2 for the other blocks.
-template <typename T, int E, int CPW>
+// 16 batch rows. With one block (kBlocks false), workgroup w owns item w.
+// With several, the blocks of one item go to workgroups w = 8 (g * blocks +
+// blk) + x for item 8 g + x: the same XCD (w % 8 == x), so the item's weights
+// come from HBM once and from that XCD's L2 for the other blocks.
+template <typename T, int E, int CPW, bool kBlocks>
 __global__ __launch_bounds__(kWaves * kWave) void linear_kernel(LinearArgs a) {
   constexpr int KC = chunk_k<T>();
   constexpr int EPL = vec_elems<T>();
@@ -231,17 +231,20 @@ __global__ __launch_bounds__(kWaves * kWave) void linear_kernel(LinearArgs a) {
   const int K = a.k;
 
   constexpr int CB = act_chunk_bytes<T>();
+  // The loads wait for these indices: the one-block instantiation keeps its
+  // prologue to two unsigned divisions.
   const int tiles = (a.n + kTileN - 1) / kTileN;
-  const int blocks = (a.batch + kBlockRows - 1) / kBlockRows;
-  int item = int(blockIdx.x), blk = 0;
-  if (blocks > 1) {
-    const int w = int(blockIdx.x), x = w % kXcds, r = w / kXcds;
-    blk = r % blocks;
-    item = (r / blocks) * kXcds + x;
-    if (item >= tiles * a.ksplit) return;  // padding of the last group of 8 items
+  unsigned item = blockIdx.x;
+  int blk = 0;
+  if constexpr (kBlocks) {
+    const unsigned blocks = (unsigned(a.batch) + kBlockRows - 1) / kBlockRows;
+    const unsigned r = blockIdx.x / kXcds;
+    blk = int(r % blocks);
+    item = (r / blocks) * kXcds + blockIdx.x % kXcds;
+    if (item >= unsigned(tiles) * unsigned(a.ksplit)) return;  // padding of the last group of 8 items
   }
-  const int tile = item % tiles;
-  const int part = item / tiles;
+  const int tile = int(item % unsigned(tiles));
+  const int part = int(item / unsigned(tiles));
   const int n0 = tile * kTileN;
   const int grp = lane / 16;
   const int b = blk * kBlockRows + lane % 16;  // this lane's batch row
@@ -456,9 +459,15 @@ template <typename T, int E, int CPW>
 int launch_linear_cpw(const LinearArgs& a, hipStream_t stream, const char* what) {
   const long items = long((a.n + kTileN - 1) / kTileN) * a.ksplit;
   const long blocks = (a.batch + kBlockRows - 1) / kBlockRows;
-  const long grid = blocks == 1 ? items : (items + kXcds - 1) / kXcds * kXcds * blocks;
-  if (grid > (1L << 31) - 1) return set_error(SFL_ERR_UNSUPPORTED, "%s: too many workgroups", what);
-  hipLaunchKernelGGL((linear_kernel<T, E, CPW>), dim3(unsigned(grid)), dim3(kWaves * kWave), 0, stream, a);
+  if (blocks == 1) {
+    hipLaunchKernelGGL((linear_kernel<T, E, CPW, false>), dim3(unsigned(items)), dim3(kWaves * kWave), 0,
+                       stream, a);
+  } else {
+    const long grid = (items + kXcds - 1) / kXcds * kXcds * blocks;
+    if (grid > (1L << 31) - 1) return set_error(SFL_ERR_UNSUPPORTED, "%s: too many workgroups", what);
+    hipLaunchKernelGGL((linear_kernel<T, E, CPW, true>), dim3(unsigned(grid)), dim3(kWaves * kWave), 0,
+                       stream, a);
+  }
   return check_launch(what);
 }
 
