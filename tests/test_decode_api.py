@@ -39,6 +39,13 @@ def test_auto_splits_bounds():
     assert auto_splits(1, 16, 4096) == 4     # single sequence: split the context
     assert auto_splits(1, 4, 1024) == 1
     assert auto_splits(1, 1, 10) == 1
+    # Grouped query heads: more, shorter splits (about 512 workgroups of >= 512 / G keys).
+    assert auto_splits(1, 4, 1024, 8) == 16
+    assert auto_splits(1, 4, 4096, 8) == 64
+    assert auto_splits(8, 4, 16384, 8) == 16
+    assert auto_splits(32, 4, 4096, 8) == 4
+    assert auto_splits(1, 8, 4096, 4) == 32
     for b, h, n in ((1, 1, 1), (3, 5, 999), (128, 32, 65536)):
-        s = auto_splits(b, h, n)
-        assert 1 <= s <= 128
+        for g in (1, 2, 4, 8):
+            s = auto_splits(b, h, n, g)
+            assert 1 <= s <= 128
