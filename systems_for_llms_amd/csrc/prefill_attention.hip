@@ -803,41 +803,59 @@ __device__ __forceinline__ void attn32_tile(const AttnArgs& a, const uint4 (&kt)
 // CSR row (mode 1) or the interval row (global blocks [0, lowg), then window
 // blocks [begin, end)). A row that starts past the sequence has none.
 struct TileRow {
-  RowSched rs;
-  TileBounds tb;
-  int lowg, count, i;
+  const int32_t* col;  // CSR row (mode 1)
+  const uint8_t* full;
+  TileBounds tb;       // interval row (mode 0)
+  int n, lowg, count, i, first, reg;
+  bool csr, no_docs;
   __device__ __forceinline__ void init(const AttnArgs& a, int row) {
-    const int n = a.n, q0 = row * BQ;
+    n = a.n;
+    const int q0 = row * BQ;
     const bool live = q0 < n;
+    csr = a.s.mode == 1;
+    no_docs = !a.m.docs;
     tb = tile_bounds(a.m, n, q0, min(q0 + BQ, n) - 1);
     lowg = min(tb.gend, tb.begin);
     int base = 0;
     if (!live) {
       count = 0;
-    } else if (a.s.mode == 1) {
+    } else if (csr) {
       base = __builtin_amdgcn_readfirstlane(a.s.row_ptr[row]);
       count = __builtin_amdgcn_readfirstlane(a.s.row_ptr[row + 1]) - base;
     } else {
       count = lowg + max(0, max(tb.end, tb.gend) - tb.begin);
     }
-    rs = RowSched{a.s.col_idx + base, a.s.full + base, count, 0, 0};
-    if (a.s.mode == 1 && live) rs.fetch(0);
+    col = a.s.col_idx + base;
+    full = a.s.full + base;
     i = 0;
+    fill(0);
+  }
+  // Entries first .. first + 63 of the row into one VGPR (lane l: entry
+  // first + l as 2 * key block + full), read from the CSR row or generated
+  // from the interval bounds, so every tile's entry is then a readlane.
+  __device__ __forceinline__ void fill(int f) {
+    first = f;
+    const int e = f + int(threadIdx.x % kWave);
+    reg = 0;
+    if (e < count) {
+      if (csr) {
+        reg = 2 * col[e] + int(full[e] != 0);
+      } else {
+        const int kb = e < lowg ? e : tb.begin + (e - lowg);
+        reg = 2 * kb + int(no_docs && covered(tb, kb * BK, min(kb * BK + BK, n) - 1));
+      }
+    }
   }
   // The next tile's key block (INT_MAX when the row is done) and full flag.
-  __device__ __forceinline__ int peek(const AttnArgs& a, bool& full) {
+  __device__ __forceinline__ int peek(bool& is_full) {
     if (i >= count) {
-      full = false;
+      is_full = false;
       return INT_MAX;
     }
-    int kb;
-    if (a.s.mode == 1) {
-      rs.at(i, kb, full);
-    } else {
-      kb = i < lowg ? i : tb.begin + (i - lowg);
-      full = !a.m.docs && covered(tb, kb * BK, min(kb * BK + BK, a.n) - 1);
-    }
-    return kb;
+    if ((i & ~63) != first) fill(i & ~63);
+    const int e = __builtin_amdgcn_readlane(reg, i & 63);
+    is_full = (e & 1) != 0;
+    return e >> 1;
   }
 };
 
@@ -849,8 +867,8 @@ struct MergedTile {
 };
 __device__ __forceinline__ MergedTile next_tile(const AttnArgs& a, TileRow (&rows)[2]) {
   MergedTile t;
-  const int c0 = rows[0].peek(a, t.full[0]);
-  const int c1 = rows[1].peek(a, t.full[1]);
+  const int c0 = rows[0].peek(t.full[0]);
+  const int c1 = rows[1].peek(t.full[1]);
   t.kb = min(c0, c1);
   t.in[0] = c0 == t.kb && c0 != INT_MAX;
   t.in[1] = c1 == t.kb && c1 != INT_MAX;
