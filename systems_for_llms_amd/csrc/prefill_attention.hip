@@ -691,11 +691,22 @@ __device__ __forceinline__ unsigned vt_slot(unsigned sg, unsigned r) { return 2u
 // Byte offset, within a tile, of lane l's 8-byte piece for key step 0, dim
 // tile t, first key half: key row 4(g >> 1) + (m >> 2), dims 32t + 16(g & 1) +
 // 4(m & 3) .. +3, with g = l / 16 and m = l % 16.
+template <int D>
 __device__ __forceinline__ unsigned vt_lane_offset(int lane, int t) {
   const unsigned g = unsigned(lane) / 16u, m = unsigned(lane) % 16u;
   const unsigned r = 4u * (g >> 1) + (m >> 2);
   const unsigned dim = 32u * unsigned(t) + 16u * (g & 1u) + 4u * (m & 3u);
-  return r * 128u + 16u * vt_slot(dim / 8u, r) + 2u * (dim % 8u);
+  return r * (2u * D) + 16u * vt_slot(dim / 8u, r) + 2u * (dim % 8u);
+}
+
+// K tile swizzle: row r's logical 16-byte slot s sits at s ^ k_swizzle<D>(r).
+// The operand reads take one logical slot of 16 consecutive rows per LDS
+// cycle; rows of 128 bytes (D = 64) alternate bank halves, so (r >> 1) & 7
+// separates the rest, and rows of 256 bytes (D = 128) all start at bank 0, so
+// the slot itself is rotated by r & 15.
+template <int D>
+__device__ __forceinline__ int k_swizzle(int r) {
+  return D == 64 ? (r >> 1) & 7 : r & 15;
 }
 
 typedef short i16x4_t __attribute__((ext_vector_type(4)));
@@ -703,11 +714,11 @@ typedef __attribute__((address_space(3))) i16x4_t lds_i16x4_t;
 
 constexpr float kLazyMax = 8.f;
 
-template <typename T, bool kMask>
-__device__ __forceinline__ void attn32_tile(const AttnArgs& a, const uint4 (&kt)[BK][8], const uint4 (&vt)[BK][8],
-                                            const u32x4 (&qreg)[4], f32x16 (&oacc)[2], float& m_run,
-                                            float& l_run, int c, int h, int qrow, int k0, bool full,
-                                            unsigned vlane0, unsigned vlane1) {
+template <typename T, bool kMask, int D>
+__device__ __forceinline__ void attn32_tile(const AttnArgs& a, const uint4 (&kt)[BK][D / 8],
+                                            const uint4 (&vt)[BK][D / 8], const u32x4 (&qreg)[D / 16],
+                                            f32x16 (&oacc)[D / 32], float& m_run, float& l_run, int c, int h,
+                                            int qrow, int k0, bool full, const unsigned (&vlane)[D / 32]) {
   const int n = a.n;
   f32x16 sacc[2];
 #pragma unroll
@@ -715,8 +726,8 @@ __device__ __forceinline__ void attn32_tile(const AttnArgs& a, const uint4 (&kt)
 #pragma unroll
     for (int j = 0; j < 16; ++j) sacc[kb2][j] = 0.f;
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      const uint4 kr = kt[32 * kb2 + c][(4 * h + ks) ^ ((c >> 1) & 7)];
+    for (int ks = 0; ks < D / 16; ++ks) {
+      const uint4 kr = kt[32 * kb2 + c][(D / 16 * h + ks) ^ k_swizzle<D>(c)];
       sacc[kb2] = mfma32<T>(u32x4{kr.x, kr.y, kr.z, kr.w}, qreg[ks], sacc[kb2]);
     }
   }
@@ -765,7 +776,7 @@ __device__ __forceinline__ void attn32_tile(const AttnArgs& a, const uint4 (&kt)
     alpha = grow ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.f;  // 0 for the first admissible tile
     m_run = m_new;
 #pragma unroll
-    for (int t = 0; t < 2; ++t) oacc[t] *= alpha;
+    for (int t = 0; t < D / 32; ++t) oacc[t] *= alpha;
   }
   const float ms = m_run == -INFINITY ? 0.f : m_run;
   u32x4 pop[4];
@@ -783,16 +794,17 @@ __device__ __forceinline__ void attn32_tile(const AttnArgs& a, const uint4 (&kt)
     pop[s2] = u32x4{pk[0], pk[1], pk[2], pk[3]};
   }
   l_run = l_run * alpha + ((psum[0] + psum[1]) + (psum[2] + psum[3]));
-  // V^T operands: this lane's piece for step s2, dim tile t and key half is
-  // at byte vlane_t + 2048 s2 + 1024 half of the tile (vt_lane_offset).
+  // V^T operands: this lane's piece for step s2 (16 keys of 2D bytes), dim
+  // tile t and key half (8 keys) is at byte vlane[t] + 32 D s2 + 16 D half
+  // of the tile (vt_lane_offset).
   const unsigned vbase = unsigned(size_t((__attribute__((address_space(3))) const char*)(&vt[0][0])));
 #pragma unroll
   for (int s2 = 0; s2 < 4; ++s2) {
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const unsigned off = vbase + (t ? vlane1 : vlane0) + 2048u * s2;
+    for (int t = 0; t < D / 32; ++t) {
+      const unsigned off = vbase + vlane[t] + 32u * D * s2;
       const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(size_t)(off));
-      const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(size_t)(off + 1024u));
+      const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(size_t)(off + 16u * D));
       const uint2 l2 = __builtin_bit_cast(uint2, lo), h2 = __builtin_bit_cast(uint2, hi);
       oacc[t] = mfma32<T>(u32x4{l2.x, l2.y, h2.x, h2.y}, pop[s2], oacc[t]);
     }
@@ -886,11 +898,19 @@ constexpr int kA32Waves = 4;
 // merge of its two rows' tile lists; a wave skips (but still synchronises on)
 // a tile its own row does not list, so each row processes exactly its own
 // tiles, as the 64-query tiling would.
-template <typename T>
-__global__ __launch_bounds__(kA32Waves * kWave) __attribute__((amdgpu_waves_per_eu(3))) void masked_attention32_kernel(AttnArgs a) {
-  constexpr int D = 64, QB = 2 * BQ;
-  __shared__ __align__(16) uint4 k_s[2][BK][8];  // [key][16-byte slot s at s ^ ((key >> 1) & 7)]
-  __shared__ __align__(16) uint4 v_s[2][BK][8];  // [key][16-byte slot, see vt_slot]
+// Head dim 64: 32 KB of LDS per workgroup, 168 VGPRs, 3 waves per SIMD. Head
+// dim 128: the same layout with 256-byte rows (64 KB, two workgroups per CU,
+// 2 waves per SIMD), 8 k-steps per score block and 4 dim tiles of O.
+template <int D> constexpr int attn32_waves_per_eu() { return D == 64 ? 3 : 2; }
+
+template <typename T, int D>
+__global__ __launch_bounds__(kA32Waves * kWave) __attribute__((amdgpu_waves_per_eu(attn32_waves_per_eu<D>())))
+void masked_attention32_kernel(AttnArgs a) {
+  constexpr int QB = 2 * BQ;
+  constexpr int SL = D / 8;      // 16-byte slots per K/V row
+  constexpr int RPL = 64 / SL;   // rows one 1 KB load moves
+  __shared__ __align__(16) uint4 k_s[2][BK][SL];  // [key][16-byte slot s at s ^ k_swizzle<D>(key)]
+  __shared__ __align__(16) uint4 v_s[2][BK][SL];  // [key][16-byte slot, see vt_slot]
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave), lane = tid % kWave;
   const int half = wave / 2;
@@ -910,21 +930,21 @@ __global__ __launch_bounds__(kA32Waves * kWave) __attribute__((amdgpu_waves_per_
   const uint16_t* kp = static_cast<const uint16_t*>(a.k) + b * a.ks[0] + hd * a.ks[1];
   const uint16_t* vp = static_cast<const uint16_t*>(a.v) + b * a.vs[0] + hd * a.vs[1];
 
-  // Q^T operand of k-step ks: Q[qrow][32h + 8ks .. +8].
-  u32x4 qreg[4];
+  // Q^T operand of k-step ks: Q[qrow][(D/2) h + 8ks .. +8].
+  u32x4 qreg[D / 16];
   {
-    const uint16_t* qr = qp + long(min(qrow, n - 1)) * a.qs[2] + 32 * h;
+    const uint16_t* qr = qp + long(min(qrow, n - 1)) * a.qs[2] + (D / 2) * h;
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
+    for (int ks = 0; ks < D / 16; ++ks) {
       const uint4 r = load16(qr + 8 * ks);
       qreg[ks] = u32x4{r.x, r.y, r.z, r.w};
     }
   }
 
   float m_run = -INFINITY, l_run = 0.f;
-  f32x16 oacc[2];
+  f32x16 oacc[D / 32];
 #pragma unroll
-  for (int t = 0; t < 2; ++t)
+  for (int t = 0; t < D / 32; ++t)
 #pragma unroll
     for (int j = 0; j < 16; ++j) oacc[t][j] = 0.f;
 
@@ -932,33 +952,36 @@ __global__ __launch_bounds__(kA32Waves * kWave) __attribute__((amdgpu_waves_per_
   rows[0].init(a, 2 * qt);
   rows[1].init(a, 2 * qt + 1);
 
-  // K tile: 8 loads of 8 rows (1 KB) per tile, 2 per wave; lane i moves row
-  // r = 8ch + i/8, logical slot (i%8) ^ ((r >> 1) & 7) into physical slot i%8
-  // (the swizzle under which the 128-bit operand reads, 32 rows by 2 slot
-  // groups, are free of LDS bank conflicts; measured). ch is 4 cw + wave, so
-  // (r >> 1) & 7 = 4 (wave & 1) + i/16 for every load of this wave. The buffer
-  // covers this head's rows [0, n): rows past n read as zeros.
-  static_assert(kA32Waves % 2 == 0, "the K swizzle below assumes ch & 1 == wave & 1");
+  // K tile: BK / RPL loads of RPL rows (1 KB) per tile, shared by the waves;
+  // lane i moves row r = RPL ch + i/SL, logical slot (i%SL) ^ k_swizzle(r)
+  // into physical slot i%SL (the swizzle under which the 128-bit operand
+  // reads are free of LDS bank conflicts; measured). ch is kA32Waves cw +
+  // wave, and k_swizzle only sees the low bits of r, so one byte offset per
+  // lane serves every load of this wave. The buffer covers this head's rows
+  // [0, n): rows past n read as zeros.
+  static_assert(kA32Waves == 4, "the K swizzle below assumes ch % 4 == wave");
   const unsigned krow_bytes = unsigned(a.ks[2]) * 2u;
   const i32x4_t krsrc = buffer_rsrc(kp, unsigned((long(n - 1) * a.ks[2] + D) * 2));
-  const unsigned kvoff =
-      unsigned(lane / 8) * krow_bytes + 16u * unsigned((lane % 8) ^ (4 * (wave & 1) + lane / 16));
-  // V tile: the same 8 loads of 8 rows; lane i moves row 8ch + i/8, logical
-  // slot sg with vt_slot(sg, i/8) == i%8, into physical slot i%8.
+  const int lrr = lane / SL, lpp = lane % SL;
+  const unsigned kvoff = unsigned(lrr) * krow_bytes + 16u * unsigned(lpp ^ k_swizzle<D>(RPL * wave + lrr));
+  // V tile: the same loads; lane i moves row RPL ch + i/SL, logical slot sg
+  // with vt_slot(sg, row) == i%SL, into physical slot i%SL (row & 3 == (i/SL) & 3).
   const unsigned vrow_bytes = unsigned(a.vs[2]) * 2u;
   const i32x4_t vrsrc = buffer_rsrc(vp, unsigned((long(n - 1) * a.vs[2] + D) * 2));
-  const unsigned vpp = unsigned(lane % 8), vrr = unsigned(lane / 8);
-  const unsigned vvoff = vrr * vrow_bytes + 16u * (2u * ((vpp >> 1) ^ (vrr & 3u)) + (vpp & 1u));
-  const unsigned vlane0 = vt_lane_offset(lane, 0), vlane1 = vt_lane_offset(lane, 1);
+  const unsigned vvoff = unsigned(lrr) * vrow_bytes +
+                         16u * (2u * ((unsigned(lpp) >> 1) ^ (unsigned(lrr) & 3u)) + (unsigned(lpp) & 1u));
+  unsigned vlane[D / 32];
+#pragma unroll
+  for (int t = 0; t < D / 32; ++t) vlane[t] = vt_lane_offset<D>(lane, t);
 #define SFL_A32_LOAD(kb, kbuf)                                                              \
   {                                                                                         \
     const int k0_ = (kb) * BK;                                                              \
-    _Pragma("unroll") for (int cw = 0; cw < BK / 8 / kA32Waves; ++cw) {                     \
+    _Pragma("unroll") for (int cw = 0; cw < BK / RPL / kA32Waves; ++cw) {                   \
       const int ch_ = cw * kA32Waves + wave;                                                \
-      lds_load16(krsrc, lds_offset(&k_s[kbuf][8 * ch_][0]), kvoff,                          \
-                 unsigned(k0_ + 8 * ch_) * krow_bytes);                                     \
-      lds_load16(vrsrc, lds_offset(&v_s[kbuf][8 * ch_][0]), vvoff,                          \
-                 unsigned(k0_ + 8 * ch_) * vrow_bytes);                                     \
+      lds_load16(krsrc, lds_offset(&k_s[kbuf][RPL * ch_][0]), kvoff,                        \
+                 unsigned(k0_ + RPL * ch_) * krow_bytes);                                   \
+      lds_load16(vrsrc, lds_offset(&v_s[kbuf][RPL * ch_][0]), vvoff,                        \
+                 unsigned(k0_ + RPL * ch_) * vrow_bytes);                                   \
     }                                                                                       \
   }
   // One key tile: S^T, masked online softmax, O^T += V^T P^T.
@@ -973,11 +996,9 @@ __global__ __launch_bounds__(kA32Waves * kWave) __attribute__((amdgpu_waves_per_
     const bool full = (half ? cur.full[1] : cur.full[0]) && a.s.use_full;
     if (half ? cur.in[1] : cur.in[0]) {
       if (full && k0 + BK <= n)
-        attn32_tile<T, false>(a, k_s[buf], v_s[buf], qreg, oacc, m_run, l_run, c, h, qrow, k0, full, vlane0,
-                              vlane1);
+        attn32_tile<T, false, D>(a, k_s[buf], v_s[buf], qreg, oacc, m_run, l_run, c, h, qrow, k0, full, vlane);
       else
-        attn32_tile<T, true>(a, k_s[buf], v_s[buf], qreg, oacc, m_run, l_run, c, h, qrow, k0, full, vlane0,
-                             vlane1);
+        attn32_tile<T, true, D>(a, k_s[buf], v_s[buf], qreg, oacc, m_run, l_run, c, h, qrow, k0, full, vlane);
     }
     __builtin_amdgcn_s_waitcnt(sfl_vmcnt(0));  // the next K and V tiles have landed
     __syncthreads();
@@ -990,7 +1011,7 @@ __global__ __launch_bounds__(kA32Waves * kWave) __attribute__((amdgpu_waves_per_
   const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
   uint16_t* op = static_cast<uint16_t*>(a.o) + b * a.os[0] + hd * a.os[1] + long(qrow) * a.os[2];
 #pragma unroll
-  for (int t = 0; t < 2; ++t)
+  for (int t = 0; t < D / 32; ++t)
 #pragma unroll
     for (int jq = 0; jq < 4; ++jq)
       *reinterpret_cast<uint2*>(op + 32 * t + 8 * jq + 4 * h) =
@@ -1011,12 +1032,18 @@ int launch_masked(const AttnArgs& a, int batch, int dim, hipStream_t stream) {
       // The 32x32 kernel addresses K and V with 32-bit buffer offsets; its
       // workgroups take two 64-query rows each.
       if (long(a.n) * a.ks[2] * 2 < (1L << 31) && long(a.n) * a.vs[2] * 2 < (1L << 31))
-        hipLaunchKernelGGL((masked_attention32_kernel<T>), dim3(unsigned((a.n + 2 * BQ - 1) / (2 * BQ)) *
+        hipLaunchKernelGGL((masked_attention32_kernel<T, 64>), dim3(unsigned((a.n + 2 * BQ - 1) / (2 * BQ)) *
                            unsigned(batch * a.heads)), dim3(kA32Waves * kWave), 0, stream, a);
       else
         hipLaunchKernelGGL((masked_attention_pair_kernel<T>), grid, dim3(kPairWaves * kWave), 0, stream, a);
       break;
-    case 128: hipLaunchKernelGGL((masked_attention_kernel<T, 128>), grid, dim3(kThreads), 0, stream, a); break;
+    case 128:
+      if (long(a.n) * a.ks[2] * 2 < (1L << 31) && long(a.n) * a.vs[2] * 2 < (1L << 31))
+        hipLaunchKernelGGL((masked_attention32_kernel<T, 128>), dim3(unsigned((a.n + 2 * BQ - 1) / (2 * BQ)) *
+                           unsigned(batch * a.heads)), dim3(kA32Waves * kWave), 0, stream, a);
+      else
+        hipLaunchKernelGGL((masked_attention_kernel<T, 128>), grid, dim3(kThreads), 0, stream, a);
+      break;
     default: return set_error(SFL_ERR_UNSUPPORTED, "masked_attention: head dim must be 32, 64 or 128");
   }
   return check_launch("masked_attention");
