@@ -15,6 +15,8 @@
 // intra-row dot-product reduction; the slots are merged once at the end of
 // the chunk with xor shuffles. Max and sum are kept in base-2 units.
 #include "act_format.hpp"
+#include "attn_mfma.hpp"
+#include "lds_dma.hpp"
 
 namespace sfl {
 namespace {
@@ -396,6 +398,222 @@ int launch_merge(const float* pmax, const float* psum, const float* pout, const 
   return check_launch("decode_merge");
 }
 
+// Grouped-query decode on the matrix cores. With G >= 4 query heads per KV
+// head the kernel above does G dot products and G multiply-adds per key
+// element on the VALU, which takes longer than streaming the element from HBM
+// (D = 128, G = 8: ~2 TB/s). Here one 32x32x16 MFMA block holds a 32-key
+// tile against all G heads: S^T = K Q^T with the heads as the B operand's
+// columns (zero past G), then O^T += V^T P^T, exactly the tile step of the
+// masked prefill attention (prefill_attention.hip) with the group's heads in
+// place of 32 queries. Each of the 4 waves owns every 4th 32-key tile of the
+// split and stages it in its own double-buffered LDS slots through LDS DMA:
+// K rows swizzled for the operand reads (k_swizzle), V rows laid out for the
+// transpose reads (vt_slot). The buffer range ends at the split's last key,
+// so key rows past the length read as zeros and stale cache rows (NaN
+// included) never reach the products. The waves' states are merged through
+// LDS (reusing the tile buffers) as in decode_attn_kernel, and the workgroup
+// writes the output or the same base-2 (max, sum, numerator) partial, which
+// decode_merge_kernel combines.
+constexpr int kGqaWaves = 4;
+constexpr int kGqaTile = 32;  // keys per wave tile
+
+template <typename T, int D, bool kMask>
+__device__ __forceinline__ void gqa32_tile(const uint4 (&kt)[kGqaTile][D / 8], const uint4 (&vt)[kGqaTile][D / 8],
+                                           const u32x4 (&qreg)[D / 16], f32x16 (&oacc)[D / 32], float& m_run,
+                                           float& l_run, int c, int h, int t0, int end, float cs,
+                                           const unsigned (&vlane)[D / 32]) {
+  f32x16 s;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) s[j] = 0.f;
+#pragma unroll
+  for (int ks = 0; ks < D / 16; ++ks) {
+    const uint4 kr = kt[c][(D / 16 * h + ks) ^ k_swizzle<D>(c)];
+    s = mfma32<T>(u32x4{kr.x, kr.y, kr.z, kr.w}, qreg[ks], s);
+  }
+  if constexpr (kMask) {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) s[j] = t0 + 8 * (j / 4) + 4 * h + j % 4 < end ? s[j] : -INFINITY;
+  }
+  float mx = fmaxf(s[0], s[1]);
+#pragma unroll
+  for (int j = 2; j < 16; j += 2) mx = fmaxf(fmaxf(mx, s[j]), s[j + 1]);
+  mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+  // Lazy maximum (as in the prefill tile): m_run moves only when a head's
+  // tile maximum exceeds it by more than kLazyMax, so probabilities stay
+  // below 2^kLazyMax and O is rescaled only on those tiles.
+  const bool grow = mx * cs > m_run + kLazyMax;
+  float alpha = 1.f;
+  if (__ballot(grow)) {
+    const float m_new = grow ? mx * cs : m_run;
+    alpha = grow ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.f;
+    m_run = m_new;
+#pragma unroll
+    for (int t = 0; t < D / 32; ++t) oacc[t] *= alpha;
+  }
+  const float ms = m_run == -INFINITY ? 0.f : m_run;
+  u32x4 pop[2];
+  float psum[2] = {0.f, 0.f};
+#pragma unroll
+  for (int s2 = 0; s2 < 2; ++s2) {
+    uint32_t pk[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int j0 = 8 * s2 + 2 * e;
+      pk[e] = pack2<T>(__builtin_amdgcn_exp2f(fmaf(s[j0], cs, -ms)), __builtin_amdgcn_exp2f(fmaf(s[j0 + 1], cs, -ms)));
+      psum[s2] = add_pair<T>(pk[e], psum[s2]);
+    }
+    pop[s2] = u32x4{pk[0], pk[1], pk[2], pk[3]};
+  }
+  l_run = l_run * alpha + (psum[0] + psum[1]);
+  const unsigned vbase = lds_offset(&vt[0][0]);
+#pragma unroll
+  for (int s2 = 0; s2 < 2; ++s2) {
+#pragma unroll
+    for (int t = 0; t < D / 32; ++t) {
+      const unsigned off = vbase + vlane[t] + 32u * D * s2;
+      const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(size_t)(off));
+      const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(size_t)(off + 16u * D));
+      const uint2 l2 = __builtin_bit_cast(uint2, lo), h2 = __builtin_bit_cast(uint2, hi);
+      oacc[t] = mfma32<T>(u32x4{l2.x, l2.y, h2.x, h2.y}, pop[s2], oacc[t]);
+    }
+  }
+}
+
+// One workgroup of 4 waves per (batch, kv head, split), grid order as
+// decode_attn_kernel. The host admits 16-byte aligned q/k/v and caches of
+// cap * D * 2 < 2^31 bytes per head (32-bit buffer offsets).
+template <typename T, typename TO, int D, int G>
+__global__ __launch_bounds__(kGqaWaves * kWave) void decode_gqa32_kernel(
+    const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
+    const int32_t* __restrict__ lengths, float* __restrict__ pmax, float* __restrict__ psum,
+    float* __restrict__ pout, void* __restrict__ out, int kv_heads, int cap, int splits, int chunk,
+    float cs) {
+  constexpr int W = kGqaWaves, BT = kGqaTile;
+  constexpr int SL = D / 8;        // 16-byte slots per key row
+  constexpr int RPL = kWave / SL;  // key rows one 1 KB DMA load moves
+  constexpr int NLD = BT / RPL;    // DMA loads per tile and operand
+  static_assert(G <= 32 && NLD * RPL == BT, "tile shape");
+  __shared__ __align__(16) uint4 kv_s[W][2][2][BT][SL];  // [wave][buffer][K, V][key][slot]
+  typedef float MergeRow[G][D + 2];
+  static_assert(sizeof(MergeRow) * W <= sizeof(kv_s), "the merge rows fit the tile buffers");
+  MergeRow* sm = reinterpret_cast<MergeRow*>(&kv_s[0][0][0][0][0]);
+  const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x) / kWave);
+  const int lane = threadIdx.x % kWave;
+  const int c = lane % 32, h = lane / 32;
+  const int split = int(blockIdx.x % splits);
+  const long bh = blockIdx.x / splits;
+  const int hk = int(bh % kv_heads), b = int(bh / kv_heads);
+  const int q_heads = kv_heads * G;
+
+  // Q^T operand of k-step ks: head c's dims (D/2) h + 8 ks .. +7; zero past G.
+  // The select waits for the loads here, before the tile prefetch is issued.
+  u32x4 qreg[D / 16];
+  {
+    const T* qp = q + (long(b) * q_heads + hk * G + min(c, G - 1)) * D + (D / 2) * h;
+#pragma unroll
+    for (int ks = 0; ks < D / 16; ++ks) {
+      const uint4 r = load16(qp + 8 * ks);
+      qreg[ks] = c < G ? u32x4{r.x, r.y, r.z, r.w} : u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+  const int len = min(max(__builtin_amdgcn_readfirstlane(lengths[b]), 0), cap);
+  const int begin = split * chunk;
+  if (splits > 1 && begin >= len) return;  // the merge reads only chunks below the length
+  const int end = min(len, begin + chunk);
+
+  const long head0 = (long(b) * kv_heads + hk) * cap * D;
+  constexpr unsigned kRow = 2u * D;  // bytes per key row
+  const i32x4_t krsrc = buffer_rsrc(k + head0, unsigned(end) * kRow);
+  const i32x4_t vrsrc = buffer_rsrc(v + head0, unsigned(end) * kRow);
+  // DMA load j of a tile moves rows RPL j .. RPL j + RPL - 1; lane i takes
+  // row RPL j + i / SL into physical slot i % SL: the K slot (i % SL) ^
+  // k_swizzle(row), the V slot sg with vt_slot(sg, row) == i % SL (row & 3 ==
+  // (i / SL) & 3 for every j).
+  const int lrr = lane / SL, lpp = lane % SL;
+  unsigned kvoff[NLD];
+#pragma unroll
+  for (int j = 0; j < NLD; ++j) {
+    const int r = RPL * j + lrr;
+    kvoff[j] = unsigned(r) * kRow + 16u * unsigned(lpp ^ k_swizzle<D>(r));
+  }
+  const unsigned vvoff = unsigned(lrr) * kRow + 16u * (2u * ((unsigned(lpp) >> 1) ^ (unsigned(lrr) & 3u)) + (unsigned(lpp) & 1u));
+  unsigned vlane[D / 32];
+#pragma unroll
+  for (int t = 0; t < D / 32; ++t) vlane[t] = vt_lane_offset<D>(lane, t);
+  auto issue = [&](int tile0, int buf) {
+#pragma unroll
+    for (int j = 0; j < NLD; ++j) {
+      lds_load16(krsrc, lds_offset(&kv_s[wave][buf][0][RPL * j][0]), kvoff[j], unsigned(tile0) * kRow);
+      lds_load16(vrsrc, lds_offset(&kv_s[wave][buf][1][RPL * j][0]), vvoff, unsigned(tile0 + RPL * j) * kRow);
+    }
+  };
+
+  float m_run = -INFINITY, l_run = 0.f;
+  f32x16 oacc[D / 32];
+#pragma unroll
+  for (int t = 0; t < D / 32; ++t)
+#pragma unroll
+    for (int j = 0; j < 16; ++j) oacc[t][j] = 0.f;
+
+  int t0 = begin + BT * wave;
+  if (t0 < end) issue(t0, 0);
+  for (int buf = 0; t0 < end; buf ^= 1) {
+    const int tn = t0 + BT * W;
+    if (tn < end) {
+      issue(tn, buf ^ 1);
+      __builtin_amdgcn_s_waitcnt(sfl_vmcnt(2 * NLD));  // this tile has landed, the next is in flight
+    } else {
+      __builtin_amdgcn_s_waitcnt(sfl_vmcnt(0));
+    }
+    if (t0 + BT <= end)
+      gqa32_tile<T, D, false>(kv_s[wave][buf][0], kv_s[wave][buf][1], qreg, oacc, m_run, l_run, c, h, t0, end, cs, vlane);
+    else
+      gqa32_tile<T, D, true>(kv_s[wave][buf][0], kv_s[wave][buf][1], qreg, oacc, m_run, l_run, c, h, t0, end, cs, vlane);
+    t0 = tn;
+  }
+
+  const float l_tot = l_run + __shfl_xor(l_run, 32, kWave);
+  __syncthreads();  // every wave is done with the tile buffers the merge rows reuse
+  if (c < G) {
+#pragma unroll
+    for (int t = 0; t < D / 32; ++t)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) sm[wave][c][32 * t + 8 * (j / 4) + 4 * h + j % 4] = oacc[t][j];
+    if (h == 0) {
+      sm[wave][c][D] = m_run;
+      sm[wave][c][D + 1] = l_tot;
+    }
+  }
+  __syncthreads();
+  for (int t = threadIdx.x; t < G * D; t += W * kWave) {
+    const int g = t / D, d = t % D;
+    float top = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < W; ++w) top = fmaxf(top, sm[w][g][D]);
+    float den = 0.f, num = 0.f;
+    if (top != -INFINITY) {
+#pragma unroll
+      for (int w = 0; w < W; ++w) {
+        const float mw = sm[w][g][D];
+        const float f = mw == -INFINITY ? 0.f : exp2f(mw - top);
+        den = fmaf(f, sm[w][g][D + 1], den);
+        num = fmaf(f, sm[w][g][d], num);
+      }
+    }
+    const long qrow = long(b) * q_heads + hk * G + g;
+    if (splits == 1) {
+      store_out<TO>(out, qrow * D + d, q_heads * D, den > 0.f ? num / den : 0.f);
+    } else {
+      const long prow = qrow * splits + split;
+      pout[prow * D + d] = num;
+      if (d == 0) {
+        pmax[prow] = top;
+        psum[prow] = den;
+      }
+    }
+  }
+}
+
 struct DecodeCall {
   const void *q, *k, *v;
   const int32_t* lengths;
@@ -414,8 +632,33 @@ template <typename T, int D, int G> constexpr int waves_for() {
   return (G == 1 && D <= 64) ? 16 : ((G <= 2 && D <= 128) ? 8 : 4);
 }
 
+// The MFMA kernel takes grouped 16-bit caches with 16-bit queries (G >= 4, D
+// of 64 or 128) when q/k/v are 16-byte aligned and a head's cache fits 32-bit
+// buffer offsets; everything else runs decode_attn_kernel.
+template <typename T, typename TQ, typename TO, int D, int G>
+constexpr bool gqa_mfma_shape() {
+  return G >= 4 && (D == 64 || D == 128) && std::is_same<T, TQ>::value &&
+         (std::is_same<T, bf16_t>::value || std::is_same<T, f16_t>::value) && !std::is_same<TO, resid_t>::value;
+}
+
+inline bool gqa_mfma_fits(const DecodeCall& c) {
+  const auto a16 = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+  return a16(c.q) && a16(c.k) && a16(c.v) && long(c.cap) * c.dim * 2 < (1L << 31);
+}
+
 template <typename T, typename TQ, typename TO, int D, int G>
 int launch_attn(const DecodeCall& c) {
+  if constexpr (gqa_mfma_shape<T, TQ, TO, D, G>()) {
+    if (gqa_mfma_fits(c)) {
+      const int chunk = (c.cap + c.splits - 1) / c.splits;
+      const long groups = long(c.batch) * c.kv_heads * c.splits;
+      hipLaunchKernelGGL((decode_gqa32_kernel<T, TO, D, G>), dim3(unsigned(groups)), dim3(kGqaWaves * kWave), 0,
+                         c.stream, static_cast<const T*>(c.q), static_cast<const T*>(c.k),
+                         static_cast<const T*>(c.v), c.lengths, c.pmax, c.psum, c.pout, c.out, c.kv_heads,
+                         c.cap, c.splits, chunk, c.scale * kLog2e);
+      return check_launch("decode_attention");
+    }
+  }
   constexpr int W = waves_for<T, D, G>();
   const int chunk = (c.cap + c.splits - 1) / c.splits;
   const long groups = long(c.batch) * c.kv_heads * c.splits;

@@ -61,23 +61,38 @@ def _validate(q, k, v, lengths, splits):
     return batch, query_heads, dim
 
 
-def auto_splits(batch: int, kv_heads: int, capacity: int, groups: int = 1) -> int:
+def auto_splits(batch: int, kv_heads: int, capacity: int, groups: int = 1, matrix_cores: bool = False) -> int:
     """Split count for ``batch`` x ``kv_heads`` caches of ``capacity`` keys, ``groups``
     query heads per KV head.
 
-    One workgroup (up to 16 waves) owns one (batch, kv head, split) chunk and
-    merges its waves through LDS; with a single split it writes the output
-    directly and no merge kernel runs. Without grouping a few hundred
-    workgroups of >= 1024 keys cover the 256 CUs. A grouped workgroup does
-    ``groups`` dot products per key, so it is given fewer keys and more
-    workgroups: about 512 of >= 512 / groups keys (measured on MI355X over the
-    reference's GQA shapes, e.g. B=1, Hq=32, Hkv=4, N=4096, D=128: 124 us at
-    the ungrouped choice of 4 splits, 24 us at 64).
+    One workgroup owns one (batch, kv head, split) chunk and merges its waves
+    through LDS; with a single split it writes the output directly and no
+    merge kernel runs. Without grouping a few hundred workgroups (up to 16
+    waves each) of >= 1024 keys cover the 256 CUs. A grouped workgroup on the
+    VALU kernel does ``groups`` dot products per key, so it is given fewer keys
+    and more workgroups: about 512 of >= 512 / groups keys. ``matrix_cores``
+    (groups >= 4, head dim 64 or 128, 16-bit q and cache) selects the MFMA
+    kernel's choice: about 256 workgroups of 4 waves (one or two per CU by
+    LDS) of >= 128 keys, one 32-key tile per wave. Measured on MI355X over the
+    reference's GQA shapes, e.g. B=1, Hq=32, Hkv=4, D=128: N=4096 11.1 us at
+    32 splits (13.8 at 64), N=65536 32.1 us at 64 (40.3 at 128); B=8, N=16384
+    46.4 us at 8 (48.7 at 16).
     """
-    target = 256 if groups == 1 else 512
-    min_keys = 1024 if groups == 1 else max(64, 512 // groups)
+    if matrix_cores:
+        target, min_keys = 256, 128
+    elif groups == 1:
+        target, min_keys = 256, 1024
+    else:
+        target, min_keys = 512, max(64, 512 // groups)
     splits = math.ceil(target / (batch * kv_heads))
     return max(1, min(MAX_SPLITS, splits, math.ceil(capacity / min_keys)))
+
+
+def uses_matrix_cores(q: torch.Tensor, k: torch.Tensor) -> bool:
+    """Whether ``sfl_decode_attention`` runs these shapes on its MFMA kernel."""
+    groups = q.shape[1] // k.shape[1]
+    return (groups >= 4 and q.shape[-1] in (64, 128) and q.dtype == k.dtype
+            and k.dtype in (torch.bfloat16, torch.float16))
 
 
 @dataclass
@@ -121,7 +136,7 @@ def prepare(q, k, v, lengths=None, *, splits=None, scale=None, variant="token") 
         raise ValueError("scale must be finite and positive")
     _lib.lib()  # fail here, before allocation, if the library is not built
     if splits is None:
-        splits = auto_splits(batch, k.shape[1], k.shape[2], heads // k.shape[1])
+        splits = auto_splits(batch, k.shape[1], k.shape[2], heads // k.shape[1], uses_matrix_cores(q, k))
     maximum = torch.empty((batch, heads, splits), device=q.device, dtype=torch.float32)
     normalizer = torch.empty_like(maximum)
     numerator = torch.empty((batch, heads, splits, dim), device=q.device, dtype=torch.float32)

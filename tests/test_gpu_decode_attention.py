@@ -104,6 +104,73 @@ def test_config4_shape_sampled_rows():
         check(out[sl], q[sl].cpu(), k[sl].cpu(), v[sl].cpu(), lengths[sl].cpu(), torch.bfloat16)
 
 
+
+@pytest.mark.parametrize("groups", [1, 4, 8])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_stale_cache_rows_past_the_length_are_ignored(groups, dtype):
+    """Cache rows at positions >= length were never written: NaN keys and inf values there must not leak."""
+    from systems_for_llms_amd.decode import prepare
+
+    q, k, v, lengths = make_inputs(4, 8, groups, 200, 128, dtype, 4242)
+    k_stale, v_stale = k.clone(), v.clone()
+    for b, n in enumerate(lengths.tolist()):
+        k_stale[b, :, n:] = float("nan")
+        v_stale[b, :, n:] = float("inf")
+    gpu = to_gpu(q, k_stale, v_stale, lengths)
+    for splits in (1, 3, None):
+        check(prepare(*gpu, splits=splits)(), q, k, v, lengths, dtype)
+
+
+@pytest.mark.parametrize("dim", [64, 128])
+def test_grouped_long_ragged_caches(dim):
+    """Grouped heads over caches of many 32-key tiles per wave, lengths off every tile boundary."""
+    from systems_for_llms_amd.decode import prepare
+
+    g = torch.Generator().manual_seed(dim)
+    q = torch.randn((4, 32, dim), generator=g).bfloat16()
+    k = torch.randn((4, 4, 3001, dim), generator=g).bfloat16()
+    v = torch.randn((4, 4, 3001, dim), generator=g).bfloat16()
+    lengths = torch.tensor([3001, 1499, 97, 2048], dtype=torch.int32)
+    gpu = to_gpu(q, k, v, lengths)
+    for splits in (1, 5, 128, None):
+        check(prepare(*gpu, splits=splits)(), q, k, v, lengths, torch.bfloat16)
+
+
+@pytest.mark.parametrize("groups", [4, 8])
+def test_grouped_outputs_in_every_output_dtype(groups):
+    """bf16 q/k/v through the C ABI into bf16, fp32 and the split-bf16 activation layout, one and several splits."""
+    from systems_for_llms_amd import _lib
+
+    batch, heads, dim, cap = 3, 16, 64, 300
+    g = torch.Generator().manual_seed(groups)
+    q = torch.randn(batch, heads, dim, generator=g).bfloat16()
+    k = torch.randn(batch, heads // groups, cap, dim, generator=g).bfloat16()
+    v = torch.randn(batch, heads // groups, cap, dim, generator=g).bfloat16()
+    lengths = torch.tensor([300, 0, 129], dtype=torch.int32)
+    expected = decode_reference(q, k, v, lengths)
+    qd, kd, vd, ld = to_gpu(q, k, v, lengths)
+    k_dim = heads * dim
+    for splits in (1, 4):
+        pmax = torch.empty(batch * heads * splits, device="cuda")
+        psum = torch.empty_like(pmax)
+        pout = torch.empty(batch * heads * splits * dim, device="cuda")
+        outs = {_lib.DTYPE_CODES[torch.bfloat16]: torch.empty(batch, k_dim, device="cuda", dtype=torch.bfloat16),
+                _lib.DTYPE_CODES[torch.float32]: torch.empty(batch, k_dim, device="cuda"),
+                _lib.DTYPE_BF16X2: torch.zeros(16 * k_dim, device="cuda")}
+        for code, out in outs.items():
+            _lib.call("sfl_decode_attention", qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), ld.data_ptr(),
+                      pmax.data_ptr(), psum.data_ptr(), pout.data_ptr(), out.data_ptr(), batch, heads,
+                      heads // groups, cap, dim, splits, dim ** -0.5, 1, 1, code, _lib.stream_handle())
+        torch.cuda.synchronize()
+        flat = expected.reshape(batch, k_dim)
+        torch.testing.assert_close(outs[1].float().cpu(), flat, atol=0.02, rtol=0.02)
+        torch.testing.assert_close(outs[0].cpu(), flat, atol=0.01, rtol=0.01)
+        # Split-bf16 layout: [k_dim / 32 chunks][hi, lo][4 groups][16 rows][8 values] per 16-row block.
+        halves = outs[_lib.DTYPE_BF16X2].cpu().view(torch.bfloat16).view(k_dim // 32, 2, 4, 16, 8).float()
+        laid = (halves[:, 0] + halves[:, 1]).permute(2, 0, 1, 3).reshape(16, k_dim)[:batch]
+        assert ((laid - outs[0].cpu()).abs() <= outs[0].cpu().abs() * 2.0 ** -14).all()
+
+
 def test_rejections_before_launch():
     from systems_for_llms_amd.decode import prepare
 
