@@ -264,6 +264,33 @@ def profile_target_attention(reps: int = 24) -> int:
     return 0
 
 
+
+def profile_target_gqa(reps: int = 40) -> int:
+    """Kernel-trace target for grouped-query decode attention on the matrix cores.
+
+    The reference's published shape B=8, Hq=32, Hkv=4, N=16384, D=128 (bf16,
+    full-capacity caches, the automatic split count): ``reps`` operator calls
+    (attention kernel + merge), event-timed as one region, so the rocprof
+    per-kernel averages can be checked against the per-call time printed here.
+    """
+    import torch
+
+    from systems_for_llms_amd.decode import prepare
+
+    b, hq, hkv, n, d = 8, 32, 4, 16384, 128
+    g = torch.Generator(device="cuda").manual_seed(11)
+    q = torch.randn((b, hq, d), device="cuda", generator=g, dtype=torch.bfloat16)
+    k = torch.randn((b, hkv, n, d), device="cuda", generator=g, dtype=torch.bfloat16)
+    v = torch.randn_like(k)
+    op = prepare(q, k, v)
+    op()
+    torch.cuda.synchronize()
+    us = time_events(op, reps) * 1000
+    kv = 2 * b * hkv * n * d * 2
+    log(f"profile target: {reps} decode_attention calls B={b} Hq={hq} Hkv={hkv} N={n} D={d} splits={op.splits}: "
+        f"{us:.1f} us per call (events, eager), K+V {kv} bytes = {kv / us / 1e3:.0f} GB/s")
+    return 0
+
 def main() -> int:
     parser = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     parser.add_argument("--gpus", type=int, default=1)
@@ -273,11 +300,13 @@ def main() -> int:
     parser.add_argument("--no-reference-shapes", action="store_true",
                         help="skip timing the reference's published attention shapes")
     parser.add_argument("--attention-reps", type=int, default=50)
-    parser.add_argument("--profile-target", choices=["attention"], default=None,
-                        help="run only the counter-collection target (see profile_target_attention)")
+    parser.add_argument("--profile-target", choices=["attention", "gqa"], default=None,
+                        help="run only a profiling target (profile_target_attention, profile_target_gqa)")
     args = parser.parse_args()
     if args.profile_target == "attention":
         return profile_target_attention()
+    if args.profile_target == "gqa":
+        return profile_target_gqa()
     if args.gpus != 1:
         print("bench.py measures one GPU: every box in this build has a single MI355X and the decode "
               "path is not sharded across GPUs (see DESIGN.md for how it would shard)", file=sys.stderr)
