@@ -71,7 +71,11 @@ const char* sfl_last_error(void);
  * work. D in {16, 32, 64, 128}; Hq/Hkv in {1, 2, 4, 8}; splits in [1, 1024].
  * kv_dtype: element type of k and v (F32, BF16 or F16); q_dtype: kv_dtype or
  * F32; out_dtype: kv_dtype, F32, BF16X2 or F32X (the last two: the GEMV
- * activation layout of [B, Hq*D]). Softmax state is fp32.
+ * activation layout of [B, Hq*D]). Softmax state is fp32. Cache rows at
+ * positions >= lengths[b] are never read into the result (they may hold
+ * anything, NaN included). Hq/Hkv >= 4 with D 64 or 128, q_dtype ==
+ * kv_dtype in {BF16, F16}, 16-byte aligned q/k/v and cap*D*2 < 2^31 run
+ * on the MFMA kernel; all other cases on the VALU kernel.
  */
 int sfl_decode_attention(const void* q, const void* k, const void* v, const int32_t* lengths,
                          float* partial_max, float* partial_sum, float* partial_out, void* out,
