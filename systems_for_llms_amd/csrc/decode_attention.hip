@@ -64,10 +64,10 @@ __device__ __forceinline__ uint4 load_proj_unit(const unsigned char* w_lane, int
   return load16(w_lane + (tile * nchunks_all + c) * kWave * 16);
 }
 
-// One workgroup of W waves per (batch, kv head, split). The split's keys are
-// divided among the waves; each wave streams its range with the per-slot
-// online softmax, the slots are merged with shuffles, and the W wave states
-// are merged through LDS. With one split the workgroup writes the final
+// One workgroup of W waves per (batch, kv head, split). The split's key
+// tiles are dealt round-robin to the waves; each wave streams its tiles with
+// the per-slot online softmax, the slots are merged with shuffles, and the W
+// wave states are merged through LDS. With one split the workgroup writes the final
 // output (or, fused, adds its heads' share of the output projection to x);
 // otherwise it writes its (max, sum, numerator) partial for the merge kernel.
 template <typename T, typename TQ, typename TO, int D, int G, int W>
@@ -103,9 +103,6 @@ __global__ __launch_bounds__(W * kWave) void decode_attn_kernel(
   const int begin = split * chunk;
   if (splits > 1 && begin >= len) return;  // the merge reads only chunks below the length
   const int end = min(len, begin + chunk);
-  const int sub = (max(0, end - begin) + W - 1) / W;
-  const int wbegin = begin + wave * sub;
-  const int wend = min(end, wbegin + sub);
 
 #pragma unroll
   for (int g = 0; g < G; ++g) {
@@ -125,10 +122,13 @@ __global__ __launch_bounds__(W * kWave) void decode_attn_kernel(
   const T* kb = k + row0 * D + dg * EPL;
   const T* vb = v + row0 * D + dg * EPL;
 
-  // Rows past the wave's range are clamped to its last row: the masked lanes
-  // of a partial tile re-read a cached row instead of fetching new HBM lines.
-  const int last = wend - 1;
-  for (int t0 = wbegin; t0 < wend; t0 += TILE) {
+  // Wave w takes tiles w, w + W, w + 2W, ... of the split, so the workgroup's
+  // loads at any time cover one contiguous run of W tiles per operand (two
+  // DRAM streams per workgroup instead of two per wave). Rows past the split
+  // are clamped to its last row: the masked lanes of the final partial tile
+  // re-read a cached row instead of fetching new HBM lines.
+  const int last = end - 1;
+  for (int t0 = begin + wave * TILE; t0 < end; t0 += W * TILE) {
     uint4 kr[NL], vr[NL];
 #pragma unroll
     for (int i = 0; i < NL; ++i) {
@@ -145,7 +145,7 @@ __global__ __launch_bounds__(W * kWave) void decode_attn_kernel(
     for (int i = 0; i < NL; ++i) {
       float kf[EPL];
       unpack16<T>(kr[i], kf);
-      const bool valid = t0 + i * TPL + slot < wend;
+      const bool valid = t0 + i * TPL + slot < end;
 #pragma unroll
       for (int g = 0; g < G; ++g) {
         float d = 0.f;
