@@ -99,10 +99,36 @@ __global__ __launch_bounds__(W * kWave) void decode_attn_kernel(
 #pragma unroll
     for (int e = 0; e < EPL; ++e) qv[g][e] = load_scalar<TQ>(qp + e);
   }
-  const int len = min(max(lengths[b], 0), cap);
+  const long row0 = (long(b) * kv_heads + h) * cap;
+  const T* kb = k + row0 * D + dg * EPL;
+  const T* vb = v + row0 * D + dg * EPL;
   const int begin = split * chunk;
+  const int t_first = begin + wave * TILE;
+
+  // With one split (the model's path) the first tile's loads are issued
+  // before the length is known, rows clamped to the capacity, so their round
+  // trip overlaps the q and length loads; rows at or past the length are
+  // zeroed once it is known (they may hold stale values, NaN included).
+  const bool spec = splits == 1;
+  uint4 kr[NL], vr[NL];
+  if (spec) {
+#pragma unroll
+    for (int i = 0; i < NL; ++i) kr[i] = load16_stream(kb + long(min(t_first + i * TPL + slot, cap - 1)) * D);
+#pragma unroll
+    for (int i = 0; i < NL; ++i) vr[i] = load16_stream(vb + long(min(t_first + i * TPL + slot, cap - 1)) * D);
+  }
+  const int len = min(max(lengths[b], 0), cap);
   if (splits > 1 && begin >= len) return;  // the merge reads only chunks below the length
   const int end = min(len, begin + chunk);
+  if (spec) {
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+      if (t_first + i * TPL + slot >= end) {
+        kr[i] = make_uint4(0u, 0u, 0u, 0u);
+        vr[i] = make_uint4(0u, 0u, 0u, 0u);
+      }
+    }
+  }
 
 #pragma unroll
   for (int g = 0; g < G; ++g) {
@@ -118,28 +144,14 @@ __global__ __launch_bounds__(W * kWave) void decode_attn_kernel(
     for (int e = 0; e < EPL; ++e) acc[g][e] = 0.f;
   }
 
-  const long row0 = (long(b) * kv_heads + h) * cap;
-  const T* kb = k + row0 * D + dg * EPL;
-  const T* vb = v + row0 * D + dg * EPL;
-
   // Wave w takes tiles w, w + W, w + 2W, ... of the split, so the workgroup's
   // loads at any time cover one contiguous run of W tiles per operand (two
   // DRAM streams per workgroup instead of two per wave). Rows past the split
   // are clamped to its last row: the masked lanes of the final partial tile
   // re-read a cached row instead of fetching new HBM lines.
   const int last = end - 1;
-  for (int t0 = begin + wave * TILE; t0 < end; t0 += W * TILE) {
-    uint4 kr[NL], vr[NL];
-#pragma unroll
-    for (int i = 0; i < NL; ++i) {
-      const int tc = min(t0 + i * TPL + slot, last);
-      kr[i] = load16_stream(kb + long(tc) * D);
-    }
-#pragma unroll
-    for (int i = 0; i < NL; ++i) {
-      const int tc = min(t0 + i * TPL + slot, last);
-      vr[i] = load16_stream(vb + long(tc) * D);
-    }
+  // One tile of the wave: scores, per-slot online softmax, V accumulation.
+  auto tile = [&](int t0, const uint4 (&kr)[NL], const uint4 (&vr)[NL]) {
     float sc[G][NL];
 #pragma unroll
     for (int i = 0; i < NL; ++i) {
@@ -185,6 +197,19 @@ __global__ __launch_bounds__(W * kWave) void decode_attn_kernel(
         for (int e = 0; e < EPL; ++e) acc[g][e] = fmaf(p[g][i], vf[e], acc[g][e]);
       }
     }
+  };
+  int t_loop = t_first;
+  if (spec) {
+    if (t_first < end) tile(t_first, kr, vr);
+    t_loop = t_first + W * TILE;
+  }
+  for (int t0 = t_loop; t0 < end; t0 += W * TILE) {
+    uint4 kn[NL], vn[NL];
+#pragma unroll
+    for (int i = 0; i < NL; ++i) kn[i] = load16_stream(kb + long(min(t0 + i * TPL + slot, last)) * D);
+#pragma unroll
+    for (int i = 0; i < NL; ++i) vn[i] = load16_stream(vb + long(min(t0 + i * TPL + slot, last)) * D);
+    tile(t0, kn, vn);
   }
 
   // Fused projection: issue the first round of W_o loads now, so they land
