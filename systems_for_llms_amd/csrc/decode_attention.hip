@@ -343,8 +343,9 @@ __device__ __forceinline__ void store_out<f32x_t>(void* out, long f, int K, floa
 }
 
 // One wave per (batch, query head): combine the chunks below the row's length.
-// Every load of a round of up to 64 chunks (their max, sum and numerators) is
-// issued before any is used, so a merge of <= 64 chunks costs one round trip.
+// Every load of a round of up to kRound = 16 chunks (their max, sum and
+// numerators) is issued before any is used, so a merge of <= 16 chunks costs
+// one round trip.
 // Lane s holds chunk s's max and sum; the numerators are weighted by shuffles.
 template <typename TO, int D>
 __global__ __launch_bounds__(256) void decode_merge_kernel(
