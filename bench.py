@@ -5,15 +5,18 @@ Workload: d_model 1024, 24 layers, 16 heads of 64, SwiGLU d_ff 2752, vocab
 prompt tokens (seed 2027) are prefilled, then greedy decode runs to context
 4096. The prompt is prefilled in one pass (MFMA GEMMs + masked attention),
 which also picks token 3072. One step = one decode position for all 16
-sequences (16 tokens), replayed from a captured HIP graph. W warmup steps run
-first and the state is rewound to the first decode position, so the K timed
-steps always cover positions 3072 .. 3072+K-1 (attention lengths 3073 ..
-3072+K); the default K = 1023 generates tokens 3073 .. 4095.
+sequences (16 tokens), replayed from a captured HIP graph. The K timed steps
+are centred on the decode's mean attention length (3584: lengths run 3073 ..
+4095 over the 1023 steps from position 3072 to context 4096), so a short run
+measures the same per-step cost as the whole range: they start at position
+3584 - (K+1)//2 (3072 for the default K = 1023, the full range). Untimed
+decode steps first fill the cache and tokens up to that position (at least W
+of them; the state is rewound when W runs past it).
 
 Printed JSON (one line): decode tok/s; ``roofline`` for the dominant kernel,
 decode attention fused with the output projection (the model path's kernel),
-timed with HIP events on its launch stream at the mean decode context of the
-timed region, rotating over the 24 layers' caches so that every call streams
+timed with HIP events on its launch stream at the decode's mean attention
+length 3584, rotating over the 24 layers' caches so that every call streams
 from HBM as it does inside the decode loop; ``decode_attention_operator``: the
 same measurement for the standalone split-KV attention operator; ``prefill``
 (the prompt pass, MFMA TFLOP/s against the bf16 dense peak);
@@ -43,6 +46,7 @@ HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 PROMPT = 3072
 CONTEXT = 4096
+MEAN_LEN = (PROMPT + 1 + CONTEXT - 1) // 2  # mean attention length of the decode, 3584
 BATCH = 16
 WEIGHT_SEED, PROMPT_SEED = 1337, 2027
 
@@ -154,7 +158,7 @@ def published_shapes():
         q = torch.randn((b, hq, d), device="cuda", generator=g, dtype=torch.bfloat16)
         k = torch.randn((b, hkv, n, d), device="cuda", generator=g, dtype=torch.bfloat16)
         v = torch.randn_like(k)
-        op = prepare(q, k, v)
+        op = prepare(q, k, v, splits=None)  # the split count chosen from the shape
         us = time_graph(op) * 1000
         kv_bytes = 2 * b * hkv * n * d * 2
         decode_rows.append({"shape": f"B={b} Hq={hq} Hkv={hkv} N={n} D={d}", "us": round(us, 1),
@@ -188,10 +192,10 @@ def cpu_baseline(cfg, seconds=12.0, max_steps=32):
     threads = os.cpu_count() or 1
     torch.set_num_threads(threads)
     sd = seeded_state_dict(cfg, WEIGHT_SEED)
-    cache = KVCacheOracle(sd, cfg, BATCH, PROMPT + max_steps + 1)
+    cache = KVCacheOracle(sd, cfg, BATCH, MEAN_LEN + max_steps + 1)
     cache.k.fill_(0.01)  # touch every page: the step streams the whole cache
     cache.v.fill_(0.01)
-    cache.length = PROMPT - 1
+    cache.length = MEAN_LEN - 1  # the decode's mean attention length, as the GPU figures
     tokens = torch.randint(0, cfg.vocab_size, (BATCH, 1), generator=torch.Generator().manual_seed(5))
     cache.step(tokens)  # first call pays one-time allocations
     started = time.perf_counter()
@@ -203,7 +207,7 @@ def cpu_baseline(cfg, seconds=12.0, max_steps=32):
     return {"value": round(BATCH * steps / elapsed, 2), "unit": "tok/s", "cores": torch.get_num_threads(),
             "kind": "port",
             "sample": f"{steps} KV-cached fp32 decode steps of the CPU oracle (oracle/model.py KVCacheOracle), "
-                      f"324M, batch {BATCH}, attention length {PROMPT}..{PROMPT + steps}; os.cpu_count()={threads}"}
+                      f"324M, batch {BATCH}, attention length {MEAN_LEN}..{MEAN_LEN + steps}; os.cpu_count()={threads}"}
 
 
 def cpu_reference_semantics(cfg, length=PROMPT):
@@ -282,7 +286,7 @@ def profile_target_gqa(reps: int = 40) -> int:
     q = torch.randn((b, hq, d), device="cuda", generator=g, dtype=torch.bfloat16)
     k = torch.randn((b, hkv, n, d), device="cuda", generator=g, dtype=torch.bfloat16)
     v = torch.randn_like(k)
-    op = prepare(q, k, v)
+    op = prepare(q, k, v, splits=None)
     op()
     torch.cuda.synchronize()
     us = time_events(op, reps) * 1000
@@ -341,27 +345,31 @@ def main() -> int:
     log(f"prefill of {BATCH}x{PROMPT} tokens in {prefill_s * 1000:.1f} ms "
         f"({BATCH * PROMPT / prefill_s:.0f} tok/s, MFMA GEMMs + masked attention)")
     first = PROMPT  # prefill chose token PROMPT; decode steps run at positions PROMPT ..
-    assert int(session.pos[0]) == first
+    assert int(session.pos[0]) == first and session.position == first
     session.step()  # eager warm-up of every decode kernel before capture
     session.capture(1)
-
-    for _ in range(args.warmup):
-        session.graph.replay()
+    # Timed steps centred on the mean attention length; untimed real decode
+    # steps fill the cache and tokens up to the first timed position.
+    start = max(first, min(CONTEXT - 1 - args.steps, MEAN_LEN - (args.steps + 1) // 2))
+    warm = min(max(args.warmup, start - session.position), CONTEXT - 1 - session.position)
+    for _ in range(warm):
+        session.replay()
     torch.cuda.synchronize()
-    session.set_position(first)
+    session.set_position(start)
     torch.cuda.synchronize()
-    ms = time_events(session.graph.replay, args.steps)
+    ms = time_events(session.replay, args.steps)
     ms_per_step = ms
     tokens_per_s = BATCH * 1000.0 / ms_per_step
-    generated = session.tokens[:, PROMPT:PROMPT + args.steps + 1]
-    assert int(session.pos[0]) == first + args.steps
+    mean_len = start + (args.steps + 1) / 2  # attention lengths start+1 .. start+K
+    generated = session.tokens[:, PROMPT:start + args.steps + 1]
+    assert int(session.pos[0]) == start + args.steps
     assert bool((generated >= 0).all()) and bool((generated < cfg.vocab_size).all())
-    log(f"decode {args.steps} steps: {ms_per_step:.3f} ms/step, {tokens_per_s:.0f} tok/s")
+    log(f"decode {args.steps} steps at positions {start}..{start + args.steps - 1} (mean attention length "
+        f"{mean_len}): {ms_per_step:.3f} ms/step, {tokens_per_s:.0f} tok/s")
 
-    # Dominant kernel: decode attention fused with output_proj, at the timed
-    # region's mean attention length.
-    mean_len = first + 1 + (args.steps - 1) / 2
-    length = int(round(mean_len))
+    # Dominant kernel: decode attention fused with output_proj, at the decode's
+    # mean attention length.
+    length = MEAN_LEN
     lengths = torch.full((BATCH,), length, device="cuda", dtype=torch.int32)
     q = torch.randn((BATCH, cfg.num_heads, cfg.head_dim), device="cuda", dtype=torch.float32)
     x_scratch = torch.zeros((BATCH, cfg.d_model), device="cuda", dtype=torch.float32)
@@ -408,7 +416,7 @@ def main() -> int:
     kc = torch.randn((64, 16, 16384, 64), device="cuda", generator=g, dtype=torch.bfloat16)
     vc = torch.randn((64, 16, 16384, 64), device="cuda", generator=g, dtype=torch.bfloat16)
     lc = torch.randint(1024, 16385, (64,), generator=torch.Generator().manual_seed(4), dtype=torch.int32)
-    op = prepare(qc, kc, vc, lc.cuda())
+    op = prepare(qc, kc, vc, lc.cuda(), splits=None)
     for _ in range(3):
         op()
     c4_ms = time_events(op, 20)
@@ -443,8 +451,10 @@ def main() -> int:
     # shape (FETCH_SIZE + WRITE_SIZE, calibrated on a copy of known size).
     traffic = None
     pmc = ROOT / "profiles" / "decode_attention_out_proj_324m_b16_len3584_pmc.json"
-    if pmc.exists() and length == 3584:
-        traffic = json.loads(pmc.read_text())["traffic_bytes"]
+    if pmc.exists():
+        record = json.loads(pmc.read_text())
+        assert record["length"] == length, "the PMC record is for another attention length"
+        traffic = record["traffic_bytes"]
 
     e2e_bytes = step_bytes(cfg, BATCH, mean_len)
     e2e_gbs = e2e_bytes / (ms_per_step * 1e-3) / 1e9
@@ -473,7 +483,9 @@ def main() -> int:
                                "greedy decode to ctx 4096",
                    "d_model": cfg.d_model, "num_layers": cfg.num_layers, "num_heads": cfg.num_heads,
                    "d_ff": cfg.d_ff, "vocab_size": cfg.vocab_size, "global_batch": BATCH,
-                   "prompt": PROMPT, "context": CONTEXT, "parallelism": "single GPU"},
+                   "prompt": PROMPT, "context": CONTEXT, "parallelism": "single GPU",
+                   "timed_positions": [start, start + args.steps - 1],
+                   "mean_attention_length": mean_len},
         "roofline": {"bound": "hbm",
                      "kernel": "decode_attn_kernel<resid_t> (decode attention + output_proj + residual, one launch)",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -481,7 +493,7 @@ def main() -> int:
                      "traffic_source": f"profiles/{pmc.name}" if traffic else None,
                      "bytes_per_launch": attn_bytes, "us_per_launch": round(attn_ms * 1000, 2),
                      "shape": f"B={BATCH} H={cfg.num_heads} D={cfg.head_dim} d_model={cfg.d_model} "
-                              f"length={length} (mean of timed region)"},
+                              f"length={length} (mean attention length of the decode to 4096)"},
         "decode_attention_operator": {"us": round(op_ms * 1000, 2), "achieved_gbs": round(op_gbs, 1),
                                       "frac": round(op_gbs / HBM_PEAK_GBS, 4), "bytes": op_bytes,
                                       "shape": f"sfl_decode_attention, same shape and caches, BF16X2 output"},

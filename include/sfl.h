@@ -243,6 +243,27 @@ int sfl_masked_attention(const void* q, const void* k, const void* v, void* o, f
 /* Query/key tile size of sfl_masked_attention (64). */
 int sfl_masked_attention_block(void);
 
+/* Compiler resource data of a kernel (hipFuncGetAttributes), not a profiler measurement. */
+typedef struct {
+  char name[96];             /* kernel and element type */
+  int registers;             /* VGPRs per lane */
+  int private_bytes;         /* scratch per lane: register spills (0 = none) */
+  int shared_bytes;          /* static LDS per workgroup */
+  int max_threads;           /* largest workgroup the code object allows */
+  int threads;               /* workgroup size of the launch */
+  int queries_per_workgroup; /* query rows one workgroup covers */
+} sfl_kernel_info;
+
+/*
+ * The kernel sfl_masked_attention launches for this head dim, dtype, sequence
+ * length and K/V row strides (elements), with its resource data. Replaces the
+ * Triton CompiledKernel metadata the reference records when its caller passes
+ * `launch_metadata` (attention_lab/triton_attention.py:39-57,
+ * launch_metadata at :326-328). Needs a HIP device; launches nothing.
+ */
+int sfl_masked_attention_kernel_info(int head_dim, int dtype, int n, long k_row_stride,
+                                     long v_row_stride, sfl_kernel_info* info);
+
 /* ---- prefill (bf16 weights) -------------------------------------------------
  * C^T = W A^T on bf16 MFMAs; A [M, K] bf16 row-major (one row per token),
  * W [N, K] bf16; K % 8 == 0. K % 64 == 0 runs 32x32x16 MFMA tiles of 256 x 256

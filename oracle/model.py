@@ -72,31 +72,41 @@ def _merge_heads(x):
     return x.transpose(-3, -2).reshape(*lead, t, h * dk)
 
 
-def _layer(sd, prefix, x, heads, cos, sin, positions, mask, kv_dtype=None):
-    h = rmsnorm(x, sd[prefix + "attn_norm.weight"])
+def _round(t: torch.Tensor, dtype) -> torch.Tensor:
+    """``t`` rounded through a narrower storage format (no-op for ``None``)."""
+    return t if dtype is None else t.to(dtype).to(t.dtype)
+
+
+def _layer(sd, prefix, x, heads, cos, sin, positions, mask, kv_dtype=None, act_dtype=None):
+    h = _round(rmsnorm(x, sd[prefix + "attn_norm.weight"]), act_dtype)
     q = _split_heads(_linear(h, sd[prefix + "attn.q_proj.weight"]), heads)
     k = _split_heads(_linear(h, sd[prefix + "attn.k_proj.weight"]), heads)
     v = _split_heads(_linear(h, sd[prefix + "attn.v_proj.weight"]), heads)
-    q = rope(q, cos, sin, positions)
+    q = _round(rope(q, cos, sin, positions), act_dtype)
     k = rope(k, cos, sin, positions)
     if kv_dtype is not None:  # keys/values stored in a narrower cache format
         k = k.to(kv_dtype).to(x.dtype)
         v = v.to(kv_dtype).to(x.dtype)
-    a = _merge_heads(attention_core(q, k, v, mask))
+    a = _round(_merge_heads(attention_core(q, k, v, mask)), act_dtype)
     x = x + _linear(a, sd[prefix + "attn.output_proj.weight"])
-    h = rmsnorm(x, sd[prefix + "ffn_norm.weight"])
+    h = _round(rmsnorm(x, sd[prefix + "ffn_norm.weight"]), act_dtype)
     a = _linear(h, sd[prefix + "ffn.w1.weight"])
-    g = a * torch.sigmoid(a)
-    x = x + _linear(g * _linear(h, sd[prefix + "ffn.w3.weight"]), sd[prefix + "ffn.w2.weight"])
+    g = _round(a * torch.sigmoid(a) * _linear(h, sd[prefix + "ffn.w3.weight"]), act_dtype)
+    x = x + _linear(g, sd[prefix + "ffn.w2.weight"])
     return x
 
 
 @torch.no_grad()
-def forward(sd: dict, config, input_ids: torch.Tensor, dtype=torch.float32, kv_dtype=None) -> torch.Tensor:
+def forward(sd: dict, config, input_ids: torch.Tensor, dtype=torch.float32, kv_dtype=None,
+            act_dtype=None) -> torch.Tensor:
     """``TransformerLM.forward`` (``transformer.py:121-139``): logits ``[..., T, V]``.
 
-    ``kv_dtype`` (not in the reference) rounds keys and values through a cache
-    storage format, to bound what a narrower KV cache alone changes.
+    Not in the reference, for bounding what storage formats alone change:
+    ``kv_dtype`` rounds keys and values through a cache format; ``act_dtype``
+    rounds the GEMM inputs a batched prefill stores in a narrow format -- the
+    RMSNorm outputs (the final one included), q after RoPE, the merged
+    attention output and the SwiGLU hidden state (the residual stream stays in
+    ``dtype``).
     """
     if not 0 < input_ids.shape[-1] <= config.context_length:
         raise ValueError("sequence length must be between 1 and context_length")
@@ -107,8 +117,8 @@ def forward(sd: dict, config, input_ids: torch.Tensor, dtype=torch.float32, kv_d
     mask = torch.tril(torch.ones(t, t, dtype=torch.bool))
     x = sd["token_embeddings.weight"][input_ids]
     for layer in range(config.num_layers):
-        x = _layer(sd, f"layers.{layer}.", x, config.num_heads, cos, sin, positions, mask, kv_dtype)
-    x = rmsnorm(x, sd["ln_final.weight"])
+        x = _layer(sd, f"layers.{layer}.", x, config.num_heads, cos, sin, positions, mask, kv_dtype, act_dtype)
+    x = _round(rmsnorm(x, sd["ln_final.weight"]), act_dtype)
     return _linear(x, sd["lm_head.weight"])
 
 
@@ -126,33 +136,21 @@ def greedy_argmax(logits: torch.Tensor) -> torch.Tensor:
     return torch.argmax(logits, dim=-1)
 
 
-@torch.no_grad()
-def greedy_recompute(sd, config, prompt: torch.Tensor, steps: int, dtype=torch.float32):
-    """The reference's decode: recompute the whole forward for every new token.
-
-    Returns ``(ids [B, P+steps], margins [B, steps])`` where margins are the gap
-    between the largest and second-largest last-position logit of each step.
-    """
-    ids = prompt.clone()
-    margins = []
-    for _ in range(steps):
-        last = forward(sd, config, ids, dtype)[:, -1, :].float()
-        top = torch.topk(last, 2, dim=-1).values
-        margins.append(top[:, 0] - top[:, 1])
-        ids = torch.cat([ids, greedy_argmax(last)[:, None]], dim=1)
-    return ids, torch.stack(margins, dim=1)
-
-
 class KVCacheOracle:
-    """KV-cached restatement of the same forward, one position at a time.
+    """KV-cached restatement of the same forward, one chunk of positions at a time.
 
     Equal to ``forward`` up to float reassociation; used as the teacher-forced
-    checker for long decodes and as the CPU baseline.
+    checker for long decodes and as the CPU baseline. ``kv_dtype`` stores the
+    cache in a narrower format; ``step(..., act_dtype=...)`` rounds that
+    chunk's GEMM inputs as ``forward`` does, so a prompt chunk can model a
+    batched prefill and the following chunk a decode that keeps fp32 inputs.
     """
 
-    def __init__(self, sd, config, batch: int, capacity: int | None = None, dtype=torch.float32):
+    def __init__(self, sd, config, batch: int, capacity: int | None = None, dtype=torch.float32,
+                 kv_dtype=None):
         self.config = config
         self.dtype = dtype
+        self.kv_dtype = kv_dtype
         self.sd = {n: t.to(dtype) for n, t in sd.items()}
         self.heads = config.num_heads
         self.dk = config.d_model // config.num_heads
@@ -164,7 +162,7 @@ class KVCacheOracle:
         self.length = 0
 
     @torch.no_grad()
-    def step(self, tokens: torch.Tensor) -> torch.Tensor:
+    def step(self, tokens: torch.Tensor, act_dtype=None) -> torch.Tensor:
         """Append ``tokens [B, T]`` at the current length; return logits ``[B, T, V]``."""
         sd, cfg = self.sd, self.config
         t = tokens.shape[1]
@@ -175,19 +173,20 @@ class KVCacheOracle:
         x = sd["token_embeddings.weight"][tokens]
         for layer in range(cfg.num_layers):
             p = f"layers.{layer}."
-            h = rmsnorm(x, sd[p + "attn_norm.weight"])
+            h = _round(rmsnorm(x, sd[p + "attn_norm.weight"]), act_dtype)
             q = rope(_split_heads(_linear(h, sd[p + "attn.q_proj.weight"]), self.heads), self.cos, self.sin, positions)
             k = rope(_split_heads(_linear(h, sd[p + "attn.k_proj.weight"]), self.heads), self.cos, self.sin, positions)
             v = _split_heads(_linear(h, sd[p + "attn.v_proj.weight"]), self.heads)
-            self.k[layer, :, :, start:total] = k
-            self.v[layer, :, :, start:total] = v
-            a = attention_core(q, self.k[layer, :, :, :total], self.v[layer, :, :, :total], mask)
-            x = x + _linear(_merge_heads(a), sd[p + "attn.output_proj.weight"])
-            h = rmsnorm(x, sd[p + "ffn_norm.weight"])
+            self.k[layer, :, :, start:total] = _round(k, self.kv_dtype)
+            self.v[layer, :, :, start:total] = _round(v, self.kv_dtype)
+            a = attention_core(_round(q, act_dtype), self.k[layer, :, :, :total], self.v[layer, :, :, :total], mask)
+            x = x + _linear(_round(_merge_heads(a), act_dtype), sd[p + "attn.output_proj.weight"])
+            h = _round(rmsnorm(x, sd[p + "ffn_norm.weight"]), act_dtype)
             a1 = _linear(h, sd[p + "ffn.w1.weight"])
-            x = x + _linear(a1 * torch.sigmoid(a1) * _linear(h, sd[p + "ffn.w3.weight"]), sd[p + "ffn.w2.weight"])
+            g = _round(a1 * torch.sigmoid(a1) * _linear(h, sd[p + "ffn.w3.weight"]), act_dtype)
+            x = x + _linear(g, sd[p + "ffn.w2.weight"])
         self.length = total
-        return _linear(rmsnorm(x, sd["ln_final.weight"]), sd["lm_head.weight"])
+        return _linear(_round(rmsnorm(x, sd["ln_final.weight"]), act_dtype), sd["lm_head.weight"])
 
 
 @torch.no_grad()

@@ -37,6 +37,7 @@ SIGNATURES: dict[str, list] = {
                              POINTER(c_long), POINTER(c_long), c_float, c_int, c_int, c_int, c_int, P,
                              c_int, P, P, P, c_int, c_int, P],
     "sfl_masked_attention_block": [],
+    "sfl_masked_attention_kernel_info": [c_int, c_int, c_int, c_long, c_long, P],
     "sfl_gemm_bf16": [P, P, P, c_int, c_int, c_int, c_int, c_int, P],
     "sfl_gemm_qkv_rope": [P, P, c_int, c_int, c_int, c_int, P, P, P, P, P, c_int, P],
     "sfl_gemm_swiglu": [P, P, P, c_int, c_int, c_int, P],
@@ -45,6 +46,14 @@ SIGNATURES: dict[str, list] = {
 }
 
 _LIB = None
+
+
+class KernelInfo(ctypes.Structure):
+    """``sfl_kernel_info`` of ``include/sfl.h``."""
+
+    _fields_ = [("name", ctypes.c_char * 96), ("registers", c_int), ("private_bytes", c_int),
+                ("shared_bytes", c_int), ("max_threads", c_int), ("threads", c_int),
+                ("queries_per_workgroup", c_int)]
 
 
 class LibraryMissing(RuntimeError):
@@ -89,6 +98,28 @@ def pack_gemv(w: torch.Tensor) -> torch.Tensor:
     call("sfl_pack_gemv_weights", w.data_ptr(), packed.data_ptr(), n, k, dtype_code(w.dtype),
          stream_handle(w.device))
     return packed
+
+
+def masked_kernel_info(head_dim: int, dtype: torch.dtype, n: int, k_row_stride: int,
+                       v_row_stride: int) -> KernelInfo:
+    """Resource data of the kernel ``sfl_masked_attention`` launches for these shapes."""
+    info = KernelInfo()
+    call("sfl_masked_attention_kernel_info", head_dim, dtype_code(dtype), n, k_row_stride, v_row_stride,
+         ctypes.addressof(info))
+    return info
+
+
+_LIB_SHA256 = None
+
+
+def library_sha256() -> str:
+    """SHA-256 of the loaded ``libsfl.so`` (identifies the compiled kernels)."""
+    global _LIB_SHA256
+    if _LIB_SHA256 is None:
+        import hashlib
+
+        _LIB_SHA256 = hashlib.sha256(LIB_PATH.read_bytes()).hexdigest()
+    return _LIB_SHA256
 
 
 def ptr(t: torch.Tensor | None) -> int | None:

@@ -194,10 +194,26 @@ def attention(q, k, v, schedule, spec, document_ids=None, num_warps=4, num_stage
         -1 if spec.window_right is None else spec.window_right, spec.global_prefix or 0, docs_gpu,
         rows, cols, fulls, use_full_blocks)
     if launch_metadata is not None:
-        launch_metadata.update({"kernel_name": "masked_attention_kernel", "block_q": TILE, "block_k": TILE,
-                                "threads": 256, "implementation": implementation,
-                                "source": "libsfl.so gfx950 HIP kernel; not a profiler measurement"})
+        _record_launch_metadata(q, k, v, implementation, launch_metadata)
     return (out, lse) if return_lse else out
+
+
+def _record_launch_metadata(q, k, v, implementation, destination):
+    """Compiler resource data of the kernel this call launched (``triton_attention.py:39-57``
+    records the same fields from Triton's CompiledKernel), never a profiler measurement."""
+    info = _lib.masked_kernel_info(q.shape[-1], q.dtype, q.shape[2], k.stride(2), v.stride(2))
+    destination.update({
+        "kernel_name": info.name.decode(),
+        "n_regs": info.registers,
+        "n_spills": info.private_bytes // 4,  # spilled 32-bit values per lane
+        "private_segment_bytes": info.private_bytes,
+        "shared_memory_bytes": info.shared_bytes,
+        "threads": info.threads,
+        "block_q": TILE, "block_k": TILE, "queries_per_workgroup": info.queries_per_workgroup,
+        "implementation": implementation,
+        "source": "hipFuncGetAttributes of the gfx950 kernel; not rocprof profiling",
+        "asm_sha256": {"libsfl.so": _lib.library_sha256()},
+    })
 
 
 def causal_prefill(q, k, v, out):

@@ -20,6 +20,7 @@
 // a sum over keys, so any order both operands share is exact), and V^T rows
 // come from LDS as 8-byte runs.
 #include <climits>
+#include <stdio.h>
 
 #include "attn_mfma.hpp"
 #include "lds_dma.hpp"
@@ -954,30 +955,52 @@ void masked_attention32_kernel(AttnArgs a) {
   }
 }
 
+// The kernel a launch runs, chosen from the head dim and the K/V row strides
+// (the 32x32 kernel addresses K and V with 32-bit buffer offsets), with its
+// grid and workgroup size; shared by the launch and sfl_masked_attention_kernel_info.
+struct MaskedLaunch {
+  const void* fn;
+  const char* name;
+  unsigned queries_per_workgroup;
+  unsigned threads;
+};
+
 template <typename T>
-int launch_masked(const AttnArgs& a, int batch, int dim, hipStream_t stream) {
-  dim3 grid(unsigned((a.n + BQ - 1) / BQ) * unsigned(batch * a.heads));
+MaskedLaunch select_masked(int dim, long n, long k_row_stride, long v_row_stride) {
+  const bool offsets32 = n * k_row_stride * 2 < (1L << 31) && n * v_row_stride * 2 < (1L << 31);
   switch (dim) {
-    case 32: hipLaunchKernelGGL((masked_attention_kernel<T, 32>), grid, dim3(kThreads), 0, stream, a); break;
+    case 32:
+      return {reinterpret_cast<const void*>(&masked_attention_kernel<T, 32>), "masked_attention_kernel<D=32>",
+              unsigned(BQ), unsigned(kThreads)};
     case 64:
-      // The 32x32 kernel addresses K and V with 32-bit buffer offsets; its
-      // workgroups take two 64-query rows each.
-      if (long(a.n) * a.ks[2] * 2 < (1L << 31) && long(a.n) * a.vs[2] * 2 < (1L << 31))
-        hipLaunchKernelGGL((masked_attention32_kernel<T, 64>), dim3(unsigned((a.n + 2 * BQ - 1) / (2 * BQ)) *
-                           unsigned(batch * a.heads)), dim3(kA32Waves * kWave), 0, stream, a);
-      else
-        hipLaunchKernelGGL((masked_attention_pair_kernel<T>), grid, dim3(kPairWaves * kWave), 0, stream, a);
-      break;
+      if (offsets32)
+        return {reinterpret_cast<const void*>(&masked_attention32_kernel<T, 64>),
+                "masked_attention32_kernel<D=64>", unsigned(2 * BQ), unsigned(kA32Waves * kWave)};
+      return {reinterpret_cast<const void*>(&masked_attention_pair_kernel<T>), "masked_attention_pair_kernel<D=64>",
+              unsigned(BQ), unsigned(kPairWaves * kWave)};
     case 128:
-      if (long(a.n) * a.ks[2] * 2 < (1L << 31) && long(a.n) * a.vs[2] * 2 < (1L << 31))
-        hipLaunchKernelGGL((masked_attention32_kernel<T, 128>), dim3(unsigned((a.n + 2 * BQ - 1) / (2 * BQ)) *
-                           unsigned(batch * a.heads)), dim3(kA32Waves * kWave), 0, stream, a);
-      else
-        hipLaunchKernelGGL((masked_attention_kernel<T, 128>), grid, dim3(kThreads), 0, stream, a);
-      break;
-    default: return set_error(SFL_ERR_UNSUPPORTED, "masked_attention: head dim must be 32, 64 or 128");
+      if (offsets32)
+        return {reinterpret_cast<const void*>(&masked_attention32_kernel<T, 128>),
+                "masked_attention32_kernel<D=128>", unsigned(2 * BQ), unsigned(kA32Waves * kWave)};
+      return {reinterpret_cast<const void*>(&masked_attention_kernel<T, 128>), "masked_attention_kernel<D=128>",
+              unsigned(BQ), unsigned(kThreads)};
+    default: return {nullptr, nullptr, 0u, 0u};
   }
-  return check_launch("masked_attention");
+}
+
+template <typename T>
+int launch_masked(AttnArgs a, int batch, int dim, hipStream_t stream) {
+  const MaskedLaunch l = select_masked<T>(dim, a.n, a.ks[2], a.vs[2]);
+  if (!l.fn) return set_error(SFL_ERR_UNSUPPORTED, "masked_attention: head dim must be 32, 64 or 128");
+  const dim3 grid(unsigned((a.n + l.queries_per_workgroup - 1) / l.queries_per_workgroup) *
+                  unsigned(batch * a.heads));
+  void* args[] = {&a};
+  const hipError_t err = hipLaunchKernel(l.fn, grid, dim3(l.threads), args, 0, stream);
+  if (err != hipSuccess) {
+    (void)hipGetLastError();  // clear the launch error
+    return set_error(SFL_ERR_HIP, "masked_attention: launch of %s failed: %s", l.name, hipGetErrorString(err));
+  }
+  return SFL_OK;
 }
 
 }  // namespace
@@ -1028,3 +1051,26 @@ extern "C" int sfl_masked_attention(const void* q, const void* k, const void* v,
 }
 
 extern "C" int sfl_masked_attention_block(void) { return BQ; }
+
+extern "C" int sfl_masked_attention_kernel_info(int head_dim, int dtype, int n, long k_row_stride,
+                                                long v_row_stride, sfl_kernel_info* info) {
+  const char* what = "masked_attention_kernel_info";
+  if (!info) return set_error(SFL_ERR_INVALID, "%s: null pointer argument", what);
+  if (n < 1 || k_row_stride < 0 || v_row_stride < 0) return set_error(SFL_ERR_INVALID, "%s: bad sizes", what);
+  MaskedLaunch l{};
+  if (dtype == SFL_DTYPE_BF16) l = select_masked<bf16_t>(head_dim, n, k_row_stride, v_row_stride);
+  else if (dtype == SFL_DTYPE_F16) l = select_masked<f16_t>(head_dim, n, k_row_stride, v_row_stride);
+  else return set_error(SFL_ERR_UNSUPPORTED, "%s: dtype must be BF16 or F16", what);
+  if (!l.fn) return set_error(SFL_ERR_UNSUPPORTED, "%s: head dim must be 32, 64 or 128", what);
+  hipFuncAttributes attr{};
+  const hipError_t err = hipFuncGetAttributes(&attr, l.fn);
+  if (err != hipSuccess) return set_error(SFL_ERR_HIP, "%s: hipFuncGetAttributes: %s", what, hipGetErrorString(err));
+  snprintf(info->name, sizeof(info->name), "%s%s", l.name, dtype == SFL_DTYPE_BF16 ? " bf16" : " f16");
+  info->registers = attr.numRegs;
+  info->private_bytes = int(attr.localSizeBytes);
+  info->shared_bytes = int(attr.sharedSizeBytes);
+  info->max_threads = attr.maxThreadsPerBlock;
+  info->threads = int(l.threads);
+  info->queries_per_workgroup = int(l.queries_per_workgroup);
+  return SFL_OK;
+}

@@ -12,8 +12,9 @@ Differences, all widenings of the reference contract:
 
 * head dimensions 16 and 32 are accepted besides 64 and 128, and fp32 besides fp16/bf16
   (the 22.7M parity model has 16 heads of 32 and runs in fp32);
-* ``splits=None`` (the default here) picks the split count from the shape; an
-  integer in [1, 128] is honoured exactly as in the reference;
+* ``splits`` defaults to 1 as in the reference (``kernel.py:85``); an integer
+  in [1, 128] is honoured exactly, and ``splits=None`` picks the split count
+  from the shape (``auto_splits``);
 * ``variant`` accepts ``"token"`` and ``"tile"`` and both run the same kernel:
   the gfx950 kernel always updates its softmax state once per tile of keys.
 """
@@ -121,7 +122,7 @@ class PreparedDecode:
                    (self.partial_max, self.partial_sum, self.partial_output))
 
 
-def prepare(q, k, v, lengths=None, *, splits=None, scale=None, variant="token") -> PreparedDecode:
+def prepare(q, k, v, lengths=None, *, splits=1, scale=None, variant="token") -> PreparedDecode:
     """Validate and allocate outside capture, then return a reusable operation (``kernel.py:85-113``)."""
     if variant not in ("token", "tile"):
         raise ValueError("variant must be 'token' or 'tile'")
@@ -145,6 +146,6 @@ def prepare(q, k, v, lengths=None, *, splits=None, scale=None, variant="token") 
                           float(scale), variant)
 
 
-def decode(q, k, v, lengths=None, *, splits=None, scale=None, variant="token") -> torch.Tensor:
+def decode(q, k, v, lengths=None, *, splits=1, scale=None, variant="token") -> torch.Tensor:
     """Allocate scratch and compute one decode step on the current stream (``kernel.py:116-118``)."""
     return prepare(q, k, v, lengths, splits=splits, scale=scale, variant=variant)()

@@ -47,9 +47,55 @@ def residual_ksplit(n: int, target_groups: int = 256) -> int:
     return max(1, min(16, target_groups // max(1, n // 16)))
 
 
+def parameter_version(model) -> tuple:
+    """Changes whenever a parameter is replaced or modified in place (``Tensor._version``)."""
+    return tuple((p.data_ptr(), p._version, p.dtype, p.device) for p in model.parameters())
+
+
+class DecodeWeights:
+    """Device copies of a model's weights in the layouts the kernels read, made once.
+
+    ``wqkv``: ``[q; k; v]`` stacked, ``[3d, d]`` (prefill GEMM); ``p_*``: every
+    projection in the decode GEMVs' packed tile layout (one contiguous 1 KB
+    block per 16 rows x K chunk); ``w13``: W1/W3 interleaved in blocks of 8
+    rows, the layout the prefill SwiGLU GEMM pairs in-lane (made on first use).
+    ``version`` is the model's ``parameter_version`` when they were made.
+    """
+
+    def __init__(self, model):
+        self.version = parameter_version(model)
+        self.model = model
+        self.wqkv = [torch.cat([blk.attn.q_proj.weight, blk.attn.k_proj.weight, blk.attn.v_proj.weight])
+                     .contiguous() for blk in model.layers]
+        pk = _lib.pack_gemv
+        self.p_qkv = [pk(w) for w in self.wqkv]
+        self.p_out = [pk(blk.attn.output_proj.weight) for blk in model.layers]
+        self.p_w1 = [pk(blk.ffn.w1.weight) for blk in model.layers]
+        self.p_w3 = [pk(blk.ffn.w3.weight) for blk in model.layers]
+        self.p_w2 = [pk(blk.ffn.w2.weight) for blk in model.layers]
+        self.p_head = pk(model.lm_head.weight)
+        self._w13 = None
+
+    def w13(self):
+        if self._w13 is None:
+            f, d = self.model.d_ff, self.model.d_model
+            self._w13 = [torch.stack([blk.ffn.w1.weight.view(f // 8, 8, d), blk.ffn.w3.weight.view(f // 8, 8, d)],
+                                     dim=1).reshape(2 * f, d).contiguous() for blk in self.model.layers]
+        return self._w13
+
+
+def decode_weights(model) -> DecodeWeights:
+    """The model's ``DecodeWeights``, remade only after a parameter changed."""
+    cached = getattr(model, "_sfl_decode_weights", None)
+    if cached is None or cached.version != parameter_version(model):
+        model._sfl_decode_weights = None  # drop the stale copies before packing anew
+        cached = model._sfl_decode_weights = DecodeWeights(model)
+    return cached
+
+
 class DecodeSession:
     def __init__(self, model, batch: int, capacity: int | None = None, *, splits: int | None = None,
-                 record_logits: bool = False):
+                 record_logits: bool = False, deterministic: bool = False):
         param = model.lm_head.weight
         if param.device.type != "cuda":
             raise RuntimeError("systems_for_llms_amd runs on the GPU: move the model to a HIP device first")
@@ -73,17 +119,11 @@ class DecodeSession:
         from .model import rope_tables
         cos, sin = rope_tables(model.theta, self.dk, cap)
         self.cos, self.sin = cos.to(dev), sin.to(dev)
-        self.wqkv = [torch.cat([blk.attn.q_proj.weight, blk.attn.k_proj.weight, blk.attn.v_proj.weight])
-                     .contiguous() for blk in model.layers]
-        # Decode-GEMV copies of the weights in the packed tile layout (one contiguous
-        # 1 KB block per 16 rows x K chunk); the prefill GEMMs read the [N, K] originals.
-        pk = _lib.pack_gemv
-        self.p_qkv = [pk(w) for w in self.wqkv]
-        self.p_out = [pk(blk.attn.output_proj.weight) for blk in model.layers]
-        self.p_w1 = [pk(blk.ffn.w1.weight) for blk in model.layers]
-        self.p_w3 = [pk(blk.ffn.w3.weight) for blk in model.layers]
-        self.p_w2 = [pk(blk.ffn.w2.weight) for blk in model.layers]
-        self.p_head = pk(model.lm_head.weight)
+        # Packed copies shared by every session of this model while its parameters are
+        # unchanged; the session keeps a reference, so its captured launches stay valid.
+        self.weights = w = decode_weights(model)
+        self.wqkv, self.p_qkv, self.p_out = w.wqkv, w.p_qkv, w.p_out
+        self.p_w1, self.p_w3, self.p_w2, self.p_head = w.p_w1, w.p_w3, w.p_w2, w.p_head
         self.k_cache = torch.zeros((n, batch, h, cap, self.dk), device=dev, dtype=dt)
         self.v_cache = torch.zeros_like(self.k_cache)
         self.x = torch.zeros((batch, d), device=dev, dtype=torch.float32)
@@ -99,6 +139,7 @@ class DecodeSession:
         self.attn = torch.zeros((blocks, ROW_BLOCK * d), device=dev, dtype=torch.float32)
         self.hidden = torch.zeros((blocks, ROW_BLOCK * f), device=dev, dtype=torch.float32)
         self.act_code = _lib.DTYPE_BF16X2 if dt == torch.bfloat16 else _lib.DTYPE_F32X
+        self.deterministic = deterministic
         self.splits = splits or auto_splits(batch, h, cap)
         self.pmax = torch.empty((batch, h, self.splits), device=dev, dtype=torch.float32)
         self.psum = torch.empty_like(self.pmax)
@@ -113,9 +154,14 @@ class DecodeSession:
         self.prompt_len = torch.ones(batch, device=dev, dtype=torch.int32)
         self.logits = (torch.zeros((batch, cap, v), device=dev, dtype=torch.float32)
                        if record_logits else None)
-        # One split: the attention kernel also applies output_proj and adds it to x.
-        self.fused_out_proj = self.splits == 1 and self.dk % (32 if dt == torch.bfloat16 else 16) == 0 \
-            and self.dk <= 128 and self.dk & (self.dk - 1) == 0
+        # One split: the attention kernel also applies output_proj and adds it to x
+        # (fp32 atomics from the 16 heads: the summation order varies from run to run).
+        # deterministic=True keeps output_proj and w2 as plain GEMVs whose every output
+        # has one writer, so repeated runs give bit-identical logits.
+        self.fused_out_proj = not deterministic and self.splits == 1 \
+            and self.dk % (32 if dt == torch.bfloat16 else 16) == 0 and self.dk <= 128 and self.dk & (self.dk - 1) == 0
+        self.ksplit = 1 if deterministic else residual_ksplit(d)
+        self.position = 0  # host mirror of every row's position (all rows move together)
         self.graph = None
         self._calls = self._plan()
 
@@ -146,13 +192,13 @@ class DecodeSession:
                     self.act_code)))
                 calls.append((lib.sfl_linear_residual, (
                     self.attn.data_ptr(), self.p_out[layer].data_ptr(), self.x.data_ptr(), rows, d, d,
-                    residual_ksplit(d), code)))
+                    self.ksplit, code)))
             calls.append((lib.sfl_rmsnorm_swiglu, (
                 self.x.data_ptr(), blk.ffn_norm.weight.data_ptr(), self.p_w1[layer].data_ptr(),
                 self.p_w3[layer].data_ptr(), self.hidden.data_ptr(), rows, d, f, code)))
             calls.append((lib.sfl_linear_residual, (
                 self.hidden.data_ptr(), self.p_w2[layer].data_ptr(), self.x.data_ptr(), rows, d, f,
-                residual_ksplit(d), code)))
+                self.ksplit, code)))
         logits = self.logits.data_ptr() if self.logits is not None else None
         calls.append((lib.sfl_rmsnorm_lm_head, (
             self.x.data_ptr(), m.ln_final.weight.data_ptr(), self.p_head.data_ptr(),
@@ -184,6 +230,7 @@ class DecodeSession:
         self.pos.zero_()
         self.lengths.fill_(1)
         self.prompt_len.fill_(forced_length or prompt.shape[1])
+        self.position = 0
         self._embed_current()
 
     def _embed_current(self) -> None:
@@ -194,14 +241,6 @@ class DecodeSession:
                   self.d, self.code, stream)
 
     # -- prefill ------------------------------------------------------------
-    def _prefill_weights(self):
-        """W1/W3 interleaved in blocks of 8 rows, the layout the SwiGLU GEMM pairs in-lane."""
-        if getattr(self, "_w13", None) is None:
-            f, d = self.d_ff, self.d
-            self._w13 = [torch.stack([blk.ffn.w1.weight.view(f // 8, 8, d), blk.ffn.w3.weight.view(f // 8, 8, d)],
-                                     dim=1).reshape(2 * f, d).contiguous() for blk in self.model.layers]
-        return self._w13
-
     @torch.no_grad()
     def prefill(self, prompt: torch.Tensor, all_logits: bool = False,
                 forced: torch.Tensor | None = None) -> torch.Tensor | None:
@@ -228,7 +267,7 @@ class DecodeSession:
         d, h, dk, f, v = self.d, self.heads, self.dk, self.d_ff, self.vocab
         m_rows = b * t
         dev, code = self.device, self.code
-        w13 = self._prefill_weights()
+        w13 = self.weights.w13()
         self.tokens.zero_()
         self.tokens[:, :t] = prompt.to(dev)
         self.predicted.fill_(-1)
@@ -271,6 +310,7 @@ class DecodeSession:
         self.x.copy_(x.view(b, t, d)[:, t - 1])
         self.pos.fill_(t - 1)
         self.lengths.fill_(t)
+        self.position = t
         for fn, args in self._calls[-2:]:  # the lm_head and the token step
             status = fn(*args, st)
             if status != 0:
@@ -280,13 +320,32 @@ class DecodeSession:
 
     def set_position(self, position: int) -> None:
         """Rewind/advance every row to ``position`` (the cache below it is kept) and re-embed."""
+        if not 0 <= position < self.cap:
+            raise ValueError(f"position must be in [0, capacity={self.cap})")
         self.pos.fill_(position)
         self.lengths.fill_(position + 1)
+        self.position = position
         self._embed_current()
+
+    def _advance(self, steps: int) -> None:
+        """Account for ``steps`` steps; the last may run at position capacity - 1.
+
+        A step at position p appends K/V at p and picks token p + 1; at
+        p = capacity - 1 it still produces the logits of p but records no token
+        and leaves the device position where it is, so no further step may run
+        until the session is restarted or rewound.
+        """
+        if self.position + steps > self.cap:
+            raise ValueError(f"{steps} steps from position {self.position} run past capacity {self.cap}")
+        self.position += steps
 
     # -- execution ----------------------------------------------------------
     def step(self) -> None:
         """Launch one decode step on the current stream (no host synchronisation)."""
+        self._advance(1)
+        self._launch()
+
+    def _launch(self) -> None:
         stream = _lib.stream_handle(self.device)
         for fn, args in self._calls:
             status = fn(*args, stream)
@@ -295,18 +354,29 @@ class DecodeSession:
                                    f"{_lib.lib().sfl_last_error().decode(errors='replace')}")
 
     def capture(self, steps_per_graph: int = 1) -> torch.cuda.CUDAGraph:
-        """Capture ``steps_per_graph`` steps into one HIP graph (replayable, state on device)."""
+        """Capture ``steps_per_graph`` steps into one HIP graph (replayable, state on device).
+
+        Capturing records the launches without executing them; ``replay`` runs
+        ``steps_per_graph`` steps from wherever the device state stands.
+        """
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph):
             for _ in range(steps_per_graph):
-                self.step()
+                self._launch()
         self.graph, self.graph_steps = graph, steps_per_graph
         return graph
+
+    def replay(self) -> None:
+        """Replay the captured graph (``graph_steps`` steps)."""
+        self._advance(self.graph_steps)
+        self.graph.replay()
 
     def run(self, steps: int, use_graph: bool = False) -> None:
         """Advance every row by ``steps`` positions (graph replays when ``use_graph``)."""
         if steps <= 0:
             return
+        self._advance(steps)  # checked up front: nothing launches if it would overrun
+        self.position -= steps
         if not use_graph:
             for _ in range(steps):
                 self.step()
@@ -317,6 +387,6 @@ class DecodeSession:
         if steps == 0:
             return
         if self.graph is None or self.graph_steps != 1:
-            self.capture(1)  # capturing records the launches without executing them
+            self.capture(1)
         for _ in range(steps):
-            self.graph.replay()
+            self.replay()

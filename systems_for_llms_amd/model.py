@@ -146,6 +146,9 @@ class TransformerLM(nn.Module):
         self.theta = rope_theta
         self.attention_backend = attention_backend
         self.activation_checkpointing = activation_checkpointing
+        # Not in the reference: True keeps every decode output at one writer (no fp32
+        # atomics), so repeated forward/generate calls give bit-identical results.
+        self.deterministic = False
         self.token_embeddings = Embedding(vocab_size, d_model, device, dtype)
         self.layers = nn.ModuleList([
             TransformerBlock(d_model, num_heads, d_ff, rope_theta, context_length, device, dtype,
@@ -205,35 +208,64 @@ class TransformerLM(nn.Module):
         if not 0 < input_ids.shape[-1] <= self.context_length:
             raise ValueError("sequence length must be between 1 and context_length")
 
+    def decode_session(self, batch: int, capacity: int, *, record_logits: bool = False,
+                       deterministic: bool = False) -> "_engine.DecodeSession":
+        """A ``DecodeSession`` of at least ``capacity`` positions for ``batch`` sequences.
+
+        The last session is kept and reused by later calls with the same batch,
+        logits recording and determinism and no larger capacity, while the
+        parameters are unchanged; its packed weights are shared through
+        ``engine.decode_weights`` (remade only after a parameter changes), so
+        repeated ``forward``/``generate`` calls neither repack weights nor
+        reallocate the KV cache.
+        """
+        session = getattr(self, "_sfl_session", None)
+        reuse = (session is not None and session.batch == batch and capacity <= session.cap
+                 and (session.logits is not None) == record_logits and session.deterministic == deterministic
+                 and session.weights is _engine.decode_weights(self))
+        if not reuse:
+            self._sfl_session = None  # free the previous KV cache first
+            session = self._sfl_session = _engine.DecodeSession(
+                self, batch=batch, capacity=capacity, record_logits=record_logits, deterministic=deterministic)
+        return session
+
     @torch.no_grad()
     def forward(self, input_ids: torch.Tensor) -> torch.Tensor:
         """Logits ``[..., T, vocab]`` for every position (``transformer.py:121-139``)."""
         self._check_ids(input_ids)
         lead = input_ids.shape[:-1]
         ids = input_ids.reshape(-1, input_ids.shape[-1])
+        t = ids.shape[-1]
         if self._gemm_prefill():
             # One pass of MFMA GEMMs and masked attention over the whole prompt.
-            session = _engine.DecodeSession(self, batch=ids.shape[0], capacity=ids.shape[-1])
+            session = self.decode_session(ids.shape[0], t, deterministic=self.deterministic)
             logits = session.prefill(ids, all_logits=True)
-            return logits.to(torch.bfloat16).reshape(*lead, ids.shape[-1], self.vocab_size)
-        session = _engine.DecodeSession(self, batch=ids.shape[0], capacity=ids.shape[-1],
-                                        record_logits=True)
+            return logits.to(torch.bfloat16).reshape(*lead, t, self.vocab_size)
+        session = self.decode_session(ids.shape[0], t, record_logits=True, deterministic=self.deterministic)
         session.start(ids)
-        session.run(ids.shape[-1])
+        session.run(t)
         # The reference returns logits in the parameter dtype (transformer.py:138).
-        return session.logits.to(self.lm_head.weight.dtype).reshape(*lead, ids.shape[-1], self.vocab_size)
+        return session.logits[:, :t].to(self.lm_head.weight.dtype).reshape(*lead, t, self.vocab_size)
 
     @torch.no_grad()
     def generate(self, input_ids: torch.Tensor, max_new_tokens: int, *, use_graph: bool = True,
                  capacity: int | None = None) -> torch.Tensor:
-        """Greedy continuation: ids ``[B, T + max_new_tokens]`` (argmax, first index on ties)."""
+        """Greedy continuation: ids ``[B, T + max_new_tokens]`` (argmax, first index on ties).
+
+        NaN logits are never chosen (``torch.argmax`` would return a NaN's
+        index); a row whose logits are all NaN continues with token 0.
+        ``capacity`` (default T + max_new_tokens) sizes the KV cache and must
+        hold the whole result.
+        """
         self._check_ids(input_ids)
         if input_ids.ndim != 2:
             raise ValueError("generate expects input_ids of shape [batch, sequence]")
         total = input_ids.shape[1] + max_new_tokens
         if max_new_tokens < 0 or total > self.context_length:
             raise ValueError("sequence length must be between 1 and context_length")
-        session = _engine.DecodeSession(self, batch=input_ids.shape[0], capacity=capacity or total)
+        if capacity is not None and not total <= capacity <= self.context_length:
+            raise ValueError("capacity must be in [prompt length + max_new_tokens, context_length]")
+        session = self.decode_session(input_ids.shape[0], capacity or total, deterministic=self.deterministic)
         if self._gemm_prefill() and max_new_tokens > 0:
             session.prefill(input_ids)  # positions 0..T-1 at once; token T chosen
             session.run(max_new_tokens - 1, use_graph=use_graph)

@@ -33,6 +33,15 @@ def test_unknown_variant_and_bad_ratio_rejected():
                 torch.zeros(1, 2, 17, 48, dtype=torch.float16))
 
 
+def test_split_count_defaults_to_one_as_in_the_reference():
+    import inspect
+
+    from systems_for_llms_amd.decode import decode
+
+    for fn in (prepare, decode):  # kernel.py:85,116: splits=1
+        assert inspect.signature(fn).parameters["splits"].default == 1
+
+
 def test_auto_splits_bounds():
     assert auto_splits(64, 16, 16384) == 1   # config 4: 1024 workgroups already
     assert auto_splits(16, 16, 4096) == 1    # 324M decode: one workgroup per (batch, head)

@@ -1,0 +1,64 @@
+"""GPU parity of the headline workload, BASELINE config 3, against the CPU oracle.
+
+324.1M llmlab decoder (``configs/scale-324m-s4096.json:3-11``), bf16, seeded
+N(0, 0.02) weights, batch 16: the GEMM prefill of 3072 prompt tokens, then
+1023 graph-replayed decode steps to context 4096 (positions 3072..4094),
+teacher-forced on a fixed random continuation so every row's tokens are
+known in advance. Two rows (0 and 15, the first and last of the batch) are
+recomputed on the CPU by the KV-cached oracle (``transformer.py:121-139``
+semantics) in fp32, and with the kernels' storage formats (the bf16-storage
+floor: bf16 weights and KV cache; bf16 GEMM inputs over the prompt chunk, as
+the prefill stores them; fp32 inputs over the decode chunk, as the decode
+GEMVs keep them). All 1023 decode positions of both rows are compared.
+"""
+
+import pytest
+import torch
+
+from oracle import model as om
+from systems_for_llms_amd.config import load_model_config
+from systems_for_llms_amd.engine import DecodeSession
+from systems_for_llms_amd.model import TransformerLM
+from systems_for_llms_amd.weights import seeded_prompt, seeded_state_dict
+
+from gates import bf16_gate
+
+pytestmark = pytest.mark.gpu
+
+PROMPT, CONTEXT, BATCH, ROWS = 3072, 4096, 16, (0, 15)
+
+
+def test_config3_prefill_and_decode_to_4096_teacher_forced():
+    cfg = load_model_config("scale-324m-s4096")
+    assert cfg.context_length == CONTEXT
+    sd = seeded_state_dict(cfg, 1337)
+    seq = seeded_prompt(cfg.vocab_size, BATCH, CONTEXT - 1, 2027)  # prompt + forced continuation
+    model = TransformerLM.from_config(cfg, device="cuda", dtype=torch.bfloat16)
+    model.load_state_dict(sd)
+    session = DecodeSession(model.eval(), BATCH, CONTEXT, record_logits=True)
+    session.prefill(seq[:, :PROMPT].cuda(), forced=seq.cuda())
+    session.run(CONTEXT - 1 - PROMPT, use_graph=True)  # positions 3072 .. 4094
+    torch.cuda.synchronize()
+    assert int(session.pos[0]) == CONTEXT - 1
+    got = session.logits[list(ROWS), PROMPT:CONTEXT - 1].float().cpu()
+    # Teacher forcing kept every forced token; the model's own picks went to `predicted`.
+    assert torch.equal(session.tokens[:, :CONTEXT - 1].cpu(), seq)
+    assert torch.equal(session.predicted[:, PROMPT + 1:CONTEXT].cpu(), session.logits[:, PROMPT:CONTEXT - 1]
+                       .argmax(-1).cpu())
+    del session, model
+    torch.cuda.empty_cache()
+
+    torch.set_num_threads(16)
+    rows = seq[list(ROWS)]
+    ref_cache = om.KVCacheOracle(sd, cfg, len(ROWS), CONTEXT)
+    ref_cache.step(rows[:, :PROMPT])
+    ref = ref_cache.step(rows[:, PROMPT:])
+    del ref_cache
+    floor_cache = om.KVCacheOracle(om.round_weights(sd), cfg, len(ROWS), CONTEXT, kv_dtype=torch.bfloat16)
+    floor_cache.step(rows[:, :PROMPT], act_dtype=torch.bfloat16)
+    floor = floor_cache.step(rows[:, PROMPT:])
+    del floor_cache
+    first, last = slice(0, 64), slice(-32, None)
+    bf16_gate("config3 rows 0,15, positions 3072..3135", got[:, first], ref[:, first], floor[:, first])
+    bf16_gate("config3 rows 0,15, positions 4063..4094", got[:, last], ref[:, last], floor[:, last])
+    bf16_gate("config3 rows 0,15, positions 3072..4094", got, ref, floor)

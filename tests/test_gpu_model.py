@@ -2,7 +2,9 @@
 
 Gates: fp32 -- identical greedy token sequences; bf16 --
 logits within max-abs 2e-2 of the fp32 reference and >= 99% greedy agreement,
-measured teacher-forced on the fp32 reference's own sequence.
+measured teacher-forced. On these random weights bf16 storage alone misses
+that gate for some configs; ``bf16_gate`` prints the north-star numbers and
+checks the kernels tightly against the bf16-storage floor.
 """
 
 import pytest
@@ -14,9 +16,9 @@ from systems_for_llms_amd.engine import DecodeSession
 from systems_for_llms_amd.model import TransformerLM
 from systems_for_llms_amd.weights import seeded_prompt, seeded_state_dict
 
-pytestmark = pytest.mark.gpu
+from gates import BF16_ATOL, bf16_gate
 
-BF16_ATOL = 2e-2
+pytestmark = pytest.mark.gpu
 
 
 def gpu_model(cfg, sd, dtype):
@@ -85,31 +87,6 @@ def test_config1_from_reference_checkpoint_greedy_identical(golden, tmp_path):
     prompt = seeded_prompt(cfg.vocab_size, 1, c1["prompt_length"], c1["prompt_seed"]).cuda()
     ids = model.generate(prompt, c1["steps"]).cpu()
     assert torch.equal(ids, torch.from_numpy(arrays["c1_ids"]))
-
-
-def bf16_gate(name, got, ref, floor, targets=None):
-    """Judge bf16 logits against the fp32 reference and against the bf16-storage floor.
-
-    ``floor`` is the CPU oracle run with the same storage formats as the kernels
-    (weights and KV cache rounded to bf16) and exact fp32 arithmetic otherwise.
-    On the N(0, 0.02) random weights the logits are flat, so the formats alone
-    move logits by ~2e-2 and flip a few near-tied greedy tokens; the BASELINE
-    tolerance (max-abs 2e-2, >= 99% agreement vs fp32) is applied up to that
-    floor, and the kernels themselves must agree with the floor tightly.
-    """
-    targets = ref.argmax(-1) if targets is None else targets
-    err = (got - ref).abs().max().item()
-    floor_err = (floor - ref).abs().max().item()
-    agree = (got.argmax(-1) == targets).float().mean().item()
-    floor_agree = (floor.argmax(-1) == targets).float().mean().item()
-    kernel_err = (got - floor).abs().max().item()
-    kernel_agree = (got.argmax(-1) == floor.argmax(-1)).float().mean().item()
-    print(f"{name}: vs fp32 max-abs {err:.4f} agree {agree:.4f} | storage floor max-abs {floor_err:.4f} "
-          f"agree {floor_agree:.4f} | kernels vs floor max-abs {kernel_err:.4f} agree {kernel_agree:.4f}")
-    assert err <= max(BF16_ATOL, 1.1 * floor_err)
-    assert agree >= min(0.99, floor_agree - 0.015)
-    assert kernel_err <= 1e-2
-    assert kernel_agree >= 0.97
 
 
 def test_config1_bf16_teacher_forced_logits_and_agreement(golden):
@@ -207,3 +184,55 @@ def test_split_cache_path_matches_fused_path(dtype):
     else:  # against the oracle with the kernels' storage formats (bf16 weights and KV)
         floor = om.forward(om.round_weights(sd), cfg, ids.cpu(), kv_dtype=torch.bfloat16)[:, :95]
         assert (fused - floor).abs().max().item() <= 1e-2
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_generate_reuses_packed_weights_until_a_parameter_changes(dtype, monkeypatch):
+    """Repeated generate() calls pack the decode weights once and reuse the session; an
+    in-place parameter change repacks, and the result follows the new weights."""
+    from systems_for_llms_amd import _lib
+
+    cfg = ModelConfig(vocab_size=500, context_length=64, d_model=256, num_layers=2, num_heads=4,
+                      d_ff=512, rope_theta=10000.0)
+    sd = seeded_state_dict(cfg, 41)
+    model = gpu_model(cfg, sd, dtype)
+    model.deterministic = True  # bit-identical reruns: the equality checks below are exact
+    packs = []
+    real = _lib.pack_gemv
+    monkeypatch.setattr(_lib, "pack_gemv", lambda w: packs.append(w.shape) or real(w))
+    prompt = seeded_prompt(cfg.vocab_size, 2, 20, 42).cuda()
+    first = model.generate(prompt, 10)
+    per_model = len(packs)
+    assert per_model == 5 * cfg.num_layers + 1  # q/k/v, output_proj, w1, w3, w2 per layer; lm_head
+    session = model._sfl_session
+    assert torch.equal(model.generate(prompt, 10), first)
+    model.generate(prompt[:, :15], 5)  # a shorter request fits the same session
+    assert len(packs) == per_model and model._sfl_session is session
+    with torch.no_grad():
+        model.layers[1].ffn.w2.weight.mul_(0.5)
+    changed = model.generate(prompt, 10)
+    assert len(packs) == 2 * per_model
+    fresh = gpu_model(cfg, {**sd, "layers.1.ffn.w2.weight": sd["layers.1.ffn.w2.weight"] * 0.5}, dtype)
+    fresh.deterministic = True
+    assert torch.equal(changed, fresh.generate(prompt, 10))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_deterministic_decode_is_bit_reproducible(dtype):
+    """deterministic=True: output_proj and w2 as one-writer GEMVs (no atomics), so two runs give
+    bit-identical logits; they match the default fused path to float reassociation."""
+    cfg = ModelConfig(vocab_size=500, context_length=96, d_model=256, num_layers=2, num_heads=4,
+                      d_ff=512, rope_theta=10000.0)
+    model = gpu_model(cfg, seeded_state_dict(cfg, 51), dtype)
+    ids = seeded_prompt(cfg.vocab_size, 3, 96, 52).cuda()
+    runs = []
+    for deterministic in (True, True, False):
+        session = DecodeSession(model, 3, 96, record_logits=True, deterministic=deterministic)
+        assert session.fused_out_proj != deterministic and (session.ksplit == 1) == deterministic
+        session.start(ids)
+        session.run(96, use_graph=True)
+        runs.append(session.logits.clone())
+    assert torch.equal(runs[0], runs[1])
+    err = (runs[0] - runs[2]).abs().max().item()
+    print(f"{dtype}: deterministic vs fused path max-abs {err:.2e}")
+    assert err < (2e-5 if dtype == torch.float32 else 2e-3)

@@ -84,6 +84,46 @@ def test_kv_cached_equals_recompute_and_prefix_invariance(golden):
     torch.testing.assert_close(om.forward(sd, cfg, changed)[:, :9], full[:, :9], atol=1e-6, rtol=1e-5)
 
 
+def test_storage_format_floors_are_consistent(golden):
+    """The bf16-storage floors the GPU gates use: chunked cache == full forward under the
+    same formats, fp32 formats are exact no-ops, and every rounding point matters."""
+    meta, arrays = golden
+    cfg = _tiny(meta)
+    sd = om.round_weights(seeded_state_dict(cfg, meta["tiny"]["seed"]))
+    ids = torch.from_numpy(arrays["tiny_ids"])
+    bf = torch.bfloat16
+    full = om.forward(sd, cfg, ids, kv_dtype=bf, act_dtype=bf)
+    cache = om.KVCacheOracle(sd, cfg, ids.shape[0], kv_dtype=bf)
+    pieces = [cache.step(ids[:, :7], act_dtype=bf), cache.step(ids[:, 7:], act_dtype=bf)]
+    torch.testing.assert_close(torch.cat(pieces, dim=1), full, atol=2e-6, rtol=2e-5)
+    plain = om.forward(sd, cfg, ids)
+    assert torch.equal(om.forward(sd, cfg, ids, kv_dtype=torch.float32, act_dtype=torch.float32), plain)
+    # Each rounding point is applied: skipping any one of them changes the floor (per layer:
+    # attention input, q, attention output, SwiGLU input, hidden; then the final norm).
+    base = om.forward(sd, cfg, ids, act_dtype=bf)
+    real = om._round
+    for skip in range(5 * cfg.num_layers + 1):
+        calls = [0]
+
+        def partial(t, dtype, skip=skip):
+            if dtype is not bf:
+                return real(t, dtype)
+            calls[0] += 1
+            return t if calls[0] - 1 == skip else real(t, dtype)
+        om._round = partial
+        try:
+            moved = om.forward(sd, cfg, ids, act_dtype=bf)
+        finally:
+            om._round = real
+        assert calls[0] == 5 * cfg.num_layers + 1
+        assert not torch.equal(moved, base), f"rounding point {skip} unused"
+    # A mixed run (prompt chunk with bf16 GEMM inputs, later positions fp32) sits between the two.
+    cache = om.KVCacheOracle(sd, cfg, ids.shape[0], kv_dtype=bf)
+    mixed = torch.cat([cache.step(ids[:, :7], act_dtype=bf), cache.step(ids[:, 7:])], dim=1)
+    torch.testing.assert_close(mixed[:, :7], full[:, :7], atol=2e-6, rtol=2e-5)
+    assert not torch.equal(mixed[:, 7:], full[:, 7:])
+
+
 @pytest.mark.slow
 def test_config1_greedy_sequence_matches_reference(golden):
     meta, arrays = golden
