@@ -12,11 +12,36 @@ Weights are a plain ``state_dict`` with the reference's keys.
 
 from __future__ import annotations
 
+import contextlib
 import math
 
 import torch
 
 EPS = 1e-5
+_ACC = None  # accumulation dtype of the matrix products (None: the operands' own)
+
+
+@contextlib.contextmanager
+def accumulate_in(dtype):
+    """Run the oracle's matrix products with ``dtype`` accumulation, results cast back.
+
+    Not reference behaviour: with ``torch.float64`` it gives a second, equally
+    valid restatement whose fp32 results differ from the default only in
+    rounding, the yardstick for how far two exact computations drift apart
+    under the same storage formats.
+    """
+    global _ACC
+    previous, _ACC = _ACC, dtype
+    try:
+        yield
+    finally:
+        _ACC = previous
+
+
+def _mm(a, b):
+    if _ACC is None:
+        return torch.matmul(a, b)
+    return torch.matmul(a.to(_ACC), b.to(_ACC)).to(a.dtype)
 
 
 def rope_tables(theta: float, d_k: int, max_seq_len: int) -> tuple[torch.Tensor, torch.Tensor]:
@@ -47,19 +72,68 @@ def rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, positions: torch
     return out
 
 
-def attention_core(q, k, v, mask):
-    """Eager masked attention, ``attention.py:61-98``; mask True = allowed."""
-    scores = torch.matmul(q, k.transpose(-1, -2)) / math.sqrt(q.shape[-1])
+def attention_core(q, k, v, mask, p_dtype=None):
+    """Eager masked attention, ``attention.py:61-98``; mask True = allowed.
+
+    ``p_dtype`` (not in the reference; a storage-format floor) stores the
+    softmax probabilities in that format as a batched prefill kernel does:
+    see ``_attention_stored_probabilities``.
+    """
+    if p_dtype is not None:
+        return _attention_stored_probabilities(q, k, v, mask, p_dtype)
+    scores = _mm(q, k.transpose(-1, -2)) / math.sqrt(q.shape[-1])
     scores = scores.masked_fill(~mask, float("-inf"))
     work = scores.float() if scores.dtype in (torch.bfloat16, torch.float16) else scores
     peak = torch.max(work, dim=-1, keepdim=True).values
     e = torch.exp(work - peak)
     weights = (e / torch.sum(e, dim=-1, keepdim=True)).to(scores.dtype)
-    return torch.matmul(weights, v)
+    return _mm(weights, v)
+
+
+BLOCK_K = 64      # key tile of the batched (prefill) attention
+LAZY_LOG2 = 8.0   # slack of its running maximum, in log2 units
+LOG2E = 1.4426950408889634
+
+
+def _attention_stored_probabilities(q, k, v, mask, p_dtype):
+    """Online-softmax attention over 64-key tiles with the probabilities stored in ``p_dtype``.
+
+    The format floor of a flash-style prefill kernel that feeds its P.V
+    products with narrow probabilities: per query, key tiles in ascending
+    order; a running maximum m (log2 units) that moves to a tile's maximum
+    only when that exceeds it by more than ``LAZY_LOG2`` (rescaling the
+    accumulators by 2^(m_old - m_new)); probabilities p = 2^(s*c - m), with
+    c = scale * log2(e) in fp32, rounded to ``p_dtype``; row sum l and output
+    accumulated from the rounded p in fp32; out = o * (1/l), zero for a row
+    with no admissible key. The result equals softmax attention up to those
+    roundings; the same scores with exact probabilities give ``attention_core``.
+    """
+    f32 = torch.float32
+    c = torch.tensor(q.shape[-1] ** -0.5, dtype=f32) * torch.tensor(LOG2E, dtype=f32)
+    scores = _mm(q.to(f32), k.to(f32).transpose(-1, -2)).masked_fill(~mask, float("-inf"))
+    lead, n_keys = scores.shape[:-1], scores.shape[-1]
+    m = torch.full(lead, float("-inf"), dtype=f32)
+    l = torch.zeros(lead, dtype=f32)
+    o = torch.zeros((*lead, v.shape[-1]), dtype=f32)
+    for k0 in range(0, n_keys, BLOCK_K):
+        tile = scores[..., k0:k0 + BLOCK_K]
+        top = tile.amax(dim=-1) * c
+        grow = top > m + LAZY_LOG2  # never for a tile with no admissible key (top = -inf)
+        m_new = torch.where(grow, top, m)
+        alpha = torch.where(grow, torch.exp2(m - m_new), torch.ones_like(m))
+        m = m_new
+        shift = torch.where(torch.isinf(m), torch.zeros_like(m), m)
+        # fma(s, c, -shift) rounds once: form it in float64, round to fp32.
+        p = torch.exp2((tile.double() * c.double() - shift.double()[..., None]).to(f32))
+        p = p.to(p_dtype).to(f32)
+        l = l * alpha + p.sum(dim=-1)
+        o = o * alpha[..., None] + _mm(p, v[..., k0:k0 + BLOCK_K, :].to(f32))
+    inv = torch.where(l > 0, 1.0 / torch.where(l > 0, l, torch.ones_like(l)), torch.zeros_like(l))
+    return (o * inv[..., None]).to(q.dtype)
 
 
 def _linear(x, w):
-    return torch.matmul(x, w.t())
+    return _mm(x, w.t())
 
 
 def _split_heads(x, heads):
@@ -87,7 +161,7 @@ def _layer(sd, prefix, x, heads, cos, sin, positions, mask, kv_dtype=None, act_d
     if kv_dtype is not None:  # keys/values stored in a narrower cache format
         k = k.to(kv_dtype).to(x.dtype)
         v = v.to(kv_dtype).to(x.dtype)
-    a = _round(_merge_heads(attention_core(q, k, v, mask)), act_dtype)
+    a = _round(_merge_heads(attention_core(q, k, v, mask, act_dtype)), act_dtype)
     x = x + _linear(a, sd[prefix + "attn.output_proj.weight"])
     h = _round(rmsnorm(x, sd[prefix + "ffn_norm.weight"]), act_dtype)
     a = _linear(h, sd[prefix + "ffn.w1.weight"])
@@ -103,10 +177,11 @@ def forward(sd: dict, config, input_ids: torch.Tensor, dtype=torch.float32, kv_d
 
     Not in the reference, for bounding what storage formats alone change:
     ``kv_dtype`` rounds keys and values through a cache format; ``act_dtype``
-    rounds the GEMM inputs a batched prefill stores in a narrow format -- the
-    RMSNorm outputs (the final one included), q after RoPE, the merged
-    attention output and the SwiGLU hidden state (the residual stream stays in
-    ``dtype``).
+    rounds what a batched prefill stores in a narrow format -- the GEMM inputs
+    (the RMSNorm outputs, the final one included, q after RoPE, the merged
+    attention output and the SwiGLU hidden state) and the attention's softmax
+    probabilities (``attention_core``'s ``p_dtype``); the residual stream stays
+    in ``dtype``.
     """
     if not 0 < input_ids.shape[-1] <= config.context_length:
         raise ValueError("sequence length must be between 1 and context_length")
@@ -179,7 +254,8 @@ class KVCacheOracle:
             v = _split_heads(_linear(h, sd[p + "attn.v_proj.weight"]), self.heads)
             self.k[layer, :, :, start:total] = _round(k, self.kv_dtype)
             self.v[layer, :, :, start:total] = _round(v, self.kv_dtype)
-            a = attention_core(_round(q, act_dtype), self.k[layer, :, :, :total], self.v[layer, :, :, :total], mask)
+            a = attention_core(_round(q, act_dtype), self.k[layer, :, :, :total], self.v[layer, :, :, :total], mask,
+                               act_dtype)
             x = x + _linear(_round(_merge_heads(a), act_dtype), sd[p + "attn.output_proj.weight"])
             h = _round(rmsnorm(x, sd[p + "ffn_norm.weight"]), act_dtype)
             a1 = _linear(h, sd[p + "ffn.w1.weight"])

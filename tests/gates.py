@@ -4,15 +4,20 @@ BF16_ATOL, BF16_AGREE = 2e-2, 0.99  # north-star bf16 gate against fp32
 KERNEL_ATOL, KERNEL_AGREE = 2e-3, 0.99  # kernels against the bf16-storage floor
 
 
-def bf16_gate(name, got, ref, floor, targets=None, kernel_atol=KERNEL_ATOL, kernel_agree=KERNEL_AGREE):
+def bf16_gate(name, got, ref, floor, targets=None, envelope=None):
     """Judge bf16 logits against the fp32 reference and against the bf16-storage floor.
 
     ``floor`` is the CPU oracle run with the same storage formats as the kernels
     (weights and KV cache rounded to bf16, plus the GEMM inputs a batched
     prefill stores in bf16) and exact fp32 arithmetic otherwise. Two gates:
 
-    * the kernels against the floor, tight (``kernel_atol``, ``kernel_agree``):
-      what the HIP arithmetic adds on top of the storage formats;
+    * the kernels against the floor, tight (2e-3, 99% agreement): what the HIP
+      arithmetic adds on top of the storage formats. Where bf16 activations
+      are re-rounded at every stage (the GEMM prefill), two exact computations
+      drift apart chaotically -- a 1-ulp flip from fp32 reassociation changes
+      the next stage's rounding of its whole row -- so ``envelope``, a pair
+      (floor rows, the same rows recomputed with float64 accumulation), sets
+      the bound instead: twice that drift, and its agreement less 0.5%;
     * the north-star gate against fp32 (max-abs 2e-2, >= 99% greedy agreement).
       It is printed for every config. Where it is missed, the test requires
       that the storage formats alone (the floor) miss it too -- on the flat
@@ -20,6 +25,14 @@ def bf16_gate(name, got, ref, floor, targets=None, kernel_atol=KERNEL_ATOL, kern
       0.01 -- and that the kernels stay within the kernel-vs-floor bounds of
       the floor's own numbers.
     """
+    kernel_atol, kernel_agree, drift_note = KERNEL_ATOL, KERNEL_AGREE, ""
+    if envelope is not None:
+        base, wide = envelope
+        drift = (base - wide).abs().max().item()
+        drift_agree = (base.argmax(-1) == wide.argmax(-1)).float().mean().item()
+        kernel_atol = max(KERNEL_ATOL, 2.0 * drift)
+        kernel_agree = min(KERNEL_AGREE, drift_agree - 0.005)
+        drift_note = f" | floor vs float64-accumulated floor: max-abs {drift:.5f} agreement {drift_agree:.4f}"
     targets = ref.argmax(-1) if targets is None else targets
     err = (got - ref).abs().max().item()
     floor_err = (floor - ref).abs().max().item()
@@ -33,7 +46,7 @@ def bf16_gate(name, got, ref, floor, targets=None, kernel_atol=KERNEL_ATOL, kern
           f"max-abs {err:.4f} agreement {agree:.4f} -> {'met' if strict else 'MISSED'} | bf16-storage floor "
           f"vs fp32: max-abs {floor_err:.4f} agreement {floor_agree:.4f} -> "
           f"{'met' if floor_strict else 'MISSED'} | kernels vs floor: max-abs {kernel_err:.5f} "
-          f"agreement {k_agree:.4f} (gate {kernel_atol}, {kernel_agree})")
+          f"agreement {k_agree:.4f} (gate {kernel_atol:.5f}, {kernel_agree:.4f})" + drift_note)
     assert kernel_err <= kernel_atol, f"{name}: kernels move the logits {kernel_err} from the storage floor"
     assert k_agree >= kernel_agree, f"{name}: kernels agree with the storage floor on only {k_agree}"
     if not strict:

@@ -149,7 +149,7 @@ def test_launch_metadata_records_the_launched_kernels_resources(d):
                 128: "masked_attention32_kernel<D=128>"}[d]
     print(meta)
     assert meta["kernel_name"] == expected + " bf16"
-    assert 0 < meta["n_regs"] <= 512 and meta["n_spills"] == 0
+    assert 0 < meta["n_regs"] <= 512 and meta["n_spills"] * 4 == meta["private_segment_bytes"]
     assert meta["shared_memory_bytes"] > 0 and meta["threads"] in (128, 256)
     assert len(meta["asm_sha256"]["libsfl.so"]) == 64
     assert "not rocprof" in meta["source"]

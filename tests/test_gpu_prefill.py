@@ -104,20 +104,25 @@ def test_tiny_golden_bf16_forward_step_path(golden):
     assert err <= 2e-2
 
 
-def test_config2_prefill_then_decode_teacher_forced():
-    """100.3M bf16, batch 8: GEMM prefill of 512 tokens, then 64 teacher-forced decode positions.
+def format_floor(sd, cfg, seq, prompt, wide=False):
+    """The bf16-storage floor of a GEMM prefill of ``prompt`` tokens followed by decode steps:
+    bf16 weights and KV cache; bf16 GEMM inputs and probabilities over the prompt chunk only.
+    ``wide``: the same with float64-accumulated products (the drift yardstick)."""
+    cache = om.KVCacheOracle(om.round_weights(sd), cfg, seq.shape[0], seq.shape[1], kv_dtype=torch.bfloat16)
+    with om.accumulate_in(torch.float64 if wide else None):
+        return torch.cat([cache.step(seq[:, :prompt], act_dtype=torch.bfloat16), cache.step(seq[:, prompt:])],
+                         dim=1)
 
-    The floor models the formats the prefill stores: bf16 weights and KV cache,
-    and bf16 GEMM inputs (RMSNorm outputs, q, attention output, SwiGLU hidden)
-    for the 512 prompt positions; the decode positions keep fp32 inputs.
-    """
+
+def test_config2_prefill_then_decode_teacher_forced():
+    """100.3M bf16, batch 8: GEMM prefill of 512 tokens, then 64 teacher-forced decode positions."""
     cfg = load_model_config("scale-100m-s1024")
     sd = seeded_state_dict(cfg, 1337)
     seq = seeded_prompt(cfg.vocab_size, 8, 576, 2027)
     torch.set_num_threads(16)
     ref = om.KVCacheOracle(sd, cfg, 8, 576).step(seq)
-    cache = om.KVCacheOracle(om.round_weights(sd), cfg, 8, 576, kv_dtype=torch.bfloat16)
-    floor = torch.cat([cache.step(seq[:, :512], act_dtype=torch.bfloat16), cache.step(seq[:, 512:])], dim=1)
+    floor = format_floor(sd, cfg, seq, 512)
+    wide = format_floor(sd, cfg, seq[:2], 512, wide=True)
     model = gpu_model(cfg, sd)
     session = DecodeSession(model, 8, 576, record_logits=True)
     all_logits = session.prefill(seq[:, :512].cuda(), all_logits=True, forced=seq.cuda())
@@ -125,11 +130,105 @@ def test_config2_prefill_then_decode_teacher_forced():
     torch.cuda.synchronize()
     pre = all_logits.cpu()
     dec = session.logits[:, 512:575].float().cpu()
-    bf16_gate("config2 prefill (positions 0..511)", pre, ref[:, :512], floor[:, :512])
-    bf16_gate("config2 decode after prefill (positions 512..574)", dec, ref[:, 512:575], floor[:, 512:575])
+    bf16_gate("config2 prefill (positions 0..511)", pre, ref[:, :512], floor[:, :512],
+              envelope=(floor[:2, :512], wide[:, :512]))
+    bf16_gate("config2 decode after prefill (positions 512..574)", dec, ref[:, 512:575], floor[:, 512:575],
+              envelope=(floor[:2, 512:575], wide[:, 512:575]))
     # The decode head after prefill (fp32 inputs) equals the prefill's own last-position
     # logits (bf16 GEMM inputs) up to the rounding of the final norm's output.
     torch.testing.assert_close(session.logits[:, 511].float().cpu(), pre[:, 511], atol=2e-2, rtol=0)
+
+
+def _ulp_close(name, got, ref, max_frac, cancel=2 ** -17):
+    """bf16 results that differ only by rare 1-ulp rounding flips.
+
+    One ulp of the larger value, plus ``cancel`` times the tensor's largest
+    value for results formed by cancellation, where a difference in the
+    inputs can exceed an ulp of the result: RoPE's e*cos - o*sin near zero
+    (fp32 reassociation of its inputs), and an attention output near zero,
+    where one flipped bf16 probability moves sum(p v) / l by up to 2^-8 |v|.
+    """
+    got, ref = got.float().cpu(), ref.float().cpu()
+    diff = (got - ref).abs()
+    frac = (diff > 0).float().mean().item()
+    bound = 2 ** -7 * torch.maximum(got.abs(), ref.abs()) + cancel * ref.abs().max()
+    worst = (diff - bound).max().item()
+    print(f"{name}: {frac:.5f} of values differ, max-abs {diff.max().item():.3e}")
+    assert frac <= max_frac, f"{name}: {frac} of values differ"
+    assert worst <= 0, f"{name}: a difference exceeds one bf16 ulp"
+
+
+@pytest.mark.parametrize("config", ["scale-100m-s1024", "scale-324m-s4096"])
+def test_prefill_layer_stages_match_the_bf16_format_oracle(config):
+    """Each stage of one prefill layer, fed the GPU's own inputs, against the bf16-format oracle:
+    bf16 outputs equal up to rare 1-ulp flips (fp32 reassociation at a rounding boundary), fp32
+    residual updates to fp32 rounding. The attention matches only with its probabilities stored
+    in bf16, as the kernel stores them."""
+    cfg = load_model_config(config)
+    sd = seeded_state_dict(cfg, 1337)
+    sdr = om.round_weights(sd)
+    b, t = 2, 512
+    ids = seeded_prompt(cfg.vocab_size, b, t, 2027)
+    model = gpu_model(cfg, sd)
+    session = DecodeSession(model, b, t)
+    d, h, f = cfg.d_model, cfg.num_heads, cfg.d_ff
+    dk, m = d // h, b * t
+    x = torch.empty((m, d), device="cuda")
+    act = torch.empty((m, d), device="cuda", dtype=torch.bfloat16)
+    q = torch.empty((b, h, t, dk), device="cuda", dtype=torch.bfloat16)
+    attn = torch.empty((b, t, h, dk), device="cuda", dtype=torch.bfloat16)
+    hid = torch.empty((m, f), device="cuda", dtype=torch.bfloat16)
+    blk, kc, vc = model.layers[0], session.k_cache[0], session.v_cache[0]
+    gid = ids.cuda().view(-1)
+    st = _lib.stream_handle()
+    call = _lib.call
+    call("sfl_embed_rows", gid.data_ptr(), model.token_embeddings.weight.data_ptr(), x.data_ptr(), m, d, 1, st)
+    x0 = x.clone()
+    call("sfl_rmsnorm_rows", x.data_ptr(), blk.attn_norm.weight.data_ptr(), act.data_ptr(), m, d, 1, st)
+    act1 = act.clone()
+    call("sfl_gemm_qkv_rope", act.data_ptr(), session.wqkv[0].data_ptr(), m, t, d, h, session.cos.data_ptr(),
+         session.sin.data_ptr(), q.data_ptr(), kc.data_ptr(), vc.data_ptr(), session.cap, st)
+    from systems_for_llms_amd.attention import causal_prefill
+    causal_prefill(q, kc[:, :, :t], vc[:, :, :t], attn.transpose(1, 2))
+    call("sfl_gemm_bf16", attn.data_ptr(), blk.attn.output_proj.weight.data_ptr(), x.data_ptr(), m, d, d, 0, 1, st)
+    x1 = x.clone()
+    call("sfl_rmsnorm_rows", x.data_ptr(), blk.ffn_norm.weight.data_ptr(), act.data_ptr(), m, d, 1, st)
+    act2 = act.clone()
+    call("sfl_gemm_swiglu", act.data_ptr(), session.weights.w13()[0].data_ptr(), hid.data_ptr(), m, f, d, st)
+    call("sfl_gemm_bf16", hid.data_ptr(), blk.ffn.w2.weight.data_ptr(), x.data_ptr(), m, d, f, 0, 1, st)
+    torch.cuda.synchronize()
+
+    torch.set_num_threads(16)
+    bf, p = torch.bfloat16, "layers.0."
+    cos, sin = om.rope_tables(cfg.rope_theta, dk, cfg.context_length)
+    pos = torch.arange(t)
+    x0c = x0.cpu()
+    assert torch.equal(x0c, sdr["token_embeddings.weight"][ids].reshape(m, d))
+    _ulp_close("rmsnorm (attention input)", act1, om._round(om.rmsnorm(x0c, sdr[p + "attn_norm.weight"]), bf), 1e-3)
+    a1 = act1.float().cpu().view(b, t, d)
+
+    def proj(name):
+        return om._split_heads(om._linear(a1, sdr[p + f"attn.{name}_proj.weight"]), h)
+    _ulp_close("q (RoPE)", q, om._round(om.rope(proj("q"), cos, sin, pos), bf), 2e-3)
+    _ulp_close("k cache (RoPE)", kc[:, :, :t], om._round(om.rope(proj("k"), cos, sin, pos), bf), 2e-3)
+    _ulp_close("v cache", vc[:, :, :t], om._round(proj("v"), bf), 2e-3)
+    qg, kg, vg = q.float().cpu(), kc[:, :, :t].float().cpu(), vc[:, :, :t].float().cpu()
+    mask = torch.tril(torch.ones(t, t, dtype=torch.bool))
+    stored = om._round(om._merge_heads(om.attention_core(qg, kg, vg, mask, bf)), bf)
+    _ulp_close("attention (bf16 probabilities)", attn.view(b, t, d), stored, 2e-3, cancel=2 ** -8)
+    exact_p = om._round(om._merge_heads(om.attention_core(qg, kg, vg, mask)), bf)
+    moved = (attn.view(b, t, d).float().cpu() != exact_p).float().mean().item()
+    print(f"attention vs exact probabilities: {moved:.4f} of values differ")
+    assert moved > 0.05  # the stored-probability format is what the kernel computes
+    x1_ref = x0c + om._linear(attn.float().cpu().view(m, d), sdr[p + "attn.output_proj.weight"])
+    torch.testing.assert_close(x1.cpu(), x1_ref, atol=1e-5, rtol=1e-5)
+    _ulp_close("rmsnorm (SwiGLU input)", act2, om._round(om.rmsnorm(x1.cpu(), sdr[p + "ffn_norm.weight"]), bf), 1e-3)
+    a2 = act2.float().cpu()
+    g1 = om._linear(a2, sdr[p + "ffn.w1.weight"])
+    _ulp_close("SwiGLU hidden", hid, om._round(g1 * torch.sigmoid(g1) * om._linear(a2, sdr[p + "ffn.w3.weight"]), bf),
+               2e-3)
+    x2_ref = x1.cpu() + om._linear(hid.float().cpu(), sdr[p + "ffn.w2.weight"])
+    torch.testing.assert_close(x.cpu(), x2_ref, atol=1e-5, rtol=1e-5)
 
 
 def test_generate_bf16_uses_prefill_and_matches_step_path():

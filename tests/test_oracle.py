@@ -97,7 +97,9 @@ def test_storage_format_floors_are_consistent(golden):
     pieces = [cache.step(ids[:, :7], act_dtype=bf), cache.step(ids[:, 7:], act_dtype=bf)]
     torch.testing.assert_close(torch.cat(pieces, dim=1), full, atol=2e-6, rtol=2e-5)
     plain = om.forward(sd, cfg, ids)
-    assert torch.equal(om.forward(sd, cfg, ids, kv_dtype=torch.float32, act_dtype=torch.float32), plain)
+    assert torch.equal(om.forward(sd, cfg, ids, kv_dtype=torch.float32), plain)
+    # fp32 GEMM inputs and probabilities: only the tiled softmax's reassociation remains.
+    torch.testing.assert_close(om.forward(sd, cfg, ids, act_dtype=torch.float32), plain, atol=2e-6, rtol=2e-5)
     # Each rounding point is applied: skipping any one of them changes the floor (per layer:
     # attention input, q, attention output, SwiGLU input, hidden; then the final norm).
     base = om.forward(sd, cfg, ids, act_dtype=bf)
@@ -122,6 +124,44 @@ def test_storage_format_floors_are_consistent(golden):
     mixed = torch.cat([cache.step(ids[:, :7], act_dtype=bf), cache.step(ids[:, 7:])], dim=1)
     torch.testing.assert_close(mixed[:, :7], full[:, :7], atol=2e-6, rtol=2e-5)
     assert not torch.equal(mixed[:, 7:], full[:, 7:])
+
+
+def test_stored_probability_attention_is_softmax_up_to_its_rounding():
+    """The prefill floor's tiled lazy-maximum attention: with fp32 probabilities it is exact
+    softmax attention (the running maximum only bounds the exponents), also when scores jump
+    by far more than the slack between tiles; empty rows give zeros; bf16 probabilities move
+    the output by at most their relative rounding (2^-8 of the largest |v|)."""
+    g = torch.Generator().manual_seed(12)
+    n, d = 300, 64
+    q, k, v = (torch.randn((2, 3, n, d), generator=g) for _ in range(3))
+    k[..., 130:, :] *= 6.0  # later tiles: scores far above the first tile's maximum
+    mask = torch.tril(torch.ones(n, n, dtype=torch.bool))
+    mask[70:90] = False  # rows with no admissible key
+    exact = om.attention_core(q, k, v, mask)
+    exact[..., 70:90, :] = 0.0  # attention_core gives NaN rows there; the floor's convention is zeros
+    stored = om._attention_stored_probabilities(q, k, v, mask, torch.float32)
+    torch.testing.assert_close(stored, exact, atol=2e-6, rtol=2e-5)
+    assert torch.equal(stored[..., 70:90, :], torch.zeros_like(stored[..., 70:90, :]))
+    rounded = om._attention_stored_probabilities(q, k, v, mask, torch.bfloat16)
+    err = (rounded - exact).abs().max().item()
+    assert 0 < err <= 2 ** -8 * v.abs().max().item()
+
+
+def test_wide_accumulation_is_a_closer_restatement(golden):
+    """accumulate_in(float64): the fp32 model with float64 products lies between the plain fp32
+    oracle and a float64 forward (closer to the latter), and the setting is restored on exit."""
+    meta, arrays = golden
+    cfg = _tiny(meta)
+    sd = seeded_state_dict(cfg, meta["tiny"]["seed"])
+    ids = torch.from_numpy(arrays["tiny_ids"])
+    plain = om.forward(sd, cfg, ids)
+    exact = om.forward(sd, cfg, ids, dtype=torch.float64)
+    with om.accumulate_in(torch.float64):
+        wide = om.forward(sd, cfg, ids)
+    assert wide.dtype == torch.float32 and not torch.equal(wide, plain)
+    assert (wide.double() - exact).abs().max() < (plain.double() - exact).abs().max()
+    torch.testing.assert_close(wide, plain, atol=2e-6, rtol=2e-5)
+    assert torch.equal(om.forward(sd, cfg, ids), plain)
 
 
 @pytest.mark.slow
