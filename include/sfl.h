@@ -84,6 +84,27 @@ int sfl_decode_attention(const void* q, const void* k, const void* v, const int3
                          void* stream);
 
 /*
+ * sfl_decode_attention without caller scratch, for callers that cannot
+ * allocate (code under HIP graph capture, serving loops, harnesses that forbid
+ * hipMalloc). No counterpart in the reference: its prepare() allocates the
+ * split scratch (attention_lab/cuda_decode/kernel.py:107-111). The split
+ * partials live in a static device buffer of
+ * sfl_decode_attention_static_scratch_bytes() (16 MiB), one per GPU, held
+ * until the process ends; a call needing more -- 2*align256(B*Hq*splits*4) +
+ * align256(B*Hq*splits*D*4) bytes -- is rejected before any launch. Every call
+ * on a GPU shares that GPU's buffer, so calls that overlap on one GPU (two
+ * streams, two threads) race; nothing in it needs clearing between calls
+ * (the merge reads only the partials its own call wrote). The current HIP
+ * device must be the one `stream` belongs to. Arguments, results and errors
+ * are otherwise those of sfl_decode_attention.
+ */
+int sfl_decode_attention_static(const void* q, const void* k, const void* v, const int32_t* lengths,
+                                void* out, int batch, int q_heads, int kv_heads, int capacity,
+                                int head_dim, int splits, float scale, int kv_dtype, int q_dtype,
+                                int out_dtype, void* stream);
+long sfl_decode_attention_static_scratch_bytes(void);
+
+/*
  * Decode attention fused with the output projection and residual add:
  *   x[b] += concat_h(attention(q[b, h], k[b, h], v[b, h])) @ w_out^T
  * for multi-head attention (Hq == Hkv == heads) with one split. Replaces

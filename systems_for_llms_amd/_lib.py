@@ -23,6 +23,9 @@ P = c_void_p
 SIGNATURES: dict[str, list] = {
     "sfl_decode_attention": [P, P, P, P, P, P, P, P, c_int, c_int, c_int, c_int, c_int, c_int,
                              c_float, c_int, c_int, c_int, P],
+    "sfl_decode_attention_static": [P, P, P, P, P, c_int, c_int, c_int, c_int, c_int, c_int, c_float, c_int,
+                                    c_int, c_int, P],
+    "sfl_decode_attention_static_scratch_bytes": [],
     "sfl_decode_attention_out_proj": [P, P, P, P, P, P, c_int, c_int, c_int, c_int, c_float, c_int, P],
     "sfl_packed_gemv_elems": [c_int, c_int],
     "sfl_pack_gemv_weights": [P, P, c_int, c_int, c_int, P],
@@ -77,6 +80,7 @@ def lib() -> ctypes.CDLL:
             fn.argtypes = args
             fn.restype = c_int
         handle.sfl_packed_gemv_elems.restype = c_long
+        handle.sfl_decode_attention_static_scratch_bytes.restype = c_long
         _LIB = handle
     return _LIB
 

@@ -14,9 +14,18 @@
 // softmax over the keys it loads, so the inner loop needs only the short
 // intra-row dot-product reduction; the slots are merged once at the end of
 // the chunk with xor shuffles. Max and sum are kept in base-2 units.
+#include <mutex>
+
 #include "act_format.hpp"
 #include "attn_mfma.hpp"
 #include "lds_dma.hpp"
+
+// Split scratch of sfl_decode_attention_static: one copy per GPU, held from
+// module load until the process ends. In host code the name is only a stand-in
+// for the symbol; every use goes through the device address that
+// hipGetSymbolAddress returns for the current device (static_scratch below).
+constexpr long kStaticScratchBytes = 16L << 20;
+static __device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
 
 namespace sfl {
 namespace {
@@ -783,6 +792,73 @@ extern "C" int sfl_decode_attention_out_proj(const float* q, const void* k, cons
   c.x = x;
   c.d_model = heads * head_dim;
   return dtype == SFL_DTYPE_BF16 ? proj_dims<bf16_t>(c) : proj_dims<float>(c);
+}
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's copy of `scratch`, looked up once per device (with that
+// device current) and kept.
+int static_scratch(void** out) {
+  int device = -1;
+  hipError_t err = hipGetDevice(&device);
+  if (err != hipSuccess)
+    return sfl::set_error(SFL_ERR_HIP, "decode_attention_static: hipGetDevice: %s", hipGetErrorString(err));
+  if (device < 0 || device >= kMaxDevices)
+    return sfl::set_error(SFL_ERR_UNSUPPORTED, "decode_attention_static: device %d beyond the %d supported",
+                          device, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_ptr[device]) {
+    void* ptr = nullptr;
+    err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || !ptr)
+      return sfl::set_error(SFL_ERR_HIP, "decode_attention_static: hipGetSymbolAddress: %s",
+                            hipGetErrorString(err));
+    g_scratch_ptr[device] = ptr;
+  }
+  *out = g_scratch_ptr[device];
+  return SFL_OK;
+}
+
+long align256(long bytes) { return (bytes + 255) / 256 * 256; }
+
+}  // namespace
+
+extern "C" long sfl_decode_attention_static_scratch_bytes(void) { return kStaticScratchBytes; }
+
+extern "C" int sfl_decode_attention_static(const void* q, const void* k, const void* v,
+                                           const int32_t* lengths, void* out, int batch, int q_heads,
+                                           int kv_heads, int capacity, int head_dim, int splits,
+                                           float scale, int kv_dtype, int q_dtype, int out_dtype,
+                                           void* stream) {
+  using namespace sfl;
+  const char* what = "decode_attention_static";
+  if (!q || !k || !v || !lengths || !out) return set_error(SFL_ERR_INVALID, "%s: null pointer argument", what);
+  if (batch <= 0 || q_heads <= 0 || kv_heads <= 0 || capacity <= 0)
+    return set_error(SFL_ERR_INVALID, "%s: batch, heads and capacity must be positive", what);
+  if (splits < 1 || splits > 1024) return set_error(SFL_ERR_INVALID, "%s: splits must be in [1, 1024]", what);
+  if (head_dim != 16 && head_dim != 32 && head_dim != 64 && head_dim != 128)
+    return set_error(SFL_ERR_UNSUPPORTED, "%s: unsupported head dim %d", what, head_dim);
+  // Partials as sfl_decode_attention takes them: max and sum [B, Hq, splits],
+  // numerator [B, Hq, splits, D], fp32, each 256-byte aligned in the buffer.
+  const long parts = long(batch) * q_heads * splits;
+  const long max_bytes = align256(parts * 4), out_bytes = align256(parts * head_dim * 4);
+  const long need = 2 * max_bytes + out_bytes;
+  if (need > kStaticScratchBytes)
+    return set_error(SFL_ERR_INVALID,
+                     "%s: batch*q_heads*splits*(head_dim+2)*4 = %ld bytes of split scratch exceed the %ld-byte "
+                     "static buffer; use fewer splits or sfl_decode_attention with caller scratch",
+                     what, parts * (head_dim + 2) * 4, kStaticScratchBytes);
+  void* base = nullptr;
+  if (int rc = static_scratch(&base)) return rc;
+  unsigned char* bytes = static_cast<unsigned char*>(base);
+  return sfl_decode_attention(q, k, v, lengths, reinterpret_cast<float*>(bytes),
+                              reinterpret_cast<float*>(bytes + max_bytes),
+                              reinterpret_cast<float*>(bytes + 2 * max_bytes), out, batch, q_heads, kv_heads,
+                              capacity, head_dim, splits, scale, kv_dtype, q_dtype, out_dtype, stream);
 }
 
 extern "C" int sfl_decode_attention(const void* q, const void* k, const void* v,
