@@ -295,6 +295,73 @@ def profile_target_gqa(reps: int = 40) -> int:
         f"{us:.1f} us per call (events, eager), K+V {kv} bytes = {kv / us / 1e3:.0f} GB/s")
     return 0
 
+def profile_target_masked(reps: int = 20) -> int:
+    """Counter-collection target: the masked prefill attention at BASELINE config 5 and at the
+    prefill's causal 16 x 16 x 3072 shape, ``reps`` eager calls each (event-timed per shape)."""
+    import torch
+
+    from systems_for_llms_amd.attention import attention
+    from systems_for_llms_amd.masks import MaskSpec, compile_mask
+
+    g = torch.Generator(device="cuda").manual_seed(5)
+    for name, (b, h, n), spec, impl in (
+            ("config 5", (4, 16, 4096), MaskSpec(causal=True, window_left=1023, global_prefix=256), "csr"),
+            ("causal 16x16x3072", (16, 16, 3072), MaskSpec(causal=True), "interval")):
+        q, k, v = (torch.randn((b, h, n, 64), device="cuda", generator=g, dtype=torch.bfloat16) for _ in range(3))
+        sched = compile_mask(n, spec, 64, 64)
+        out = torch.empty_like(q)
+        call = lambda: attention(q, k, v, sched, spec, implementation=impl, out=out)  # noqa: E731
+        call()
+        torch.cuda.synchronize()
+        log(f"profile target: {reps} masked attention calls, {name}: {time_events(call, reps) * 1000:.1f} us each")
+        del q, k, v, out
+    return 0
+
+
+def profile_target_gemm(reps: int = 10) -> int:
+    """Counter-collection target: the prefill GEMMs of the 324M model at M = 16 x 3072 tokens
+    (q/k/v + RoPE + cache write, output_proj, w1/w3 + SwiGLU, w2, lm_head), ``reps`` calls each."""
+    import torch
+
+    from systems_for_llms_amd import _lib
+
+    m, d, f, v, h, t = BATCH * PROMPT, 1024, 2752, 10000, 16, PROMPT
+    g = torch.Generator(device="cuda").manual_seed(3)
+    act = torch.randn((m, d), device="cuda", generator=g, dtype=torch.bfloat16)
+    hid = torch.randn((m, f), device="cuda", generator=g, dtype=torch.bfloat16)
+    w = {name: torch.randn(shape, device="cuda", generator=g, dtype=torch.bfloat16) * 0.02
+         for name, shape in (("qkv", (3 * d, d)), ("o", (d, d)), ("w13", (2 * f, d)), ("w2", (d, f)),
+                             ("head", (v, d)))}
+    x = torch.zeros((m, d), device="cuda")
+    logits = torch.empty((m, v), device="cuda")
+    q = torch.empty((BATCH, h, t, d // h), device="cuda", dtype=torch.bfloat16)
+    kc = torch.empty((BATCH, h, CONTEXT, d // h), device="cuda", dtype=torch.bfloat16)
+    vc = torch.empty_like(kc)
+    from systems_for_llms_amd.model import rope_tables
+    cos, sin = (c.cuda() for c in rope_tables(10000.0, d // h, CONTEXT))
+    st = _lib.stream_handle()
+    calls = {
+        "q/k/v": lambda: _lib.call("sfl_gemm_qkv_rope", act.data_ptr(), w["qkv"].data_ptr(), m, t, d, h, cos.data_ptr(),
+                                   sin.data_ptr(), q.data_ptr(), kc.data_ptr(), vc.data_ptr(), CONTEXT, st),
+        "output_proj": lambda: _lib.call("sfl_gemm_bf16", act.data_ptr(), w["o"].data_ptr(), x.data_ptr(), m, d, d,
+                                         0, 1, st),
+        "w1/w3": lambda: _lib.call("sfl_gemm_swiglu", act.data_ptr(), w["w13"].data_ptr(), hid.data_ptr(), m, f, d,
+                                   st),
+        "w2": lambda: _lib.call("sfl_gemm_bf16", hid.data_ptr(), w["w2"].data_ptr(), x.data_ptr(), m, d, f, 0, 1, st),
+        "lm_head": lambda: _lib.call("sfl_gemm_bf16", act.data_ptr(), w["head"].data_ptr(), logits.data_ptr(), m, v,
+                                     d, 0, 0, st),
+    }
+    flops = {"q/k/v": 2 * m * 3 * d * d, "output_proj": 2 * m * d * d, "w1/w3": 2 * m * 2 * f * d,
+             "w2": 2 * m * d * f, "lm_head": 2 * m * v * d}
+    for name, call in calls.items():
+        call()
+        torch.cuda.synchronize()
+        us = time_events(call, reps) * 1000
+        log(f"profile target: {reps} GEMM calls, {name}: {us:.1f} us each, "
+            f"{flops[name] / us / 1e6:.0f} TFLOP/s")
+    return 0
+
+
 def main() -> int:
     parser = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     parser.add_argument("--gpus", type=int, default=1)
@@ -304,13 +371,17 @@ def main() -> int:
     parser.add_argument("--no-reference-shapes", action="store_true",
                         help="skip timing the reference's published attention shapes")
     parser.add_argument("--attention-reps", type=int, default=50)
-    parser.add_argument("--profile-target", choices=["attention", "gqa"], default=None,
-                        help="run only a profiling target (profile_target_attention, profile_target_gqa)")
+    parser.add_argument("--profile-target", choices=["attention", "gqa", "masked", "gemm"], default=None,
+                        help="run only a profiling target (profile_target_attention, _gqa, _masked, _gemm)")
     args = parser.parse_args()
     if args.profile_target == "attention":
         return profile_target_attention()
     if args.profile_target == "gqa":
         return profile_target_gqa()
+    if args.profile_target == "masked":
+        return profile_target_masked()
+    if args.profile_target == "gemm":
+        return profile_target_gemm()
     if args.gpus != 1:
         print("bench.py measures one GPU: every box in this build has a single MI355X and the decode "
               "path is not sharded across GPUs (see DESIGN.md for how it would shard)", file=sys.stderr)

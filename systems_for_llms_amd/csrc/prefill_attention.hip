@@ -643,14 +643,17 @@ __device__ __forceinline__ KeyRanges key_ranges(const MaskArgs& m, int q, int n,
 // probabilities with dot2 (the sum of exactly the values the P V product
 // weights), kept per lane and added with the partner's at the end.
 // One key tile of masked_attention32_kernel for this wave: S^T = K Q^T from the
-// swizzled K tile, the online softmax (masked when kMask), and O^T += V^T P^T.
-// Instantiated separately for full and masked tiles so each is straight-line
-// code.
-template <typename T, bool kMask, int D>
+// swizzled K tile, the online softmax (with the token mask when `masked`), and
+// O^T += V^T P^T. One code path for full and masked tiles, the mask a
+// wave-uniform branch on the scores alone: with two instantiations of the
+// whole tile the compiler kept the O accumulators of one in a second register
+// set and copied them every tile (33 moves, and spills at D = 128).
+template <typename T, int D>
 __device__ __forceinline__ void attn32_tile(const AttnArgs& a, const uint4 (&kt)[BK][D / 8],
                                             const uint4 (&vt)[BK][D / 8], const u32x4 (&qreg)[D / 16],
                                             f32x16 (&oacc)[D / 32], float& m_run, float& l_run, int c, int h,
-                                            int qrow, int k0, bool full, const unsigned (&vlane)[D / 32]) {
+                                            int qrow, int k0, bool full, const unsigned (&vlane)[D / 32],
+                                            bool masked) {
   const int n = a.n;
   f32x16 sacc[2];
 #pragma unroll
@@ -663,7 +666,7 @@ __device__ __forceinline__ void attn32_tile(const AttnArgs& a, const uint4 (&kt)
       sacc[kb2] = mfma32<T>(u32x4{kr.x, kr.y, kr.z, kr.w}, qreg[ks], sacc[kb2]);
     }
   }
-  if constexpr (kMask) {
+  if (masked) {  // wave-uniform: full tiles skip the token mask
     if (!a.m.docs) {
       const KeyRanges kr = key_ranges(a.m, qrow, n, k0 + 4 * h, full);
 #pragma unroll
@@ -707,8 +710,12 @@ __device__ __forceinline__ void attn32_tile(const AttnArgs& a, const uint4 (&kt)
     const float m_new = grow ? mx * cs : m_run;
     alpha = grow ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.f;  // 0 for the first admissible tile
     m_run = m_new;
+    // In place (tied operands): the accumulators keep their registers on both
+    // sides of this rare branch, so the common path needs no copies of them.
 #pragma unroll
-    for (int t = 0; t < D / 32; ++t) oacc[t] *= alpha;
+    for (int t = 0; t < D / 32; ++t)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) asm volatile("v_mul_f32 %0, %0, %1" : "+v"(oacc[t][j]) : "v"(alpha));
   }
   const float ms = m_run == -INFINITY ? 0.f : m_run;
   u32x4 pop[4];
@@ -927,10 +934,8 @@ void masked_attention32_kernel(AttnArgs a) {
     const int k0 = cur.kb * BK;
     const bool full = (half ? cur.full[1] : cur.full[0]) && a.s.use_full;
     if (half ? cur.in[1] : cur.in[0]) {
-      if (full && k0 + BK <= n)
-        attn32_tile<T, false, D>(a, k_s[buf], v_s[buf], qreg, oacc, m_run, l_run, c, h, qrow, k0, full, vlane);
-      else
-        attn32_tile<T, true, D>(a, k_s[buf], v_s[buf], qreg, oacc, m_run, l_run, c, h, qrow, k0, full, vlane);
+      attn32_tile<T, D>(a, k_s[buf], v_s[buf], qreg, oacc, m_run, l_run, c, h, qrow, k0, full, vlane,
+                        !(full && k0 + BK <= n));
     }
     __builtin_amdgcn_s_waitcnt(sfl_vmcnt(0));  // the next K and V tiles have landed
     __syncthreads();

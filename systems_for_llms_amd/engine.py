@@ -167,49 +167,56 @@ class DecodeSession:
 
     # -- launch plan --------------------------------------------------------
     def _plan(self):
-        """The ctypes calls of one step, with every argument but the stream bound."""
+        """The ctypes calls of one step over every row, in launch order."""
+        bufs = {"attn": self.attn, "hidden": self.hidden, "pmax": self.pmax, "psum": self.psum,
+                "pout": self.pout, "best_val": self.best_val, "best_idx": self.best_idx}
+        layers, tail = self._plan_rows(0, self.batch, bufs, self.splits, self.fused_out_proj)
+        return [call for layer in layers for call in layer] + tail
+
+    def _plan_rows(self, r0, nb, bufs, splits, fused):
+        """One step's ctypes calls (every argument but the stream bound) for rows
+        r0 .. r0 + nb - 1: ``(layers, tail)``, where ``layers[i]`` lists layer i's
+        launches with the attention launch second, and ``tail`` is the lm_head and
+        the token step."""
         lib = _lib.lib()
         d, h, dk, f, v, cap, code = self.d, self.heads, self.dk, self.d_ff, self.vocab, self.cap, self.code
         m = self.model
-        calls = []
         scale = float(dk) ** -0.5
-        rows = self.batch  # every GEMV launch covers all rows, 16 per workgroup
+        x, q = self.x[r0:].data_ptr(), self.q[r0:].data_ptr()
+        pos, lengths = self.pos[r0:].data_ptr(), self.lengths[r0:].data_ptr()
+        attn, hidden = bufs["attn"].data_ptr(), bufs["hidden"].data_ptr()
+        layers = []
         for layer, blk in enumerate(m.layers):
-            kc, vc = self.k_cache[layer], self.v_cache[layer]
-            calls.append((lib.sfl_rmsnorm_qkv_rope_append, (
-                self.x.data_ptr(), blk.attn_norm.weight.data_ptr(), self.p_qkv[layer].data_ptr(),
-                self.cos.data_ptr(), self.sin.data_ptr(), self.pos.data_ptr(),
-                self.q.data_ptr(), kc.data_ptr(), vc.data_ptr(), rows, d, h, cap, code)))
-            if self.fused_out_proj:
+            kc, vc = self.k_cache[layer, r0:].data_ptr(), self.v_cache[layer, r0:].data_ptr()
+            calls = [(lib.sfl_rmsnorm_qkv_rope_append, (
+                x, blk.attn_norm.weight.data_ptr(), self.p_qkv[layer].data_ptr(), self.cos.data_ptr(),
+                self.sin.data_ptr(), pos, q, kc, vc, nb, d, h, cap, code))]
+            if fused:
                 calls.append((lib.sfl_decode_attention_out_proj, (
-                    self.q.data_ptr(), kc.data_ptr(), vc.data_ptr(), self.lengths.data_ptr(),
-                    self.p_out[layer].data_ptr(), self.x.data_ptr(), self.batch, h, cap, dk, scale, code)))
+                    q, kc, vc, lengths, self.p_out[layer].data_ptr(), x, nb, h, cap, dk, scale, code)))
             else:
                 calls.append((lib.sfl_decode_attention, (
-                    self.q.data_ptr(), kc.data_ptr(), vc.data_ptr(), self.lengths.data_ptr(),
-                    self.pmax.data_ptr(), self.psum.data_ptr(), self.pout.data_ptr(), self.attn.data_ptr(),
-                    self.batch, h, h, cap, dk, self.splits, scale, code, _lib.DTYPE_CODES[torch.float32],
+                    q, kc, vc, lengths, bufs["pmax"].data_ptr(), bufs["psum"].data_ptr(), bufs["pout"].data_ptr(),
+                    attn, nb, h, h, cap, dk, splits, scale, code, _lib.DTYPE_CODES[torch.float32],
                     self.act_code)))
                 calls.append((lib.sfl_linear_residual, (
-                    self.attn.data_ptr(), self.p_out[layer].data_ptr(), self.x.data_ptr(), rows, d, d,
-                    self.ksplit, code)))
+                    attn, self.p_out[layer].data_ptr(), x, nb, d, d, self.ksplit, code)))
             calls.append((lib.sfl_rmsnorm_swiglu, (
-                self.x.data_ptr(), blk.ffn_norm.weight.data_ptr(), self.p_w1[layer].data_ptr(),
-                self.p_w3[layer].data_ptr(), self.hidden.data_ptr(), rows, d, f, code)))
-            calls.append((lib.sfl_linear_residual, (
-                self.hidden.data_ptr(), self.p_w2[layer].data_ptr(), self.x.data_ptr(), rows, d, f,
-                self.ksplit, code)))
-        logits = self.logits.data_ptr() if self.logits is not None else None
-        calls.append((lib.sfl_rmsnorm_lm_head, (
-            self.x.data_ptr(), m.ln_final.weight.data_ptr(), self.p_head.data_ptr(),
-            logits, cap * v, self.pos.data_ptr(), v, self.best_val.data_ptr(),
-            self.best_idx.data_ptr(), self.batch, rows, d, v, code)))
-        calls.append((lib.sfl_next_token, (
-            self.best_val.data_ptr(), self.best_idx.data_ptr(), self.tiles, self.tokens.data_ptr(),
-            self.predicted.data_ptr(), cap, self.prompt_len.data_ptr(), self.pos.data_ptr(),
-            self.lengths.data_ptr(), m.token_embeddings.weight.data_ptr(), self.x.data_ptr(),
-            self.batch, d, cap, code)))
-        return calls
+                x, blk.ffn_norm.weight.data_ptr(), self.p_w1[layer].data_ptr(), self.p_w3[layer].data_ptr(),
+                hidden, nb, d, f, code)))
+            calls.append((lib.sfl_linear_residual, (hidden, self.p_w2[layer].data_ptr(), x, nb, d, f,
+                                                    self.ksplit, code)))
+            layers.append(calls)
+        logits = self.logits[r0:].data_ptr() if self.logits is not None else None
+        tail = [(lib.sfl_rmsnorm_lm_head, (
+                    x, m.ln_final.weight.data_ptr(), self.p_head.data_ptr(), logits, cap * v, pos, v,
+                    bufs["best_val"].data_ptr(), bufs["best_idx"].data_ptr(), nb, nb, d, v, code)),
+                (lib.sfl_next_token, (
+                    bufs["best_val"].data_ptr(), bufs["best_idx"].data_ptr(), self.tiles,
+                    self.tokens[r0:].data_ptr(), self.predicted[r0:].data_ptr(), cap,
+                    self.prompt_len[r0:].data_ptr(), pos, lengths, m.token_embeddings.weight.data_ptr(), x,
+                    nb, d, cap, code))]
+        return layers, tail
 
     # -- state --------------------------------------------------------------
     @torch.no_grad()
@@ -346,8 +353,11 @@ class DecodeSession:
         self._launch()
 
     def _launch(self) -> None:
+        self._launch_calls(self._calls)
+
+    def _launch_calls(self, calls) -> None:
         stream = _lib.stream_handle(self.device)
-        for fn, args in self._calls:
+        for fn, args in calls:
             status = fn(*args, stream)
             if status != 0:
                 raise RuntimeError(f"{fn.__name__} failed ({status}): "
