@@ -176,7 +176,7 @@ class DecodeSession:
     def _plan_rows(self, r0, nb, bufs, splits, fused):
         """One step's ctypes calls (every argument but the stream bound) for rows
         r0 .. r0 + nb - 1: ``(layers, tail)``, where ``layers[i]`` lists layer i's
-        launches with the attention launch second, and ``tail`` is the lm_head and
+        launches, and ``tail`` is the lm_head and
         the token step."""
         lib = _lib.lib()
         d, h, dk, f, v, cap, code = self.d, self.heads, self.dk, self.d_ff, self.vocab, self.cap, self.code
