@@ -283,7 +283,8 @@ typedef struct {
  * launch_metadata at :326-328). Needs a HIP device; launches nothing.
  */
 int sfl_masked_attention_kernel_info(int head_dim, int dtype, int n, long k_row_stride,
-                                     long v_row_stride, sfl_kernel_info* info);
+                                     long v_row_stride, int causal, int window_left,
+                                     int window_right, int global_prefix, sfl_kernel_info* info);
 
 /* ---- prefill (bf16 weights) -------------------------------------------------
  * C^T = W A^T on bf16 MFMAs; A [M, K] bf16 row-major (one row per token),

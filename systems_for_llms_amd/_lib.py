@@ -40,7 +40,7 @@ SIGNATURES: dict[str, list] = {
                              POINTER(c_long), POINTER(c_long), c_float, c_int, c_int, c_int, c_int, P,
                              c_int, P, P, P, c_int, c_int, P],
     "sfl_masked_attention_block": [],
-    "sfl_masked_attention_kernel_info": [c_int, c_int, c_int, c_long, c_long, P],
+    "sfl_masked_attention_kernel_info": [c_int, c_int, c_int, c_long, c_long, c_int, c_int, c_int, c_int, P],
     "sfl_gemm_bf16": [P, P, P, c_int, c_int, c_int, c_int, c_int, P],
     "sfl_gemm_qkv_rope": [P, P, c_int, c_int, c_int, c_int, P, P, P, P, P, c_int, P],
     "sfl_gemm_swiglu": [P, P, P, c_int, c_int, c_int, P],
@@ -105,11 +105,13 @@ def pack_gemv(w: torch.Tensor) -> torch.Tensor:
 
 
 def masked_kernel_info(head_dim: int, dtype: torch.dtype, n: int, k_row_stride: int,
-                       v_row_stride: int) -> KernelInfo:
-    """Resource data of the kernel ``sfl_masked_attention`` launches for these shapes."""
+                       v_row_stride: int, causal: bool = True, window_left: int = -1, window_right: int = -1,
+                       global_prefix: int = 0) -> KernelInfo:
+    """Resource data of the kernel ``sfl_masked_attention`` launches for these shapes and mask
+    (windows < 0: unbounded)."""
     info = KernelInfo()
     call("sfl_masked_attention_kernel_info", head_dim, dtype_code(dtype), n, k_row_stride, v_row_stride,
-         ctypes.addressof(info))
+         int(causal), window_left, window_right, global_prefix, ctypes.addressof(info))
     return info
 
 

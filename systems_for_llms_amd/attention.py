@@ -194,14 +194,17 @@ def attention(q, k, v, schedule, spec, document_ids=None, num_warps=4, num_stage
         -1 if spec.window_right is None else spec.window_right, spec.global_prefix or 0, docs_gpu,
         rows, cols, fulls, use_full_blocks)
     if launch_metadata is not None:
-        _record_launch_metadata(q, k, v, implementation, launch_metadata)
+        _record_launch_metadata(q, k, v, spec, implementation, launch_metadata)
     return (out, lse) if return_lse else out
 
 
-def _record_launch_metadata(q, k, v, implementation, destination):
+def _record_launch_metadata(q, k, v, spec, implementation, destination):
     """Compiler resource data of the kernel this call launched (``triton_attention.py:39-57``
     records the same fields from Triton's CompiledKernel), never a profiler measurement."""
-    info = _lib.masked_kernel_info(q.shape[-1], q.dtype, q.shape[2], k.stride(2), v.stride(2))
+    info = _lib.masked_kernel_info(
+        q.shape[-1], q.dtype, q.shape[2], k.stride(2), v.stride(2), bool(spec.causal),
+        -1 if spec.window_left is None else spec.window_left,
+        -1 if spec.window_right is None else spec.window_right, spec.global_prefix or 0)
     destination.update({
         "kernel_name": info.name.decode(),
         "n_regs": info.registers,

@@ -19,6 +19,7 @@
 // operand is exactly the probabilities the lane already holds (the product is
 // a sum over keys, so any order both operands share is exact), and V^T rows
 // come from LDS as 8-byte runs.
+#include <algorithm>
 #include <climits>
 #include <stdio.h>
 
@@ -816,6 +817,15 @@ struct MergedTile {
   int kb;
   bool in[2], full[2];
 };
+__device__ __forceinline__ MergedTile next_tile(const AttnArgs&, TileRow (&rows)[1]) {
+  MergedTile t;
+  t.kb = rows[0].peek(t.full[0]);
+  t.in[0] = t.kb != INT_MAX;
+  t.in[1] = false;
+  t.full[1] = false;
+  rows[0].i += t.in[0];
+  return t;
+}
 __device__ __forceinline__ MergedTile next_tile(const AttnArgs& a, TileRow (&rows)[2]) {
   MergedTile t;
   const int c0 = rows[0].peek(t.full[0]);
@@ -842,10 +852,12 @@ constexpr int kA32Waves = 4;
 // 2 waves per SIMD), 8 k-steps per score block and 4 dim tiles of O.
 template <int D> constexpr int attn32_waves_per_eu() { return D == 64 ? 3 : 2; }
 
-template <typename T, int D>
-__global__ __launch_bounds__(kA32Waves * kWave) __attribute__((amdgpu_waves_per_eu(attn32_waves_per_eu<D>())))
+template <typename T, int D, int NW>
+__global__ __launch_bounds__(NW * kWave) __attribute__((amdgpu_waves_per_eu(attn32_waves_per_eu<D>())))
 void masked_attention32_kernel(AttnArgs a) {
-  constexpr int QB = 2 * BQ;
+  static_assert(NW == 2 || NW == 4, "one or two 64-query rows per workgroup");
+  constexpr int NR = NW / 2;     // 64-query schedule rows per workgroup
+  constexpr int QB = NR * BQ;
   constexpr int SL = D / 8;      // 16-byte slots per K/V row
   constexpr int RPL = 64 / SL;   // rows one 1 KB load moves
   __shared__ __align__(16) uint4 k_s[2][BK][SL];  // [key][16-byte slot s at s ^ k_swizzle<D>(key)]
@@ -887,9 +899,9 @@ void masked_attention32_kernel(AttnArgs a) {
 #pragma unroll
     for (int j = 0; j < 16; ++j) oacc[t][j] = 0.f;
 
-  TileRow rows[2];
-  rows[0].init(a, 2 * qt);
-  rows[1].init(a, 2 * qt + 1);
+  TileRow rows[NR];
+#pragma unroll
+  for (int r = 0; r < NR; ++r) rows[r].init(a, NR * qt + r);
 
   // K tile: BK / RPL loads of RPL rows (1 KB) per tile, shared by the waves;
   // lane i moves row r = RPL ch + i/SL, logical slot (i%SL) ^ k_swizzle(r)
@@ -898,11 +910,16 @@ void masked_attention32_kernel(AttnArgs a) {
   // wave, and k_swizzle only sees the low bits of r, so one byte offset per
   // lane serves every load of this wave. The buffer covers this head's rows
   // [0, n): rows past n read as zeros.
-  static_assert(kA32Waves == 4, "the K swizzle below assumes ch % 4 == wave");
   const unsigned krow_bytes = unsigned(a.ks[2]) * 2u;
   const i32x4_t krsrc = buffer_rsrc(kp, unsigned((long(n - 1) * a.ks[2] + D) * 2));
   const int lrr = lane / SL, lpp = lane % SL;
-  const unsigned kvoff = unsigned(lrr) * krow_bytes + 16u * unsigned(lpp ^ k_swizzle<D>(RPL * wave + lrr));
+  // k_swizzle sees only the low bits of the row: those of ch & 3 (D 128) or
+  // ch & 1 (D 64), so per wave ch = NW cw + wave takes two offsets, by cw & 1
+  // (one when NW = 4).
+  unsigned kvoff[NW == 4 ? 1 : 2];
+#pragma unroll
+  for (int par = 0; par < (NW == 4 ? 1 : 2); ++par)
+    kvoff[par] = unsigned(lrr) * krow_bytes + 16u * unsigned(lpp ^ k_swizzle<D>(RPL * (par * NW + wave) + lrr));
   // V tile: the same loads; lane i moves row RPL ch + i/SL, logical slot sg
   // with vt_slot(sg, row) == i%SL, into physical slot i%SL (row & 3 == (i/SL) & 3).
   const unsigned vrow_bytes = unsigned(a.vs[2]) * 2u;
@@ -915,9 +932,9 @@ void masked_attention32_kernel(AttnArgs a) {
 #define SFL_A32_LOAD(kb, kbuf)                                                              \
   {                                                                                         \
     const int k0_ = (kb) * BK;                                                              \
-    _Pragma("unroll") for (int cw = 0; cw < BK / RPL / kA32Waves; ++cw) {                   \
-      const int ch_ = cw * kA32Waves + wave;                                                \
-      lds_load16(krsrc, lds_offset(&k_s[kbuf][RPL * ch_][0]), kvoff,                        \
+    _Pragma("unroll") for (int cw = 0; cw < BK / RPL / NW; ++cw) {                          \
+      const int ch_ = cw * NW + wave;                                                       \
+      lds_load16(krsrc, lds_offset(&k_s[kbuf][RPL * ch_][0]), kvoff[NW == 4 ? 0 : cw & 1],  \
                  unsigned(k0_ + RPL * ch_) * krow_bytes);                                   \
       lds_load16(vrsrc, lds_offset(&v_s[kbuf][RPL * ch_][0]), vvoff,                        \
                  unsigned(k0_ + RPL * ch_) * vrow_bytes);                                   \
@@ -932,8 +949,8 @@ void masked_attention32_kernel(AttnArgs a) {
     const MergedTile nxt = next_tile(a, rows);
     if (nxt.kb != INT_MAX) SFL_A32_LOAD(nxt.kb, buf ^ 1)
     const int k0 = cur.kb * BK;
-    const bool full = (half ? cur.full[1] : cur.full[0]) && a.s.use_full;
-    if (half ? cur.in[1] : cur.in[0]) {
+    const bool full = (NR == 2 && half ? cur.full[1] : cur.full[0]) && a.s.use_full;
+    if (NR == 2 && half ? cur.in[1] : cur.in[0]) {
       attn32_tile<T, D>(a, k_s[buf], v_s[buf], qreg, oacc, m_run, l_run, c, h, qrow, k0, full, vlane,
                         !(full && k0 + BK <= n));
     }
@@ -970,22 +987,41 @@ struct MaskedLaunch {
   unsigned threads;
 };
 
+// Keys one 64-query row of the mask can see: its window (left + right + one
+// tile, clipped to the sequence) plus the global prefix.
+inline long row_keys(const MaskArgs& m, long n) {
+  const long left = m.left >= 0 ? std::min<long>(m.left, n) : n;
+  const long right = m.causal ? 0 : (m.right >= 0 ? std::min<long>(m.right, n) : n);
+  return std::min<long>(n, left + right + BQ) + std::min<long>(m.prefix, n);
+}
+// Rows of at most this many keys (about 8 tiles) run one row per workgroup
+// (2 waves, head dim 64): with so few tiles per row the per-tile barrier of 4 waves and
+// the two rows' merged tile list cost more than sharing each K/V tile saves.
+#ifndef SFL_A32_SHORT_KEYS
+#define SFL_A32_SHORT_KEYS 512
+#endif
+constexpr long kShortRowKeys = SFL_A32_SHORT_KEYS;
+
 template <typename T>
-MaskedLaunch select_masked(int dim, long n, long k_row_stride, long v_row_stride) {
+MaskedLaunch select_masked(int dim, long n, long k_row_stride, long v_row_stride, const MaskArgs& m) {
   const bool offsets32 = n * k_row_stride * 2 < (1L << 31) && n * v_row_stride * 2 < (1L << 31);
+  const bool one_row = row_keys(m, n) <= kShortRowKeys;
   switch (dim) {
     case 32:
       return {reinterpret_cast<const void*>(&masked_attention_kernel<T, 32>), "masked_attention_kernel<D=32>",
               unsigned(BQ), unsigned(kThreads)};
     case 64:
+      if (offsets32 && one_row)
+        return {reinterpret_cast<const void*>(&masked_attention32_kernel<T, 64, 2>),
+                "masked_attention32_kernel<D=64, 2 waves>", unsigned(BQ), unsigned(2 * kWave)};
       if (offsets32)
-        return {reinterpret_cast<const void*>(&masked_attention32_kernel<T, 64>),
+        return {reinterpret_cast<const void*>(&masked_attention32_kernel<T, 64, kA32Waves>),
                 "masked_attention32_kernel<D=64>", unsigned(2 * BQ), unsigned(kA32Waves * kWave)};
       return {reinterpret_cast<const void*>(&masked_attention_pair_kernel<T>), "masked_attention_pair_kernel<D=64>",
               unsigned(BQ), unsigned(kPairWaves * kWave)};
-    case 128:
+    case 128:  // (one row per workgroup at D = 128 needs 300 VGPRs: one wave per SIMD)
       if (offsets32)
-        return {reinterpret_cast<const void*>(&masked_attention32_kernel<T, 128>),
+        return {reinterpret_cast<const void*>(&masked_attention32_kernel<T, 128, kA32Waves>),
                 "masked_attention32_kernel<D=128>", unsigned(2 * BQ), unsigned(kA32Waves * kWave)};
       return {reinterpret_cast<const void*>(&masked_attention_kernel<T, 128>), "masked_attention_kernel<D=128>",
               unsigned(BQ), unsigned(kThreads)};
@@ -995,7 +1031,7 @@ MaskedLaunch select_masked(int dim, long n, long k_row_stride, long v_row_stride
 
 template <typename T>
 int launch_masked(AttnArgs a, int batch, int dim, hipStream_t stream) {
-  const MaskedLaunch l = select_masked<T>(dim, a.n, a.ks[2], a.vs[2]);
+  const MaskedLaunch l = select_masked<T>(dim, a.n, a.ks[2], a.vs[2], a.m);
   if (!l.fn) return set_error(SFL_ERR_UNSUPPORTED, "masked_attention: head dim must be 32, 64 or 128");
   const dim3 grid(unsigned((a.n + l.queries_per_workgroup - 1) / l.queries_per_workgroup) *
                   unsigned(batch * a.heads));
@@ -1058,13 +1094,16 @@ extern "C" int sfl_masked_attention(const void* q, const void* k, const void* v,
 extern "C" int sfl_masked_attention_block(void) { return BQ; }
 
 extern "C" int sfl_masked_attention_kernel_info(int head_dim, int dtype, int n, long k_row_stride,
-                                                long v_row_stride, sfl_kernel_info* info) {
+                                                long v_row_stride, int causal, int window_left,
+                                                int window_right, int global_prefix, sfl_kernel_info* info) {
   const char* what = "masked_attention_kernel_info";
   if (!info) return set_error(SFL_ERR_INVALID, "%s: null pointer argument", what);
-  if (n < 1 || k_row_stride < 0 || v_row_stride < 0) return set_error(SFL_ERR_INVALID, "%s: bad sizes", what);
+  if (n < 1 || k_row_stride < 0 || v_row_stride < 0 || global_prefix < 0)
+    return set_error(SFL_ERR_INVALID, "%s: bad sizes", what);
+  const MaskArgs m{causal, window_left, window_right, global_prefix, nullptr};
   MaskedLaunch l{};
-  if (dtype == SFL_DTYPE_BF16) l = select_masked<bf16_t>(head_dim, n, k_row_stride, v_row_stride);
-  else if (dtype == SFL_DTYPE_F16) l = select_masked<f16_t>(head_dim, n, k_row_stride, v_row_stride);
+  if (dtype == SFL_DTYPE_BF16) l = select_masked<bf16_t>(head_dim, n, k_row_stride, v_row_stride, m);
+  else if (dtype == SFL_DTYPE_F16) l = select_masked<f16_t>(head_dim, n, k_row_stride, v_row_stride, m);
   else return set_error(SFL_ERR_UNSUPPORTED, "%s: dtype must be BF16 or F16", what);
   if (!l.fn) return set_error(SFL_ERR_UNSUPPORTED, "%s: head dim must be 32, 64 or 128", what);
   hipFuncAttributes attr{};

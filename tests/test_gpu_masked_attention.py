@@ -140,16 +140,21 @@ def test_kernel_follows_a_hand_edited_schedule(use_full):
 @pytest.mark.parametrize("d", [32, 64, 128])
 def test_launch_metadata_records_the_launched_kernels_resources(d):
     """launch_metadata gets the compiler's resource data for the kernel the call ran
-    (triton_attention.py:39-57 records the same fields from Triton)."""
-    q, k, v = (t.cuda() for t in inputs(1, 2, 130, d, torch.bfloat16, 3))
-    meta = {}
-    spec = MaskSpec(causal=True)
-    attention(q, k, v, compile_mask(130, spec), spec, launch_metadata=meta)
-    expected = {32: "masked_attention_kernel<D=32>", 64: "masked_attention32_kernel<D=64>",
-                128: "masked_attention32_kernel<D=128>"}[d]
-    print(meta)
-    assert meta["kernel_name"] == expected + " bf16"
-    assert 0 < meta["n_regs"] <= 512 and meta["n_spills"] * 4 == meta["private_segment_bytes"]
-    assert meta["shared_memory_bytes"] > 0 and meta["threads"] in (128, 256)
-    assert len(meta["asm_sha256"]["libsfl.so"]) == 64
-    assert "not rocprof" in meta["source"]
+    (triton_attention.py:39-57 records the same fields from Triton): rows of at most 512
+    visible keys run one 64-query row per workgroup at head dim 64."""
+    for n, spec, kind in ((130, MaskSpec(causal=True), "short"), (1000, MaskSpec(causal=True), "long"),
+                          (1000, MaskSpec(causal=True, window_left=127), "short")):
+        q, k, v = (t.cuda() for t in inputs(1, 2, n, d, torch.bfloat16, 3))
+        meta = {}
+        attention(q, k, v, compile_mask(n, spec), spec, launch_metadata=meta)
+        expected = {32: "masked_attention_kernel<D=32>",
+                    64: "masked_attention32_kernel<D=64, 2 waves>" if kind == "short"
+                    else "masked_attention32_kernel<D=64>",
+                    128: "masked_attention32_kernel<D=128>"}[d]
+        print(meta)
+        assert meta["kernel_name"] == expected + " bf16"
+        assert meta["queries_per_workgroup"] == (64 if d == 32 or "2 waves" in expected else 128)
+        assert 0 < meta["n_regs"] <= 512 and meta["n_spills"] * 4 == meta["private_segment_bytes"]
+        assert meta["shared_memory_bytes"] > 0 and meta["threads"] in (128, 256)
+        assert len(meta["asm_sha256"]["libsfl.so"]) == 64
+        assert "not rocprof" in meta["source"]
