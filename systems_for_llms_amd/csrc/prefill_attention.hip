@@ -657,8 +657,8 @@ __device__ __forceinline__ void attn32_tile(const AttnArgs& a, const uint4 (&kt)
                                             bool masked) {
   const int n = a.n;
   f32x16 sacc[2];
-#pragma unroll
-  for (int kb2 = 0; kb2 < 2; ++kb2) {
+  // S^T for key block kb2 (keys 32 kb2 .. +31 of the tile).
+  auto scores = [&](int kb2) {
 #pragma unroll
     for (int j = 0; j < 16; ++j) sacc[kb2][j] = 0.f;
 #pragma unroll
@@ -666,8 +666,18 @@ __device__ __forceinline__ void attn32_tile(const AttnArgs& a, const uint4 (&kt)
       const uint4 kr = kt[32 * kb2 + c][(D / 16 * h + ks) ^ k_swizzle<D>(c)];
       sacc[kb2] = mfma32<T>(u32x4{kr.x, kr.y, kr.z, kr.w}, qreg[ks], sacc[kb2]);
     }
-  }
-  if (masked) {  // wave-uniform: full tiles skip the token mask
+  };
+  // The scores are computed inside each branch (the masked one takes the
+  // blocks in the other order, so the compiler cannot hoist them above the
+  // branch): both branches then define the scores afresh, and the join needs
+  // no copy of them (with the MFMAs shared ahead of the branch the full-tile
+  // path copied all 32 scores every tile).
+  if (!masked) {  // wave-uniform: full tiles skip the token mask
+    scores(0);
+    scores(1);
+  } else {
+    scores(1);
+    scores(0);
     if (!a.m.docs) {
       const KeyRanges kr = key_ranges(a.m, qrow, n, k0 + 4 * h, full);
 #pragma unroll
