@@ -643,6 +643,19 @@ __device__ __forceinline__ KeyRanges key_ranges(const MaskArgs& m, int q, int n,
 // with dim 32t + l%32 of the 8 keys its P^T partner slots hold. The row sum comes from the packed
 // probabilities with dot2 (the sum of exactly the values the P V product
 // weights), kept per lane and added with the partner's at the end.
+// Max / sum of a value over lanes l and l ^ 32 (the two halves of a 32x32
+// MFMA column), exchanged with v_permlane32_swap instead of an LDS permute:
+// the swap leaves {v[l], v[l ^ 32]} in the two results in some order, and max
+// and + are symmetric.
+__device__ __forceinline__ float pair_max(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float pair_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 // One key tile of masked_attention32_kernel for this wave: S^T = K Q^T from the
 // swizzled K tile, the online softmax (with the token mask when `masked`), and
 // O^T += V^T P^T. One code path for full and masked tiles, the mask a
@@ -708,7 +721,7 @@ __device__ __forceinline__ void attn32_tile(const AttnArgs& a, const uint4 (&kt)
     mb = fmaxf(fmaxf(mb, sacc[1][j]), sacc[1][j + 1]);
   }
   float mx = fmaxf(ma, mb);
-  mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+  mx = pair_max(mx);
   const float cs = a.scale_log2;
   // Lazy maximum: the subtracted maximum m_run moves only when the tile's
   // maximum exceeds it by more than kLazyMax (log2 units), so the probabilities
@@ -970,7 +983,7 @@ void masked_attention32_kernel(AttnArgs a) {
   }
 #undef SFL_A32_LOAD
 
-  const float l_tot = l_run + __shfl_xor(l_run, 32, kWave);
+  const float l_tot = pair_sum(l_run);
   if (qrow >= n) return;
   const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
   uint16_t* op = static_cast<uint16_t*>(a.o) + b * a.os[0] + hd * a.os[1] + long(qrow) * a.os[2];
