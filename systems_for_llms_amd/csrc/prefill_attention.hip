@@ -761,11 +761,20 @@ __device__ __forceinline__ void attn32_tile(const AttnArgs& a, const uint4 (&kt)
   // tile t and key half (8 keys) is at byte vlane[t] + 32 D s2 + 16 D half
   // of the tile (vt_lane_offset).
   const unsigned vbase = unsigned(size_t((__attribute__((address_space(3))) const char*)(&vt[0][0])));
+  // One address register per dim tile, opaque to the compiler, so the step
+  // and half offsets go into the reads' offset fields (otherwise it forms
+  // every address with its own VALU add).
+  unsigned vaddr[D / 32];
+#pragma unroll
+  for (int t = 0; t < D / 32; ++t) {
+    vaddr[t] = vbase + vlane[t];
+    asm volatile("" : "+v"(vaddr[t]));
+  }
 #pragma unroll
   for (int s2 = 0; s2 < 4; ++s2) {
 #pragma unroll
     for (int t = 0; t < D / 32; ++t) {
-      const unsigned off = vbase + vlane[t] + 32u * D * s2;
+      const unsigned off = vaddr[t] + 32u * D * s2;
       const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(size_t)(off));
       const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(size_t)(off + 16u * D));
       const uint2 l2 = __builtin_bit_cast(uint2, lo), h2 = __builtin_bit_cast(uint2, hi);
