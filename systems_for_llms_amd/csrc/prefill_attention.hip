@@ -684,9 +684,9 @@ template <> __device__ __forceinline__ float first_pair<f16_t>(uint32_t pk, uint
 template <typename T, int D>
 __device__ __forceinline__ void attn32_tile(const AttnArgs& a, const uint4 (&kt)[BK][D / 8],
                                             const uint4 (&vt)[BK][D / 8], const u32x4 (&qreg)[D / 16],
-                                            f32x16 (&oacc)[D / 32], float& m_run, float& l_run, int c, int h,
-                                            int qrow, int k0, bool full, const unsigned (&vlane)[D / 32],
-                                            bool masked) {
+                                            f32x16 (&oacc)[D / 32], float& m_run, float& l_run, float& m_lim,
+                                            float& m_sub, int c, int h, int qrow, int k0, bool full,
+                                            const unsigned (&vlane)[D / 32], bool masked) {
   const int n = a.n;
   f32x16 sacc[2];
   // S^T for key block kb2 (keys 32 kb2 .. +31 of the tile).
@@ -747,12 +747,16 @@ __device__ __forceinline__ void attn32_tile(const AttnArgs& a, const uint4 (&kt)
   // stay below 2^kLazyMax and the O rescale runs only on the rare tiles where
   // some query's maximum jumps. Any m_run that bounds the exponents gives the
   // same O / l; it only has to keep them from overflowing.
-  const bool grow = mx * cs > m_run + kLazyMax;  // false for a fully masked row (mx = -inf)
+  // m_lim = m_run + kLazyMax and m_sub = the subtracted maximum (0 while
+  // m_run is -inf) change only with m_run, so they are kept, not recomputed.
+  const bool grow = mx * cs > m_lim;  // false for a fully masked row (mx = -inf)
   float alpha = 1.f;
   if (__ballot(grow)) {  // wave-uniform
     const float m_new = grow ? mx * cs : m_run;
     alpha = grow ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.f;  // 0 for the first admissible tile
     m_run = m_new;
+    m_lim = m_run + kLazyMax;
+    m_sub = m_run == -INFINITY ? 0.f : m_run;
     // In place (tied operands): the accumulators keep their registers on both
     // sides of this rare branch, so the common path needs no copies of them.
 #pragma unroll
@@ -760,7 +764,7 @@ __device__ __forceinline__ void attn32_tile(const AttnArgs& a, const uint4 (&kt)
 #pragma unroll
       for (int j = 0; j < 16; ++j) asm volatile("v_mul_f32 %0, %0, %1" : "+v"(oacc[t][j]) : "v"(alpha));
   }
-  const float ms = m_run == -INFINITY ? 0.f : m_run;
+  const float ms = m_sub;
   u32x4 pop[4];
   float psum[4];  // one accumulator per key step: short dot2 chains
   const uint32_t ones2 = ones_pair<T>();
@@ -946,6 +950,7 @@ void masked_attention32_kernel(AttnArgs a) {
   }
 
   float m_run = -INFINITY, l_run = 0.f;
+  float m_lim = -INFINITY, m_sub = 0.f;  // m_run + kLazyMax and the subtracted maximum (attn32_tile)
   f32x16 oacc[D / 32];
 #pragma unroll
   for (int t = 0; t < D / 32; ++t)
@@ -1004,7 +1009,7 @@ void masked_attention32_kernel(AttnArgs a) {
     const int k0 = cur.kb * BK;
     const bool full = (NR == 2 && half ? cur.full[1] : cur.full[0]) && a.s.use_full;
     if (NR == 2 && half ? cur.in[1] : cur.in[0]) {
-      attn32_tile<T, D>(a, k_s[buf], v_s[buf], qreg, oacc, m_run, l_run, c, h, qrow, k0, full, vlane,
+      attn32_tile<T, D>(a, k_s[buf], v_s[buf], qreg, oacc, m_run, l_run, m_lim, m_sub, c, h, qrow, k0, full, vlane,
                         !(full && k0 + BK <= n));
     }
     __builtin_amdgcn_s_waitcnt(sfl_vmcnt(0));  // the next K and V tiles have landed
