@@ -142,10 +142,11 @@ def test_config1_bf16_free_running_first_divergence(golden):
 
 
 def test_config2_bf16_teacher_forced_against_cpu_oracle():
-    """100.3M model, batch 8, 512-token prompt then 64 positions, vs the fp32 KV-cached oracle."""
+    """100.3M model, batch 8, the whole context: 512-token prompt then the remaining 512 positions
+    decoded step by step (graph replays), vs the fp32 KV-cached oracle."""
     cfg = load_model_config("scale-100m-s1024")
     sd = seeded_state_dict(cfg, 1337)
-    prompt_len, extra = 512, 64
+    prompt_len, extra = 512, cfg.context_length - 512
     seq = seeded_prompt(cfg.vocab_size, 8, prompt_len + extra, 2027)
     torch.set_num_threads(16)
     ref = om.KVCacheOracle(sd, cfg, 8, prompt_len + extra).step(seq)[:, prompt_len - 1:, :]

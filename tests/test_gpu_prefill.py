@@ -115,25 +115,27 @@ def format_floor(sd, cfg, seq, prompt, wide=False):
 
 
 def test_config2_prefill_then_decode_teacher_forced():
-    """100.3M bf16, batch 8: GEMM prefill of 512 tokens, then 64 teacher-forced decode positions."""
+    """100.3M bf16, batch 8, the whole context of config 2: GEMM prefill of 512 tokens,
+    then teacher-forced decode of the remaining 511 positions to ctx 1024."""
     cfg = load_model_config("scale-100m-s1024")
     sd = seeded_state_dict(cfg, 1337)
-    seq = seeded_prompt(cfg.vocab_size, 8, 576, 2027)
+    ctx = cfg.context_length  # 1024
+    seq = seeded_prompt(cfg.vocab_size, 8, ctx, 2027)
     torch.set_num_threads(16)
-    ref = om.KVCacheOracle(sd, cfg, 8, 576).step(seq)
+    ref = om.KVCacheOracle(sd, cfg, 8, ctx).step(seq)
     floor = format_floor(sd, cfg, seq, 512)
-    wide = format_floor(sd, cfg, seq[:2], 512, wide=True)
+    wide = format_floor(sd, cfg, seq, 512, wide=True)  # the drift over the same rows the gates compare
     model = gpu_model(cfg, sd)
-    session = DecodeSession(model, 8, 576, record_logits=True)
+    session = DecodeSession(model, 8, ctx, record_logits=True)
     all_logits = session.prefill(seq[:, :512].cuda(), all_logits=True, forced=seq.cuda())
-    session.run(64, use_graph=True)
+    session.run(ctx - 1 - 512, use_graph=True)  # positions 512 .. ctx - 2 predict tokens 513 .. ctx - 1
     torch.cuda.synchronize()
     pre = all_logits.cpu()
-    dec = session.logits[:, 512:575].float().cpu()
+    dec = session.logits[:, 512:ctx - 1].float().cpu()
     bf16_gate("config2 prefill (positions 0..511)", pre, ref[:, :512], floor[:, :512],
-              envelope=(floor[:2, :512], wide[:, :512]))
-    bf16_gate("config2 decode after prefill (positions 512..574)", dec, ref[:, 512:575], floor[:, 512:575],
-              envelope=(floor[:2, 512:575], wide[:, 512:575]))
+              envelope=(floor[:, :512], wide[:, :512]))
+    bf16_gate(f"config2 decode after prefill (positions 512..{ctx - 2})", dec, ref[:, 512:ctx - 1],
+              floor[:, 512:ctx - 1], envelope=(floor[:, 512:ctx - 1], wide[:, 512:ctx - 1]))
     # The decode head after prefill (fp32 inputs) equals the prefill's own last-position
     # logits (bf16 GEMM inputs) up to the rounding of the final norm's output.
     torch.testing.assert_close(session.logits[:, 511].float().cpu(), pre[:, 511], atol=2e-2, rtol=0)
