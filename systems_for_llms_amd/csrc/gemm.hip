@@ -48,6 +48,9 @@ struct GemmArgs {
   uint16_t* v_cache;
   // SWIGLU
   uint16_t* h_out;     // [M, N/2]
+  // Every bf16 output base is 16-byte aligned: the 32x32 kernel then stores
+  // 8 consecutive outputs per lane (lane pairs exchange halves first).
+  int vec16;
 };
 
 __device__ __forceinline__ f32x4 mfma_bf16(const u32x4& a, const u32x4& b, f32x4 c) {
@@ -80,6 +83,38 @@ __device__ __forceinline__ QkvFeat qkv_feat(const GemmArgs& g, int n) {
 __device__ __forceinline__ QkvTok qkv_tok(const GemmArgs& g, int m) {
   const int b = m / g.seq;
   return QkvTok{b, m - b * g.seq};
+}
+
+// RoPE (attention.py:44-58) of 4 consecutive q or k features (dims dim ..
+// dim+3 of one head: two rotation pairs) of token qt; v features pass through.
+__device__ __forceinline__ void rope4(const GemmArgs& g, float (&y)[4], const QkvFeat& qf, const QkvTok& qt) {
+  if (qf.section >= 2) return;
+  const int half = g.head_dim / 2;
+  const float2 c = *reinterpret_cast<const float2*>(g.cos_t + long(qt.t) * half + qf.dim / 2);
+  const float2 s = *reinterpret_cast<const float2*>(g.sin_t + long(qt.t) * half + qf.dim / 2);
+  const float e0 = y[0], o0 = y[1], e1 = y[2], o1 = y[3];
+  y[0] = e0 * c.x - o0 * s.x;
+  y[1] = e0 * s.x + o0 * c.x;
+  y[2] = e1 * c.y - o1 * s.y;
+  y[3] = e1 * s.y + o1 * c.y;
+}
+
+// Destination of feature qf of token qt: q [B, H, T, dk] or the k / v cache [B, H, cap, dk].
+__device__ __forceinline__ uint16_t* qkv_dst(const GemmArgs& g, const QkvFeat& qf, const QkvTok& qt) {
+  if (qf.section == 0) return g.q_out + ((long(qt.b) * g.heads + qf.head) * g.seq + qt.t) * g.head_dim + qf.dim;
+  uint16_t* cache = qf.section == 1 ? g.k_cache : g.v_cache;
+  return cache + ((long(qt.b) * g.heads + qf.head) * g.cap + qt.t) * g.head_dim + qf.dim;
+}
+
+// Two packed groups of 4 bf16 outputs, A (lane-local features f .. f+3) and
+// B (f+8 .. f+11), where lane l ^ 32 holds f+4 .. f+7 and f+12 .. f+15: one
+// v_permlane32_swap per dword gives lanes 0..31 features f .. f+7 (own A,
+// partner's A) and lanes 32..63 features f+8 .. f+15 (partner's B, own B),
+// one 16-byte store each instead of two 8-byte stores.
+__device__ __forceinline__ uint4 pair8(const uint32_t (&a)[2], const uint32_t (&b)[2]) {
+  const auto s0 = __builtin_amdgcn_permlane32_swap(a[0], b[0], false, false);
+  const auto s1 = __builtin_amdgcn_permlane32_swap(a[1], b[1], false, false);
+  return make_uint4(s0[0], s1[0], s0[1], s1[1]);
 }
 
 // Epilogue of one 16x16 MFMA tile: v holds features nt + 4*grp + (0..3) of
@@ -126,26 +161,8 @@ __device__ __forceinline__ void store_tile(const GemmArgs& g, const f32x4& v, in
         }
       }
     } else {  // G_QKV
-      const int section = qf.section, head = qf.head, dim = qf.dim;
-      const int b = qt.b, t = qt.t;
-      if (section < 2) {
-        const int half = g.head_dim / 2;
-        const float2 c = *reinterpret_cast<const float2*>(g.cos_t + long(t) * half + dim / 2);
-        const float2 s = *reinterpret_cast<const float2*>(g.sin_t + long(t) * half + dim / 2);
-        const float e0 = y[0], o0 = y[1], e1 = y[2], o1 = y[3];
-        y[0] = e0 * c.x - o0 * s.x;
-        y[1] = e0 * s.x + o0 * c.x;
-        y[2] = e1 * c.y - o1 * s.y;
-        y[3] = e1 * s.y + o1 * c.y;
-      }
-      uint16_t* dst;
-      if (section == 0) {
-        dst = g.q_out + ((long(b) * g.heads + head) * g.seq + t) * g.head_dim + dim;
-      } else {
-        uint16_t* cache = section == 1 ? g.k_cache : g.v_cache;
-        dst = cache + ((long(b) * g.heads + head) * g.cap + t) * g.head_dim + dim;
-      }
-      *reinterpret_cast<uint2*>(dst) = make_uint2(pack_bf16(y[0], y[1]), pack_bf16(y[2], y[3]));
+      rope4(g, y, qf, qt);
+      *reinterpret_cast<uint2*>(qkv_dst(g, qf, qt)) = make_uint2(pack_bf16(y[0], y[1]), pack_bf16(y[2], y[3]));
     }
   }
 }
@@ -403,20 +420,78 @@ void gemm32_kernel(GemmArgs g) {
       const int nt = n0 + (TBN / WN) * wn + 32 * i;
       if constexpr (E == G_SWIGLU) {
         // W1/W3 interleaved in blocks of 8 rows: groups q = 0, 2 are W1 features,
-        // q + 1 the matching W3 features, all in this lane.
-        if (m >= g.m) continue;
+        // q + 1 the matching W3 features, all in this lane. Hidden features
+        // nt/2 + 4q + 4hf .. +3; with vec16 the two groups go out as one
+        // 16-byte store per lane at nt/2 + 8hf (d_ff % 8 == 0: a group of 8 is
+        // wholly inside or outside d_ff).
+        uint32_t pk[2][2];
 #pragma unroll
         for (int q = 0; q < 4; q += 2) {
-          const int f = nt / 2 + 4 * q + 4 * hf;  // hidden feature index
-          if (f >= g.n / 2) continue;
           float h[4];
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const float a1 = acc[i][j][4 * q + e], a3 = acc[i][j][4 * q + 4 + e];
             h[e] = a1 / (1.f + expf(-a1)) * a3;
           }
-          *reinterpret_cast<uint2*>(g.h_out + long(m) * (g.n / 2) + f) =
-              make_uint2(pack_bf16(h[0], h[1]), pack_bf16(h[2], h[3]));
+          pk[q / 2][0] = pack_bf16(h[0], h[1]);
+          pk[q / 2][1] = pack_bf16(h[2], h[3]);
+        }
+        if (g.vec16) {
+          const uint4 v8 = pair8(pk[0], pk[1]);
+          const int f = nt / 2 + 8 * hf;
+          if (m < g.m && f < g.n / 2) *reinterpret_cast<uint4*>(g.h_out + long(m) * (g.n / 2) + f) = v8;
+        } else if (m < g.m) {
+#pragma unroll
+          for (int q = 0; q < 4; q += 2) {
+            const int f = nt / 2 + 4 * q + 4 * hf;  // hidden feature index
+            if (f < g.n / 2)
+              *reinterpret_cast<uint2*>(g.h_out + long(m) * (g.n / 2) + f) = make_uint2(pk[q / 2][0], pk[q / 2][1]);
+          }
+        }
+      } else if (E != G_PLAIN || (!g.c_f32 && !g.accumulate)) {
+        // bf16 outputs (q/k/v, plain bf16): feature groups q and q + 1 of the
+        // lane pair go out as 16-byte stores (vec16; whole 32-feature blocks
+        // inside N), else 8 bytes per group.
+        const bool wide = g.vec16 && nt + 32 <= g.n && (E == G_QKV || g.n % 8 == 0);
+#pragma unroll
+        for (int q = 0; q < 4; q += 2) {
+          uint32_t pk[2][2];
+          QkvFeat feat[2];
+#pragma unroll
+          for (int r = 0; r < 2; ++r) {
+            float y[4] = {acc[i][j][4 * (q + r)], acc[i][j][4 * (q + r) + 1], acc[i][j][4 * (q + r) + 2],
+                          acc[i][j][4 * (q + r) + 3]};
+            feat[r] = E == G_QKV ? qkv_feat(g, nt + 8 * (q + r) + 4 * hf) : QkvFeat{};
+            if constexpr (E == G_QKV) rope4(g, y, feat[r], tok);
+            pk[r][0] = pack_bf16(y[0], y[1]);
+            pk[r][1] = pack_bf16(y[2], y[3]);
+          }
+          if (wide) {
+            const uint4 v8 = pair8(pk[0], pk[1]);
+            if (m < g.m) {
+              const int f = nt + 8 * q + 8 * hf;  // first of this lane's 8 features
+              uint16_t* dst = E == G_QKV ? qkv_dst(g, qkv_feat(g, f), tok)
+                                         : static_cast<uint16_t*>(g.c) + long(m) * g.n + f;
+              *reinterpret_cast<uint4*>(dst) = v8;
+            }
+          } else if (m < g.m) {
+#pragma unroll
+            for (int r = 0; r < 2; ++r) {
+              const int n = nt + 8 * (q + r) + 4 * hf;
+              if (E == G_QKV) {
+                if (n < g.n) *reinterpret_cast<uint2*>(qkv_dst(g, feat[r], tok)) = make_uint2(pk[r][0], pk[r][1]);
+              } else if (n + 3 < g.n && (g.n & 3) == 0) {
+                *reinterpret_cast<uint2*>(static_cast<uint16_t*>(g.c) + long(m) * g.n + n) =
+                    make_uint2(pk[r][0], pk[r][1]);
+              } else {
+                uint16_t* c = static_cast<uint16_t*>(g.c) + long(m) * g.n + n;
+                const uint32_t w[2] = {pk[r][0], pk[r][1]};
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                  if (n + e < g.n) c[e] = uint16_t(w[e / 2] >> (16 * (e % 2)));
+              }
+            }
+          }
         }
       } else {
 #pragma unroll
@@ -430,6 +505,8 @@ void gemm32_kernel(GemmArgs g) {
     }
   }
 }
+
+inline bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
 
 template <int E>
 int launch_gemm(const GemmArgs& g, hipStream_t s, const char* what) {
@@ -528,6 +605,7 @@ extern "C" int sfl_gemm_bf16(const void* a, const void* w, void* c, int m, int n
   GemmArgs g{};
   g.a = static_cast<const uint16_t*>(a); g.w = static_cast<const uint16_t*>(w);
   g.m = m; g.n = n; g.k = k; g.c = c; g.c_f32 = c_dtype == SFL_DTYPE_F32; g.accumulate = accumulate;
+  g.vec16 = aligned16(c);
   return launch_gemm<G_PLAIN>(g, static_cast<hipStream_t>(stream), "gemm_bf16");
 }
 
@@ -548,6 +626,7 @@ extern "C" int sfl_gemm_qkv_rope(const void* a, const void* w_qkv, int m, int se
   g.d_model = d_model; g.cap = capacity;
   g.q_out = static_cast<uint16_t*>(q_out); g.k_cache = static_cast<uint16_t*>(k_cache);
   g.v_cache = static_cast<uint16_t*>(v_cache);
+  g.vec16 = aligned16(q_out) && aligned16(k_cache) && aligned16(v_cache);
   return launch_gemm<G_QKV>(g, static_cast<hipStream_t>(stream), what);
 }
 
@@ -559,6 +638,7 @@ extern "C" int sfl_gemm_swiglu(const void* a, const void* w13_interleaved, void*
   GemmArgs g{};
   g.a = static_cast<const uint16_t*>(a); g.w = static_cast<const uint16_t*>(w13_interleaved);
   g.m = m; g.n = 2 * d_ff; g.k = k; g.h_out = static_cast<uint16_t*>(h_out);
+  g.vec16 = aligned16(h_out);
   return launch_gemm<G_SWIGLU>(g, static_cast<hipStream_t>(stream), what);
 }
 

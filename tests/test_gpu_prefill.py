@@ -52,6 +52,72 @@ def test_gemm_large_grid_matches_fp32_matmul(m, n, k):
     torch.testing.assert_close(out[rows.cuda()].cpu(), ref, atol=1e-3 * k ** 0.5, rtol=1e-4)
 
 
+def _sample_rows(m, g):
+    return torch.cat([torch.arange(0, 40), torch.randint(0, m, (200,), generator=g), torch.arange(m - 40, m)])
+
+
+def _bf16_out(shape, aligned):
+    """A zeroed bf16 output on the GPU; ``aligned=False`` starts it 8 bytes past a
+    16-byte boundary (the kernels then store 8 bytes per lane instead of 16)."""
+    n = 1
+    for s in shape:
+        n *= s
+    off = 0 if aligned else 4
+    buf = torch.zeros(n + off, device="cuda", dtype=torch.bfloat16)
+    out = buf[off:].view(shape)
+    assert (out.data_ptr() % 16 == 0) == aligned
+    return out
+
+
+# The bf16 epilogues of the 256 x 256 kernel (q/k/v + RoPE + cache write,
+# SwiGLU, plain bf16 output) with ragged M (token tiles spanning two batch
+# rows), a ragged N, and outputs that are / are not 16-byte aligned.
+@pytest.mark.parametrize("aligned", [True, False])
+def test_gemm_large_grid_bf16_epilogues(aligned):
+    d, h, f, b, t, cap = 1024, 16, 2752, 4, 3000, 3072
+    dk, m = d // h, b * t
+    g = torch.Generator().manual_seed(11)
+    a = torch.randn((m, d), generator=g).bfloat16()
+    wqkv = (torch.randn((3 * d, d), generator=g) * 0.03).bfloat16()
+    w1 = (torch.randn((f, d), generator=g) * 0.03).bfloat16()
+    w3 = (torch.randn((f, d), generator=g) * 0.03).bfloat16()
+    w13 = torch.stack([w1.view(f // 8, 8, d), w3.view(f // 8, 8, d)], dim=1).reshape(2 * f, d).contiguous()
+    cos, sin = om.rope_tables(10000.0, dk, cap)
+    ga, gqkv, g13, gcos, gsin = a.cuda(), wqkv.cuda(), w13.cuda(), cos.cuda(), sin.cuda()
+    q = _bf16_out((b, h, t, dk), aligned)
+    kc, vc = _bf16_out((b, h, cap, dk), aligned), _bf16_out((b, h, cap, dk), aligned)
+    hid = _bf16_out((m, f), aligned)
+    n_plain = 8200  # 32 x 256 + 8: the last feature block is partial
+    wp = (torch.randn((n_plain, d), generator=g) * 0.03).bfloat16()
+    gwp = wp.cuda()
+    plain = _bf16_out((m, n_plain), aligned)
+    st = _lib.stream_handle()
+    _lib.call("sfl_gemm_qkv_rope", ga.data_ptr(), gqkv.data_ptr(), m, t, d, h, gcos.data_ptr(), gsin.data_ptr(),
+              q.data_ptr(), kc.data_ptr(), vc.data_ptr(), cap, st)
+    _lib.call("sfl_gemm_swiglu", ga.data_ptr(), g13.data_ptr(), hid.data_ptr(), m, f, d, st)
+    _lib.call("sfl_gemm_bf16", ga.data_ptr(), gwp.data_ptr(), plain.data_ptr(), m, n_plain, d, 1, 0, st)
+    torch.cuda.synchronize()
+
+    rows = _sample_rows(m, g)
+    bi, ti = rows // t, rows % t
+    proj = a[rows].float() @ wqkv.float().t()  # [R, 3d]
+    c, s = cos[ti][:, None, :], sin[ti][:, None, :]
+
+    def rot(x):  # [R, h, dk], each row at its own position
+        out = torch.empty_like(x)
+        out[..., 0::2] = x[..., 0::2] * c - x[..., 1::2] * s
+        out[..., 1::2] = x[..., 0::2] * s + x[..., 1::2] * c
+        return out
+    qr, kr, vr = (proj[:, i * d:(i + 1) * d].view(-1, h, dk) for i in range(3))
+    _ulp_close("q (RoPE)", q.cpu()[bi, :, ti], om._round(rot(qr), torch.bfloat16), 2e-3)
+    _ulp_close("k cache (RoPE)", kc.cpu()[bi, :, ti], om._round(rot(kr), torch.bfloat16), 2e-3)
+    _ulp_close("v cache", vc.cpu()[bi, :, ti], om._round(vr, torch.bfloat16), 2e-3)
+    assert not kc[:, :, t:].any() and not vc[:, :, t:].any(), "wrote cache rows past the sequence"
+    g1, g3 = a[rows].float() @ w1.float().t(), a[rows].float() @ w3.float().t()
+    _ulp_close("SwiGLU hidden", hid.cpu()[rows], om._round(g1 * torch.sigmoid(g1) * g3, torch.bfloat16), 2e-3)
+    _ulp_close("plain bf16", plain.cpu()[rows], om._round(a[rows].float() @ wp.float().t(), torch.bfloat16), 2e-3)
+
+
 # d % 4 == 0 and d <= 2048 take the one-wave-per-row kernel (m not a multiple
 # of its 4 rows per workgroup included); other widths the workgroup-per-row one.
 @pytest.mark.parametrize("m,d", [(1, 64), (7, 96), (130, 1024), (33, 2048), (5, 2052), (9, 1030)])
