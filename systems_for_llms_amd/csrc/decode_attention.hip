@@ -114,11 +114,14 @@ __global__ __launch_bounds__(W * kWave) void decode_attn_kernel(
   const int begin = split * chunk;
   const int t_first = begin + wave * TILE;
 
-  // With one split (the model's path) the first tile's loads are issued
-  // before the length is known, rows clamped to the capacity, so their round
-  // trip overlaps the q and length loads; rows at or past the length are
-  // zeroed once it is known (they may hold stale values, NaN included).
-  const bool spec = splits == 1;
+  // With one split (the model's path) the first W/2 waves issue their first
+  // tile's loads before the length is known, rows clamped to the capacity, so
+  // their round trip overlaps the q and length loads; rows at or past the
+  // length are zeroed once it is known (they may hold stale values, NaN
+  // included). The other waves wait for the length: a short row then wastes
+  // at most W/2 tiles of loads (all W waves speculating: ~15.5 us per 324M
+  // launch below length 1024 against ~11.5, and no faster at 3584).
+  const bool spec = splits == 1 && wave < W / 2;
   uint4 kr[NL], vr[NL];
   if (spec) {
 #pragma unroll
