@@ -37,12 +37,17 @@ struct split_t {};
 struct f32x_t {};
 struct resid_t {};
 
-template <typename T, int D, int G>
+// kStep: the fused output projection of the model's decode step (one split
+// per row). Its D = 64, one-head-per-group tiles are 4 loads deep: the 324M
+// decode step measured 1.404 -> 1.360 ms against 8 loads (config 4's split
+// launches, which keep 8, measured 1.3% slower with 4; the operator's
+// outputs keep 8, so its fp32 and activation-format outputs stay equal).
+template <typename T, int D, int G, bool kStep = false>
 struct DecodeShape {
   static constexpr int EPL = vec_elems<T>();  // elements per lane per load
   static constexpr int LPT = D / EPL;          // lanes per key row
   static constexpr int TPL = kWave / LPT;      // key rows per wave load
-  static constexpr int NL = (G >= 4) ? 4 : 8;  // loads per tile and operand
+  static constexpr int NL = (G >= 4 || (kStep && G == 1 && D == 64)) ? 4 : 8;  // loads per tile and operand
   static constexpr int TILE = NL * TPL;        // keys per tile
   static_assert(LPT >= 1 && LPT <= kWave, "head dim does not fit a wave");
 };
@@ -85,9 +90,9 @@ __global__ __launch_bounds__(W * kWave) void decode_attn_kernel(
     const int32_t* __restrict__ lengths, float* __restrict__ pmax, float* __restrict__ psum,
     float* __restrict__ pout, void* __restrict__ out, int kv_heads, int cap, int splits, int chunk,
     float qscale, float* __restrict__ x, int d_model) {
-  using S = DecodeShape<T, D, G>;
-  constexpr int EPL = S::EPL, LPT = S::LPT, TPL = S::TPL, NL = S::NL, TILE = S::TILE;
   constexpr bool kProj = std::is_same<TO, resid_t>::value;
+  using S = DecodeShape<T, D, G, kProj>;
+  constexpr int EPL = S::EPL, LPT = S::LPT, TPL = S::TPL, NL = S::NL, TILE = S::TILE;
   __shared__ float sm[W][G][D + 2];
   __shared__ float os[kProj ? G * D : 1];
   const int wave = threadIdx.x / kWave;
@@ -114,14 +119,15 @@ __global__ __launch_bounds__(W * kWave) void decode_attn_kernel(
   const int begin = split * chunk;
   const int t_first = begin + wave * TILE;
 
-  // With one split (the model's path) the first W/2 waves issue their first
+  // With one split (the model's path) the first waves issue their first
   // tile's loads before the length is known, rows clamped to the capacity, so
   // their round trip overlaps the q and length loads; rows at or past the
   // length are zeroed once it is known (they may hold stale values, NaN
-  // included). The other waves wait for the length: a short row then wastes
-  // at most W/2 tiles of loads (all W waves speculating: ~15.5 us per 324M
-  // launch below length 1024 against ~11.5, and no faster at 3584).
-  const bool spec = splits == 1 && wave < W / 2;
+  // included). The others wait for the length: the speculative loads stay at
+  // W/2 tiles of 8 loads (W tiles of 4), so a short row wastes at most that
+  // much (with every wave speculating 8-load tiles: ~15.5 us per 324M launch
+  // below length 1024 against ~11.5, and no faster at 3584).
+  const bool spec = splits == 1 && wave < W * 4 / NL;
   uint4 kr[NL], vr[NL];
   if (spec) {
 #pragma unroll
