@@ -216,18 +216,43 @@ __global__ __launch_bounds__(W * kWave) void decode_attn_kernel(
       }
     }
   };
-  int t_loop = t_first;
-  if (spec) {
-    if (t_first < end) tile(t_first, kr, vr);
-    t_loop = t_first + W * TILE;
-  }
-  for (int t0 = t_loop; t0 < end; t0 += W * TILE) {
-    uint4 kn[NL], vn[NL];
+  const int t_loop = spec ? t_first + W * TILE : t_first;
+  if constexpr (kProj && NL == 4) {
+    // The fused path's 4-load tiles leave registers for one tile of loads in
+    // flight ahead of the tile being computed (324M decode step -0.8%); past
+    // the end the loads re-read the split's last row.
+    uint4 kc[NL], vc[NL];
+    if (t_loop < end) {
 #pragma unroll
-    for (int i = 0; i < NL; ++i) kn[i] = load16_stream(kb + long(min(t0 + i * TPL + slot, last)) * D);
+      for (int i = 0; i < NL; ++i) kc[i] = load16_stream(kb + long(min(t_loop + i * TPL + slot, last)) * D);
 #pragma unroll
-    for (int i = 0; i < NL; ++i) vn[i] = load16_stream(vb + long(min(t0 + i * TPL + slot, last)) * D);
-    tile(t0, kn, vn);
+      for (int i = 0; i < NL; ++i) vc[i] = load16_stream(vb + long(min(t_loop + i * TPL + slot, last)) * D);
+    }
+    if (spec && t_first < end) tile(t_first, kr, vr);
+    for (int t0 = t_loop; t0 < end; t0 += W * TILE) {
+      const int t1 = min(t0 + W * TILE, last);
+      uint4 kn[NL], vn[NL];
+#pragma unroll
+      for (int i = 0; i < NL; ++i) kn[i] = load16_stream(kb + long(min(t1 + i * TPL + slot, last)) * D);
+#pragma unroll
+      for (int i = 0; i < NL; ++i) vn[i] = load16_stream(vb + long(min(t1 + i * TPL + slot, last)) * D);
+      tile(t0, kc, vc);
+#pragma unroll
+      for (int i = 0; i < NL; ++i) {
+        kc[i] = kn[i];
+        vc[i] = vn[i];
+      }
+    }
+  } else {
+    if (spec && t_first < end) tile(t_first, kr, vr);
+    for (int t0 = t_loop; t0 < end; t0 += W * TILE) {
+      uint4 kn[NL], vn[NL];
+#pragma unroll
+      for (int i = 0; i < NL; ++i) kn[i] = load16_stream(kb + long(min(t0 + i * TPL + slot, last)) * D);
+#pragma unroll
+      for (int i = 0; i < NL; ++i) vn[i] = load16_stream(vb + long(min(t0 + i * TPL + slot, last)) * D);
+      tile(t0, kn, vn);
+    }
   }
 
   // Fused projection: issue the first round of W_o loads now, so they land
