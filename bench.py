@@ -384,7 +384,8 @@ def main() -> int:
         return profile_target_gemm()
     if args.gpus != 1:
         print("bench.py measures one GPU: every box in this build has a single MI355X and the decode "
-              "path is not sharded across GPUs (see DESIGN.md for how it would shard)", file=sys.stderr)
+              "path is not sharded across GPUs (data parallel over the batch would need no exchange)",
+              file=sys.stderr)
         return 2
     if not 1 <= args.steps <= CONTEXT - PROMPT - 1 or not 0 <= args.warmup <= CONTEXT - PROMPT - 1:
         print(f"--steps and --warmup must be in [1, {CONTEXT - PROMPT - 1}]", file=sys.stderr)
