@@ -112,6 +112,33 @@ def test_attention_out_proj_matches_reference(dtype, dim, batch, heads):
         torch.testing.assert_close(got[1], x0[1].double(), atol=0, rtol=0)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_attention_out_proj_long_ragged_rows(dtype):
+    """Rows several key tiles per wave long (head dim 64: the tile loop with one tile of loads ahead),
+    lengths on and off the tile and round boundaries, the capacity, 0 and 1."""
+    g = torch.Generator().manual_seed(77)
+    heads, dim, cap = 4, 64, 2100
+    lengths = torch.tensor([cap, 0, 1, 31, 32, 33, 511, 512, 513, 1024, 1537, 2099], dtype=torch.int32)
+    batch, d_model = lengths.numel(), heads * dim
+    q = torch.randn(batch, heads, dim, generator=g)
+    k = torch.randn(batch, heads, cap, dim, generator=g).to(dtype)
+    v = torch.randn(batch, heads, cap, dim, generator=g).to(dtype)
+    w_out = (torch.randn(d_model, d_model, generator=g) * d_model ** -0.5).to(dtype)
+    x0 = torch.randn(batch, d_model, generator=g)
+    x = x0.cuda()
+    scale = dim ** -0.5
+    qd, kd, vd, ld, wd = q.cuda(), k.cuda(), v.cuda(), lengths.cuda(), _lib.pack_gemv(w_out.cuda())
+    _lib.call("sfl_decode_attention_out_proj", qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), ld.data_ptr(),
+              wd.data_ptr(), x.data_ptr(), batch, heads, cap, dim, scale, _lib.dtype_code(dtype),
+              _lib.stream_handle())
+    o = reference_attention(q, k, v, lengths.long(), scale).reshape(batch, d_model)
+    ref = x0.double() + o @ w_out.double().T
+    got = x.cpu().double()
+    print(f"{dtype} long rows: max abs err {(got - ref).abs().max().item():.2e}")
+    torch.testing.assert_close(got, ref, atol=5e-5, rtol=5e-5)
+    torch.testing.assert_close(got[1], x0[1].double(), atol=0, rtol=0)  # the empty row adds nothing
+
+
 def test_attention_out_proj_rejects_unsupported_shapes():
     t = torch.zeros(4096, device="cuda")
     args = lambda dim, dtype: (t.data_ptr(),) * 4 + (t.data_ptr(), t.data_ptr(), 1, 2, 8, dim, 0.1, dtype,
