@@ -288,8 +288,8 @@ int sfl_masked_attention_kernel_info(int head_dim, int dtype, int n, long k_row_
 
 /* ---- prefill (bf16 weights) -------------------------------------------------
  * C^T = W A^T on bf16 MFMAs; A [M, K] bf16 row-major (one row per token),
- * W [N, K] bf16; K % 8 == 0. K % 64 == 0 runs 32x32x16 MFMA tiles of 256 x 256
- * (grids of >= 512 such tiles) or 128 x 128 features x tokens, other K the
+ * W [N, K] bf16; K % 8 == 0. K % 64 == 0 runs 32x32x16 MFMA tiles of 256 x 384
+ * (grids of >= 320 such tiles) or 128 x 128 features x tokens, other K the
  * 16x16x32 kernel on 128 x 128 tiles.
  * Replace, for a whole prompt, the Linear layers of one TransformerBlock and
  * the lm_head (src/llmlab/model/layers.py:34-35, attention.py:160-162,199-203,

@@ -292,7 +292,8 @@ __device__ __forceinline__ int stage_swizzle(int r) {
 // XCD x is given a contiguous range of the tile order, and that order walks
 // groups of kGroupM token tiles across the feature tiles. The workgroups an
 // XCD runs at once then cover about 4 token tiles x 8 feature tiles, whose
-// operands stay in (or near) its 4 MB L2.
+// operands stay in (or near) its 4 MB L2 (for 256 x 384 tiles, 448 KB of the
+// 2.5 MB a K step requests are distinct).
 constexpr int kXcds = 8;
 constexpr int kGroupM = 4;
 
@@ -310,10 +311,11 @@ __device__ __forceinline__ int2 xcd_tile(int b, int tn, int tm) {
 
 // TBN x TBM tiles (features x tokens) per workgroup of WN x WM waves; a wave
 // owns (TBN/WN) x (TBM/WM) as blocks of 32 x 32. 128 x 128 with 2 x 2 waves:
-// two workgroups per CU (64 KB of LDS each), 64 x 64 per wave. 256 x 256 with
-// 4 x 2 waves: one workgroup of 8 waves per CU (128 KB), 64 x 128 per wave,
-// which reads 3/4 of the LDS operand bytes per MFMA of the 64 x 64 wave tile
-// and stages half the bytes per MFMA through LDS.
+// two workgroups per CU (64 KB of LDS each), 64 x 64 per wave. 256 x 384 with
+// 4 x 2 waves: one workgroup of 8 waves per CU using all 160 KB of LDS (two
+// stages of 80 KB), 64 x 192 per wave (12 accumulator blocks, ~236 VGPRs, no
+// spills); per MFMA it stages 5/8 of the bytes of the 128 x 128 tile through
+// LDS and reads 2/3 of its LDS operand bytes.
 template <int E, int TBN, int TBM, int WN, int WM, int KS, int NS>
 __global__ __launch_bounds__(64 * WN * WM) __attribute__((amdgpu_waves_per_eu(2)))
 void gemm32_kernel(GemmArgs g) {
@@ -515,12 +517,14 @@ int launch_gemm(const GemmArgs& g, hipStream_t s, const char* what) {
   if (g.k % K2 == 0 && long(g.m) * g.k < (1L << 30) && long(g.n) * g.k < (1L << 30)) {
     const long tiles = long((g.n + TB - 1) / TB) * ((g.m + TB - 1) / TB);
     if (tiles > (1L << 31) - 1) return set_error(SFL_ERR_UNSUPPORTED, "%s: too many tiles", what);
-    // 256 x 256 tiles where they still give every CU several workgroups.
-    const long big = long((g.n + 255) / 256) * ((g.m + 255) / 256);
-    if (big >= 512)
-      // (A ring of 4 stages of K = 32 in the same 128 KB measured 6% slower:
-      // the deeper prefetch does not pay for twice the steps and barriers.)
-      hipLaunchKernelGGL((gemm32_kernel<E, 256, 256, 4, 2, 64, 2>), dim3(unsigned(big)), dim3(512), 0, s, g);
+    // 256 x 384 tiles where they still give every CU more than one workgroup
+    // (measured against 256 x 256 on the 324M prefill shapes, bit-identical
+    // outputs: q/k/v 437 -> 421 us, output_proj 171 -> 145, w1/w3 640 -> 603,
+    // w2 330 -> 308; 2 x 4 waves of 128 x 96 and a ring of 4 stages of K = 32
+    // were no better).
+    const long big = long((g.n + 255) / 256) * ((g.m + 383) / 384);
+    if (big >= 320)
+      hipLaunchKernelGGL((gemm32_kernel<E, 256, 384, 4, 2, 64, 2>), dim3(unsigned(big)), dim3(512), 0, s, g);
     else
       hipLaunchKernelGGL((gemm32_kernel<E, 128, 128, 2, 2, 64, 2>), dim3(unsigned(tiles)), dim3(kThreads), 0, s, g);
     return check_launch(what);

@@ -36,7 +36,7 @@ def test_gemm_matches_fp32_matmul(m, n, k):
     torch.testing.assert_close(ob.float().cpu(), ref.bfloat16().float(), atol=1e-2, rtol=1e-2)
 
 
-# Grids of >= 512 tiles of 256 x 256 take the 256 x 256 kernel with its ring
+# Grids of >= 320 tiles of 256 x 384 take the 256 x 384 kernel with its ring
 # of LDS stages: K of 64 (fewer steps than stages), 192 and 2752 (the model's
 # d_ff), ragged M and N. Sampled token rows keep the CPU reference small.
 @pytest.mark.parametrize("m,n,k", [(4100, 8200, 64), (4100, 8200, 192), (2304, 14400, 2752)])
@@ -69,7 +69,7 @@ def _bf16_out(shape, aligned):
     return out
 
 
-# The bf16 epilogues of the 256 x 256 kernel (q/k/v + RoPE + cache write,
+# The bf16 epilogues of the 256 x 384 kernel (q/k/v + RoPE + cache write,
 # SwiGLU, plain bf16 output) with ragged M (token tiles spanning two batch
 # rows), a ragged N, and outputs that are / are not 16-byte aligned.
 @pytest.mark.parametrize("aligned", [True, False])
