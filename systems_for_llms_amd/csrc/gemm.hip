@@ -80,6 +80,23 @@ __device__ __forceinline__ QkvFeat qkv_feat(const GemmArgs& g, int n) {
   const int head = f / g.head_dim;
   return QkvFeat{section, head, f - head * g.head_dim};
 }
+// qkv_feat of feature nt + off from base = qkv_feat(nt), 0 <= off < 32: the
+// head changes at most twice within 32 features (head dims >= 16), so two
+// compare-and-wrap steps replace the two integer divisions.
+__device__ __forceinline__ QkvFeat qkv_feat_at(const GemmArgs& g, const QkvFeat& base, int off) {
+  QkvFeat f{base.section, base.head, base.dim + off};
+#pragma unroll
+  for (int w = 0; w < 2; ++w) {
+    if (f.dim >= g.head_dim) {
+      f.dim -= g.head_dim;
+      if (++f.head == g.heads) {
+        f.head = 0;
+        ++f.section;
+      }
+    }
+  }
+  return f;
+}
 __device__ __forceinline__ QkvTok qkv_tok(const GemmArgs& g, int m) {
   const int b = m / g.seq;
   return QkvTok{b, m - b * g.seq};
@@ -420,6 +437,12 @@ void gemm32_kernel(GemmArgs g) {
 #pragma unroll
     for (int i = 0; i < NBN; ++i) {
       const int nt = n0 + (TBN / WN) * wn + 32 * i;
+      // One division pair per 32-feature block; the lane's features derive from
+      // it. With head dims that are multiples of 32 the block is one head of one
+      // section: its features share the destination row.
+      const QkvFeat fb = E == G_QKV ? qkv_feat(g, nt) : QkvFeat{};
+      const bool blk = E == G_QKV && g.head_dim % 32 == 0;
+      uint16_t* const base = blk ? qkv_dst(g, fb, tok) : nullptr;
       if constexpr (E == G_SWIGLU) {
         // W1/W3 interleaved in blocks of 8 rows: groups q = 0, 2 are W1 features,
         // q + 1 the matching W3 features, all in this lane. Hidden features
@@ -463,7 +486,9 @@ void gemm32_kernel(GemmArgs g) {
           for (int r = 0; r < 2; ++r) {
             float y[4] = {acc[i][j][4 * (q + r)], acc[i][j][4 * (q + r) + 1], acc[i][j][4 * (q + r) + 2],
                           acc[i][j][4 * (q + r) + 3]};
-            feat[r] = E == G_QKV ? qkv_feat(g, nt + 8 * (q + r) + 4 * hf) : QkvFeat{};
+            feat[r] = E != G_QKV ? QkvFeat{}
+                      : blk ? QkvFeat{fb.section, fb.head, fb.dim + 8 * (q + r) + 4 * hf}
+                            : qkv_feat_at(g, fb, 8 * (q + r) + 4 * hf);
             if constexpr (E == G_QKV) rope4(g, y, feat[r], tok);
             pk[r][0] = pack_bf16(y[0], y[1]);
             pk[r][1] = pack_bf16(y[2], y[3]);
@@ -472,7 +497,7 @@ void gemm32_kernel(GemmArgs g) {
             const uint4 v8 = pair8(pk[0], pk[1]);
             if (m < g.m) {
               const int f = nt + 8 * q + 8 * hf;  // first of this lane's 8 features
-              uint16_t* dst = E == G_QKV ? qkv_dst(g, qkv_feat(g, f), tok)
+              uint16_t* dst = E == G_QKV ? (blk ? base + 8 * q + 8 * hf : qkv_dst(g, qkv_feat_at(g, fb, 8 * q + 8 * hf), tok))
                                          : static_cast<uint16_t*>(g.c) + long(m) * g.n + f;
               *reinterpret_cast<uint4*>(dst) = v8;
             }
@@ -500,7 +525,7 @@ void gemm32_kernel(GemmArgs g) {
         for (int q = 0; q < 4; ++q) {
           const f32x4 v = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
           // store_tile's feature index is nt + 4 * grp: grp = 2q + hf.
-          const QkvFeat feat = E == G_QKV ? qkv_feat(g, nt + 8 * q + 4 * hf) : QkvFeat{};
+          const QkvFeat feat = E == G_QKV ? qkv_feat_at(g, fb, 8 * q + 4 * hf) : QkvFeat{};
           store_tile<E>(g, v, nt, 2 * q + hf, m, feat, tok);
         }
       }

@@ -118,6 +118,41 @@ def test_gemm_large_grid_bf16_epilogues(aligned):
     _ulp_close("plain bf16", plain.cpu()[rows], om._round(a[rows].float() @ wp.float().t(), torch.bfloat16), 2e-3)
 
 
+# Head dims that are not multiples of 32: a 32-feature MFMA block then holds
+# two heads (16) or straddles a head boundary (48). The 256 x 384 kernel
+# (large grids), the 128 x 128 one, and for d_model 144 (K % 64 != 0, the
+# q | k | v boundaries inside a 32-feature block) the 16x16 kernel.
+@pytest.mark.parametrize("dk,h,b,t", [(16, 64, 4, 2600), (48, 16, 4, 3500), (16, 8, 2, 100), (48, 3, 3, 70)])
+def test_gemm_qkv_rope_head_dims_across_feature_blocks(dk, h, b, t):
+    d, m, cap = dk * h, b * t, t + 16
+    g = torch.Generator().manual_seed(dk * 1000 + t)
+    a = torch.randn((m, d), generator=g).bfloat16()
+    wqkv = (torch.randn((3 * d, d), generator=g) * 0.03).bfloat16()
+    cos, sin = om.rope_tables(10000.0, dk, cap)
+    q = torch.zeros((b, h, t, dk), device="cuda", dtype=torch.bfloat16)
+    kc = torch.zeros((b, h, cap, dk), device="cuda", dtype=torch.bfloat16)
+    vc = torch.zeros_like(kc)
+    gcos, gsin, ga, gw = cos.cuda(), sin.cuda(), a.cuda(), wqkv.cuda()
+    _lib.call("sfl_gemm_qkv_rope", ga.data_ptr(), gw.data_ptr(), m, t, d, h, gcos.data_ptr(), gsin.data_ptr(),
+              q.data_ptr(), kc.data_ptr(), vc.data_ptr(), cap, _lib.stream_handle())
+    torch.cuda.synchronize()
+    rows = _sample_rows(m, g) if m > 400 else torch.arange(m)
+    bi, ti = rows // t, rows % t
+    proj = a[rows].float() @ wqkv.float().t()
+    c, s = cos[ti][:, None, :], sin[ti][:, None, :]
+
+    def rot(x):
+        out = torch.empty_like(x)
+        out[..., 0::2] = x[..., 0::2] * c - x[..., 1::2] * s
+        out[..., 1::2] = x[..., 0::2] * s + x[..., 1::2] * c
+        return out
+    qr, kr, vr = (proj[:, i * d:(i + 1) * d].view(-1, h, dk) for i in range(3))
+    _ulp_close(f"q (RoPE, dk {dk})", q.cpu()[bi, :, ti], om._round(rot(qr), torch.bfloat16), 2e-3)
+    _ulp_close(f"k cache (RoPE, dk {dk})", kc.cpu()[bi, :, ti], om._round(rot(kr), torch.bfloat16), 2e-3)
+    _ulp_close(f"v cache (dk {dk})", vc.cpu()[bi, :, ti], om._round(vr, torch.bfloat16), 2e-3)
+    assert not kc[:, :, t:].any() and not vc[:, :, t:].any(), "wrote cache rows past the sequence"
+
+
 # d % 4 == 0 and d <= 2048 take the one-wave-per-row kernel (m not a multiple
 # of its 4 rows per workgroup included); other widths the workgroup-per-row one.
 @pytest.mark.parametrize("m,d", [(1, 64), (7, 96), (130, 1024), (33, 2048), (5, 2052), (9, 1030)])
