@@ -123,6 +123,15 @@ __device__ __forceinline__ uint16_t* qkv_dst(const GemmArgs& g, const QkvFeat& q
   return cache + ((long(qt.b) * g.heads + qf.head) * g.cap + qt.t) * g.head_dim + qf.dim;
 }
 
+// silu(a) * c = a * c / (1 + e^-a) with the hardware base-2 exponential and
+// reciprocal (e^-a = 2^(-a log2 e); each ~1 ulp): the bf16 rounding of the
+// result dominates their error. a -> -inf gives 2^+inf = inf and a zero
+// reciprocal (a signed zero), as the exact form does.
+__device__ __forceinline__ float silu_mul(float a, float c) {
+  const float e = __builtin_amdgcn_exp2f(a * -1.4426950408889634f);
+  return a * c * __builtin_amdgcn_rcpf(1.f + e);
+}
+
 // Two packed groups of 4 bf16 outputs, A (lane-local features f .. f+3) and
 // B (f+8 .. f+11), where lane l ^ 32 holds f+4 .. f+7 and f+12 .. f+15: one
 // v_permlane32_swap per dword gives lanes 0..31 features f .. f+7 (own A,
@@ -152,7 +161,7 @@ __device__ __forceinline__ void store_tile(const GemmArgs& g, const f32x4& v, in
     if (f >= g.n / 2) return;
     float h[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) h[e] = y[e] / (1.f + expf(-y[e])) * c3[e];
+    for (int e = 0; e < 4; ++e) h[e] = silu_mul(y[e], c3[e]);
     *reinterpret_cast<uint2*>(g.h_out + long(m) * (g.n / 2) + f) = make_uint2(pack_bf16(h[0], h[1]), pack_bf16(h[2], h[3]));
   } else {
     if (m >= g.m || n >= g.n) return;
@@ -456,7 +465,7 @@ void gemm32_kernel(GemmArgs g) {
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const float a1 = acc[i][j][4 * q + e], a3 = acc[i][j][4 * q + 4 + e];
-            h[e] = a1 / (1.f + expf(-a1)) * a3;
+            h[e] = silu_mul(a1, a3);
           }
           pk[q / 2][0] = pack_bf16(h[0], h[1]);
           pk[q / 2][1] = pack_bf16(h[2], h[3]);
