@@ -299,14 +299,25 @@ __global__ __launch_bounds__(kWaves * kWave) void linear_kernel(LinearArgs a) {
   const int nl = min(n, a.n - 4);
   float4 pre_x = make_float4(0.f, 0.f, 0.f, 0.f);
   float2 pre_c = make_float2(0.f, 0.f), pre_s = make_float2(0.f, 0.f);
+  // QKV: where this lane's features go (section 0 q, 1 k, 2 v), worked out while the loads fly.
+  int section = 0;
+  void* qkv_dst = nullptr;
   if (wave == 0) {
     if constexpr (E == EPI_RESIDUAL) {
       if (a.ksplit == 1) pre_x = *reinterpret_cast<const float4*>(a.x + long(row) * a.n + nl);
     } else if constexpr (E == EPI_QKV) {
-      const int half = a.head_dim / 2;
-      const long at = long(pre_p) * half + (nl % a.d_model % a.head_dim) / 2;
+      section = nl / a.d_model;
+      const int f = nl - section * a.d_model;
+      const int head = f / a.head_dim;
+      const int dim = f - head * a.head_dim;
+      const long at = long(pre_p) * (a.head_dim / 2) + dim / 2;
       pre_c = *reinterpret_cast<const float2*>(a.cos_t + at);
       pre_s = *reinterpret_cast<const float2*>(a.sin_t + at);
+      if (section == 0)
+        qkv_dst = static_cast<float*>(a.q_out) + (long(row) * a.heads + head) * a.head_dim + dim;
+      else
+        qkv_dst = static_cast<T*>(section == 1 ? a.k_cache : a.v_cache) +
+                  ((long(row) * a.heads + head) * a.cap + pre_p) * a.head_dim + dim;
     }
   }
 
@@ -427,14 +438,10 @@ __global__ __launch_bounds__(kWaves * kWave) void linear_kernel(LinearArgs a) {
   } else if constexpr (E == EPI_SWIGLU) {
     float h[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) h[i] = v1[i] / (1.f + expf(-v1[i])) * v3[i];
+    for (int i = 0; i < 4; ++i)
+      h[i] = v1[i] * v3[i] * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(v1[i] * -1.4426950408889634f));
     store_act4<T>(static_cast<unsigned char*>(a.h_out), b, n, a.n, h);
   } else {  // EPI_QKV
-    const int section = n / a.d_model;  // 0 q, 1 k, 2 v
-    const int f = n % a.d_model;
-    const int head = f / a.head_dim;
-    const int dim = f % a.head_dim;
-    const int p = pre_p;
     float y[4] = {v1[0], v1[1], v1[2], v1[3]};
     if (section < 2) {
       // Pairs (dim, dim+1) and (dim+2, dim+3) use table columns dim/2 and dim/2+1.
@@ -446,13 +453,8 @@ __global__ __launch_bounds__(kWaves * kWave) void linear_kernel(LinearArgs a) {
         y[i + 1] = e * sn[i / 2] + o * c[i / 2];
       }
     }
-    if (section == 0) {
-      float* dst = static_cast<float*>(a.q_out) + (long(b) * a.heads + head) * a.head_dim + dim;
-      *reinterpret_cast<float4*>(dst) = make_float4(y[0], y[1], y[2], y[3]);
-    } else {
-      T* cache = static_cast<T*>(section == 1 ? a.k_cache : a.v_cache);
-      store4<T>(cache + ((long(b) * a.heads + head) * a.cap + p) * a.head_dim + dim, y);
-    }
+    if (section == 0) *static_cast<float4*>(qkv_dst) = make_float4(y[0], y[1], y[2], y[3]);
+    else store4<T>(static_cast<T*>(qkv_dst), y);
   }
 }
 
