@@ -63,8 +63,12 @@ __device__ __forceinline__ uint4 keep16(const uint4& v, bool keep) {
   return make_uint4(keep ? v.x : 0u, keep ? v.y : 0u, keep ? v.z : 0u, keep ? v.w : 0u);
 }
 
+// Two values rounded to bf16 (round to nearest even, as f32_to_bf16_bits)
+// with one v_cvt_pk_bf16_f32.
+typedef __bf16 bf16x2_pk __attribute__((ext_vector_type(2)));
+typedef float f32x2_pk __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
-  return uint32_t(f32_to_bf16_bits(lo)) | (uint32_t(f32_to_bf16_bits(hi)) << 16);
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_pk{lo, hi}), bf16x2_pk));
 }
 
 // Where a lane's 4 QKV features and its token go: section (0 q, 1 k, 2 v),
