@@ -419,6 +419,32 @@ void gemm32_kernel(GemmArgs g) {
     for (int j = 0; j < NBM; ++j)
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+  // Residual accumulation into fp32 C (x += A W^T): the accumulators start
+  // from the old C values, loaded now, while the first stages are in flight,
+  // so the epilogue only stores. (Unconditional loads from clamped addresses;
+  // the values of rows / columns past C are never stored.)
+  const bool acc_c = E == G_PLAIN && g.c_f32 && g.accumulate && (g.n & 3) == 0;
+  if constexpr (E == G_PLAIN) {
+    if (acc_c) {
+      const float* c = static_cast<const float*>(g.c);
+#pragma unroll
+      for (int j = 0; j < NBM; ++j) {
+        const long mr = min(m0 + (TBM / WM) * wm + 32 * j + l32, g.m - 1);
+#pragma unroll
+        for (int i = 0; i < NBN; ++i) {
+          const int nt = n0 + (TBN / WN) * wn + 32 * i;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const float4 o = *reinterpret_cast<const float4*>(c + mr * g.n + min(nt + 8 * q + 4 * hf, g.n - 4));
+            acc[i][j][4 * q] = o.x;
+            acc[i][j][4 * q + 1] = o.y;
+            acc[i][j][4 * q + 2] = o.z;
+            acc[i][j][4 * q + 3] = o.w;
+          }
+        }
+      }
+    }
+  }
 
   // NS LDS stages in a ring: step kt computes from stage kt % NS while the
   // loads of the next NS - 1 steps are in flight. At step kt the wave waits
@@ -440,6 +466,28 @@ void gemm32_kernel(GemmArgs g) {
   }
 #undef SFL_G32_COMPUTE
 #undef SFL_G32_ISSUE
+
+  if constexpr (E == G_PLAIN) {
+    if (acc_c) {
+      float* const c = static_cast<float*>(g.c);
+#pragma unroll
+      for (int j = 0; j < NBM; ++j) {
+        const int m = m0 + (TBM / WM) * wm + 32 * j + l32;
+#pragma unroll
+        for (int i = 0; i < NBN; ++i) {
+          const int nt = n0 + (TBN / WN) * wn + 32 * i;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int n = nt + 8 * q + 4 * hf;
+            if (m < g.m && n < g.n)
+              *reinterpret_cast<float4*>(c + long(m) * g.n + n) =
+                  make_float4(acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);
+          }
+        }
+      }
+      return;
+    }
+  }
 
   // acc[i][j][4q + e] holds feature n0 + (TBN/WN)wn + 32i + 8q + 4hf + e of
   // token m0 + (TBM/WM)wm + 32j + l32.
