@@ -52,6 +52,27 @@ def test_gemm_large_grid_matches_fp32_matmul(m, n, k):
     torch.testing.assert_close(out[rows.cuda()].cpu(), ref, atol=1e-3 * k ** 0.5, rtol=1e-4)
 
 
+# The residual form (fp32 C += A W^T) on the same large ragged grids: the
+# accumulators start from the old C (loads clamped at the matrix edges), and
+# nothing outside C is written (guard rows before and after it).
+@pytest.mark.parametrize("m,n,k", [(4100, 8200, 64), (2304, 14400, 2752)])
+def test_gemm_large_grid_accumulates_into_fp32(m, n, k):
+    g = torch.Generator().manual_seed(m + n + k + 1)
+    a = torch.randn((m, k), generator=g).bfloat16()
+    w = torch.randn((n, k), generator=g).bfloat16()
+    c0 = torch.randn((m, n), generator=g)
+    rows = torch.cat([torch.arange(0, 40), torch.randint(0, m, (200,), generator=g), torch.arange(m - 40, m)])
+    ref = c0[rows] + a[rows].float() @ w.float().t()
+    ga, gw = a.cuda(), w.cuda()
+    c = torch.full(((m + 2) * n,), 7.0, device="cuda")
+    cv = c[n:n + m * n].view(m, n)  # one guard row before C, one after
+    cv.copy_(c0.cuda())
+    _lib.call("sfl_gemm_bf16", ga.data_ptr(), gw.data_ptr(), cv.data_ptr(), m, n, k, 0, 1, _lib.stream_handle())
+    torch.cuda.synchronize()
+    torch.testing.assert_close(cv[rows.cuda()].cpu(), ref, atol=1e-3 * k ** 0.5, rtol=1e-4)
+    assert bool((c[:n] == 7.0).all()) and bool((c[n + m * n:] == 7.0).all()), "wrote outside C"
+
+
 def _sample_rows(m, g):
     return torch.cat([torch.arange(0, 40), torch.randint(0, m, (200,), generator=g), torch.arange(m - 40, m)])
 
