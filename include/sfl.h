@@ -321,6 +321,41 @@ int sfl_embed_rows(const int64_t* ids, const void* emb, float* x, int m, int d_m
 int sfl_rmsnorm_rows(const float* x, const void* w, void* out_bf16, int m, int d_model, int dtype,
                      void* stream);
 
+/* ---- prefill with the RMSNorm folded into the neighbouring GEMMs -------------
+ * RMSNorm(x) W^T = (1 / rms(x)) ((x * w) W^T) per token: the norm's input side
+ * is xg = bf16(x * w) plus a per-token scale r = 1 / rms(x) that the consuming
+ * GEMM applies to its fp32 products, and the residual GEMM producing x writes
+ * xg for the next norm and per-token sums of squares over each 128-feature
+ * part, so no separate pass re-reads x. Same layers as above (layers.py:133-141
+ * feeding attention.py:160-162 and layers.py:114-115); bf16, d_model and d_ff
+ * multiples of 64 (the 32x32 MFMA kernels).
+ */
+
+/* act_xg[r] = bf16(x[r] * w), rscale[r] = 1 / sqrt(mean(x[r]^2) + 1e-5); w bf16
+ * (dtype must be SFL_DTYPE_BF16), d_model <= 2048. */
+int sfl_rmsnorm_rows_scaled(const float* x, const void* w, void* act_xg, float* rscale, int m, int d_model,
+                            int dtype, void* stream);
+
+/* x += A W^T (fp32, as sfl_gemm_bf16 with accumulate) and, from the updated
+ * x: act_xg = bf16(x * gain_next) and ss_parts[p][r] = sum of x[r][f]^2 over
+ * the features f of part p = f / 128 (ceil(n / 128) parts). n % 4 == 0. */
+int sfl_gemm_residual_norm(const void* a, const void* w, float* x, int m, int n, int k, const void* gain_next,
+                           void* act_xg, float* ss_parts, void* stream);
+
+/* rscale[r] = 1 / sqrt(sum_p ss_parts[p][r] / d_model + 1e-5), parts summed in order. */
+int sfl_norm_scale(const float* ss_parts, int parts, int m, int d_model, float* rscale, void* stream);
+
+/* sfl_gemm_qkv_rope on act_xg, each token's products scaled by rscale[r]
+ * before RoPE and the bf16 stores. */
+int sfl_gemm_qkv_rope_scaled(const void* a_xg, const void* w_qkv, const float* rscale, int m, int seq,
+                             int d_model, int heads, const float* cos_t, const float* sin_t, void* q_out,
+                             void* k_cache, void* v_cache, int capacity, void* stream);
+
+/* sfl_gemm_swiglu on act_xg, both products of a token scaled by rscale[r]
+ * before silu(.) * (.). */
+int sfl_gemm_swiglu_scaled(const void* a_xg, const void* w13_interleaved, const float* rscale, void* h_out,
+                           int m, int d_ff, int k, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

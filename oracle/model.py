@@ -151,6 +151,25 @@ def _round(t: torch.Tensor, dtype) -> torch.Tensor:
     return t if dtype is None else t.to(dtype).to(t.dtype)
 
 
+def _norm_input(x, weight, act_dtype, fold):
+    """The GEMM input made from ``rmsnorm(x, weight)`` and the per-token factor for its products.
+
+    ``fold`` (not in the reference; the storage-format floor of a prefill that
+    folds the norm into its GEMMs): the stored input is ``x * weight`` and the
+    products are scaled by ``r = 1 / sqrt(mean(x^2) + eps)`` afterwards -- the
+    same value in exact arithmetic, rounded at another point. Otherwise the
+    norm's output itself is stored and the factor is ``None`` (one).
+    """
+    if not fold:
+        return _round(rmsnorm(x, weight), act_dtype), None
+    r = 1.0 / torch.sqrt(torch.mean(x * x, dim=-1, keepdim=True) + EPS)
+    return _round(x * weight, act_dtype), r
+
+
+def _scaled(y, r):
+    return y if r is None else y * r
+
+
 def _layer(sd, prefix, x, heads, cos, sin, positions, mask, kv_dtype=None, act_dtype=None):
     h = _round(rmsnorm(x, sd[prefix + "attn_norm.weight"]), act_dtype)
     q = _split_heads(_linear(h, sd[prefix + "attn.q_proj.weight"]), heads)
@@ -237,8 +256,12 @@ class KVCacheOracle:
         self.length = 0
 
     @torch.no_grad()
-    def step(self, tokens: torch.Tensor, act_dtype=None) -> torch.Tensor:
-        """Append ``tokens [B, T]`` at the current length; return logits ``[B, T, V]``."""
+    def step(self, tokens: torch.Tensor, act_dtype=None, norm_fold: bool = False) -> torch.Tensor:
+        """Append ``tokens [B, T]`` at the current length; return logits ``[B, T, V]``.
+
+        ``norm_fold`` stores the layers' RMSNorm inputs as ``_norm_input`` with
+        ``fold`` does (the final norm stays as it is).
+        """
         sd, cfg = self.sd, self.config
         t = tokens.shape[1]
         start = self.length
@@ -248,18 +271,20 @@ class KVCacheOracle:
         x = sd["token_embeddings.weight"][tokens]
         for layer in range(cfg.num_layers):
             p = f"layers.{layer}."
-            h = _round(rmsnorm(x, sd[p + "attn_norm.weight"]), act_dtype)
-            q = rope(_split_heads(_linear(h, sd[p + "attn.q_proj.weight"]), self.heads), self.cos, self.sin, positions)
-            k = rope(_split_heads(_linear(h, sd[p + "attn.k_proj.weight"]), self.heads), self.cos, self.sin, positions)
-            v = _split_heads(_linear(h, sd[p + "attn.v_proj.weight"]), self.heads)
+            h, r = _norm_input(x, sd[p + "attn_norm.weight"], act_dtype, norm_fold)
+            q = rope(_split_heads(_scaled(_linear(h, sd[p + "attn.q_proj.weight"]), r), self.heads), self.cos,
+                     self.sin, positions)
+            k = rope(_split_heads(_scaled(_linear(h, sd[p + "attn.k_proj.weight"]), r), self.heads), self.cos,
+                     self.sin, positions)
+            v = _split_heads(_scaled(_linear(h, sd[p + "attn.v_proj.weight"]), r), self.heads)
             self.k[layer, :, :, start:total] = _round(k, self.kv_dtype)
             self.v[layer, :, :, start:total] = _round(v, self.kv_dtype)
             a = attention_core(_round(q, act_dtype), self.k[layer, :, :, :total], self.v[layer, :, :, :total], mask,
                                act_dtype)
             x = x + _linear(_round(_merge_heads(a), act_dtype), sd[p + "attn.output_proj.weight"])
-            h = _round(rmsnorm(x, sd[p + "ffn_norm.weight"]), act_dtype)
-            a1 = _linear(h, sd[p + "ffn.w1.weight"])
-            g = _round(a1 * torch.sigmoid(a1) * _linear(h, sd[p + "ffn.w3.weight"]), act_dtype)
+            h, r = _norm_input(x, sd[p + "ffn_norm.weight"], act_dtype, norm_fold)
+            a1 = _scaled(_linear(h, sd[p + "ffn.w1.weight"]), r)
+            g = _round(a1 * torch.sigmoid(a1) * _scaled(_linear(h, sd[p + "ffn.w3.weight"]), r), act_dtype)
             x = x + _linear(g, sd[p + "ffn.w2.weight"])
         self.length = total
         return _linear(_round(rmsnorm(x, sd["ln_final.weight"]), act_dtype), sd["lm_head.weight"])

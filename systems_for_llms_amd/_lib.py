@@ -46,6 +46,11 @@ SIGNATURES: dict[str, list] = {
     "sfl_gemm_swiglu": [P, P, P, c_int, c_int, c_int, P],
     "sfl_embed_rows": [P, P, P, c_int, c_int, c_int, P],
     "sfl_rmsnorm_rows": [P, P, P, c_int, c_int, c_int, P],
+    "sfl_rmsnorm_rows_scaled": [P, P, P, P, c_int, c_int, c_int, P],
+    "sfl_gemm_residual_norm": [P, P, P, c_int, c_int, c_int, P, P, P, P],
+    "sfl_norm_scale": [P, c_int, c_int, c_int, P, P],
+    "sfl_gemm_qkv_rope_scaled": [P, P, P, c_int, c_int, c_int, c_int, P, P, P, P, P, c_int, P],
+    "sfl_gemm_swiglu_scaled": [P, P, P, P, c_int, c_int, c_int, P],
 }
 
 _LIB = None

@@ -48,6 +48,15 @@ struct GemmArgs {
   uint16_t* v_cache;
   // SWIGLU
   uint16_t* h_out;     // [M, N/2]
+  // PLAIN residual (fp32 C += A W^T) that also prepares the next RMSNorm
+  // (norm_gain null: not): norm_act = bf16(C * gain), and per token and
+  // 128-feature part the sum of C^2 in norm_ss [ceil(N / 128)][M].
+  const uint16_t* norm_gain;
+  uint16_t* norm_act;
+  float* norm_ss;
+  // QKV / SWIGLU fed by such an input: the products are scaled by
+  // row_scale[m] = 1 / rms of token m (null: not).
+  const float* row_scale;
   // Every bf16 output base is 16-byte aligned: the 32x32 kernel then stores
   // 8 consecutive outputs per lane (lane pairs exchange halves first).
   int vec16;
@@ -446,6 +455,18 @@ void gemm32_kernel(GemmArgs g) {
     }
   }
 
+  // Row scales of the normalized input (q/k/v, SwiGLU), loaded while the
+  // first stages are in flight.
+  float rsc[NBM];
+#pragma unroll
+  for (int j = 0; j < NBM; ++j) rsc[j] = 1.f;
+  if constexpr (E != G_PLAIN) {
+    if (g.row_scale) {
+#pragma unroll
+      for (int j = 0; j < NBM; ++j) rsc[j] = g.row_scale[min(m0 + (TBM / WM) * wm + 32 * j + l32, g.m - 1)];
+    }
+  }
+
   // NS LDS stages in a ring: step kt computes from stage kt % NS while the
   // loads of the next NS - 1 steps are in flight. At step kt the wave waits
   // only for stage kt's loads (the younger stages' CPW each may stay
@@ -470,18 +491,78 @@ void gemm32_kernel(GemmArgs g) {
   if constexpr (E == G_PLAIN) {
     if (acc_c) {
       float* const c = static_cast<float*>(g.c);
+      const bool norm = g.norm_gain != nullptr;  // uniform
+      // The next norm's gains for this lane's features (one batch of loads,
+      // before any store).
+      uint2 gw[NBN][4];
+      if (norm) {
+#pragma unroll
+        for (int i = 0; i < NBN; ++i)
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            gw[i][q] = *reinterpret_cast<const uint2*>(
+                g.norm_gain + min(n0 + (TBN / WN) * wn + 32 * i + 8 * q + 4 * hf, g.n - 4));
+      }
+      float ssq[NBM];
 #pragma unroll
       for (int j = 0; j < NBM; ++j) {
         const int m = m0 + (TBM / WM) * wm + 32 * j + l32;
+        ssq[j] = 0.f;
 #pragma unroll
         for (int i = 0; i < NBN; ++i) {
           const int nt = n0 + (TBN / WN) * wn + 32 * i;
+          uint32_t pk[4][2];  // bf16(x * gain) of features nt + 8q + 4hf + (0..3)
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
             const int n = nt + 8 * q + 4 * hf;
-            if (m < g.m && n < g.n)
-              *reinterpret_cast<float4*>(c + long(m) * g.n + n) =
-                  make_float4(acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);
+            const float4 v = make_float4(acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
+                                         acc[i][j][4 * q + 3]);
+            const bool in = m < g.m && n < g.n;
+            if (in) *reinterpret_cast<float4*>(c + long(m) * g.n + n) = v;
+            if (norm) {
+              pk[q][0] = pack_bf16(v.x * bf16_lo(gw[i][q].x), v.y * bf16_hi(gw[i][q].x));
+              pk[q][1] = pack_bf16(v.z * bf16_lo(gw[i][q].y), v.w * bf16_hi(gw[i][q].y));
+              if (in) ssq[j] += (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w);
+            }
+          }
+          if (norm) {
+            if (g.vec16) {  // 8 consecutive features per lane (every lane swaps)
+#pragma unroll
+              for (int q = 0; q < 4; q += 2) {
+                const uint4 o = pair8(pk[q], pk[q + 1]);
+                const int n = nt + 8 * q + 8 * hf;
+                if (m < g.m && n < g.n) *reinterpret_cast<uint4*>(g.norm_act + long(m) * g.n + n) = o;
+              }
+            } else {
+#pragma unroll
+              for (int q = 0; q < 4; ++q) {
+                const int n = nt + 8 * q + 4 * hf;
+                if (m < g.m && n < g.n)
+                  *reinterpret_cast<uint2*>(g.norm_act + long(m) * g.n + n) = make_uint2(pk[q][0], pk[q][1]);
+              }
+            }
+          }
+        }
+      }
+      if (norm) {
+        // Sum of squares per token over each 128-feature part: this lane's 32
+        // features, its partner lane's (l ^ 32: the other 4 of each 8), then
+        // the wave pair (wn, wn ^ 1) covering the part, in that order.
+        float* const part_s = reinterpret_cast<float*>(&st[0]);  // [WN][TBM] (the stages are free now)
+        __syncthreads();  // every wave has read the last stage
+#pragma unroll
+        for (int j = 0; j < NBM; ++j) {
+          const float t = ssq[j] + __shfl_xor(ssq[j], 32, kWave);
+          if (hf == 0) part_s[wn * TBM + (TBM / WM) * wm + 32 * j + l32] = t;
+        }
+        __syncthreads();
+        static_assert(TBN / WN == 64, "two waves per 128-feature part");
+        const int part = (n0 + (TBN / WN) * wn) / 128;
+        if ((wn & 1) == 0 && part * 128 < g.n) {
+          for (int r = lane; r < TBM / WM; r += kWave) {
+            const int row = (TBM / WM) * wm + r;
+            const int m = m0 + row;
+            if (m < g.m) g.norm_ss[long(part) * g.m + m] = part_s[wn * TBM + row] + part_s[(wn + 1) * TBM + row];
           }
         }
       }
@@ -516,7 +597,7 @@ void gemm32_kernel(GemmArgs g) {
           float h[4];
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            const float a1 = acc[i][j][4 * q + e], a3 = acc[i][j][4 * q + 4 + e];
+            const float a1 = acc[i][j][4 * q + e] * rsc[j], a3 = acc[i][j][4 * q + 4 + e] * rsc[j];
             h[e] = silu_mul(a1, a3);
           }
           pk[q / 2][0] = pack_bf16(h[0], h[1]);
@@ -545,8 +626,8 @@ void gemm32_kernel(GemmArgs g) {
           QkvFeat feat[2];
 #pragma unroll
           for (int r = 0; r < 2; ++r) {
-            float y[4] = {acc[i][j][4 * (q + r)], acc[i][j][4 * (q + r) + 1], acc[i][j][4 * (q + r) + 2],
-                          acc[i][j][4 * (q + r) + 3]};
+            float y[4] = {acc[i][j][4 * (q + r)] * rsc[j], acc[i][j][4 * (q + r) + 1] * rsc[j],
+                          acc[i][j][4 * (q + r) + 2] * rsc[j], acc[i][j][4 * (q + r) + 3] * rsc[j]};
             feat[r] = E != G_QKV ? QkvFeat{}
                       : blk ? QkvFeat{fb.section, fb.head, fb.dim + 8 * (q + r) + 4 * hf}
                             : qkv_feat_at(g, fb, 8 * (q + r) + 4 * hf);
@@ -584,7 +665,8 @@ void gemm32_kernel(GemmArgs g) {
       } else {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          const f32x4 v = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+          const f32x4 v = {acc[i][j][4 * q] * rsc[j], acc[i][j][4 * q + 1] * rsc[j], acc[i][j][4 * q + 2] * rsc[j],
+                           acc[i][j][4 * q + 3] * rsc[j]};
           // store_tile's feature index is nt + 4 * grp: grp = 2q + hf.
           const QkvFeat feat = E == G_QKV ? qkv_feat_at(g, fb, 8 * q + 4 * hf) : QkvFeat{};
           store_tile<E>(g, v, nt, 2 * q + hf, m, feat, tok);
@@ -650,9 +732,11 @@ __global__ __launch_bounds__(256) void rmsnorm_rows_kernel(const float* x, const
 // of squares is a wave reduction (no LDS, no barrier), and each lane stores
 // four bf16 values at a time.
 constexpr int kNormVec = 8;
-template <typename T>
+// kScaled: out = bf16(x * w) and rscale[row] = 1 / rms(x), for a consumer GEMM
+// that applies the scale to its products.
+template <typename T, bool kScaled = false>
 __global__ __launch_bounds__(256) void rmsnorm_rows_wave_kernel(const float* x, const T* w, uint16_t* out, int m,
-                                                               int d) {
+                                                               int d, float* rscale = nullptr) {
   const long row = long(blockIdx.x) * 4 + threadIdx.x / kWave;
   const int lane = threadIdx.x % kWave;
   if (row >= m) return;
@@ -669,15 +753,32 @@ __global__ __launch_bounds__(256) void rmsnorm_rows_wave_kernel(const float* x, 
     ss = fmaf(v[j].w, v[j].w, ss);
   }
   const float inv = 1.f / sqrtf(wave_sum(ss) / float(d) + 1e-5f);
+  if (kScaled && lane == 0) rscale[row] = inv;
+  const float sc = kScaled ? 1.f : inv;
 #pragma unroll
   for (int j = 0; j < kNormVec; ++j) {
     const int i = 4 * (j * kWave + lane);
     if (i < d) {
-      const float y0 = (v[j].x * inv) * load_scalar<T>(w + i), y1 = (v[j].y * inv) * load_scalar<T>(w + i + 1);
-      const float y2 = (v[j].z * inv) * load_scalar<T>(w + i + 2), y3 = (v[j].w * inv) * load_scalar<T>(w + i + 3);
+      float y0 = v[j].x, y1 = v[j].y, y2 = v[j].z, y3 = v[j].w;
+      if (!kScaled) {
+        y0 *= sc; y1 *= sc; y2 *= sc; y3 *= sc;
+      }
+      y0 *= load_scalar<T>(w + i); y1 *= load_scalar<T>(w + i + 1);
+      y2 *= load_scalar<T>(w + i + 2); y3 *= load_scalar<T>(w + i + 3);
       *reinterpret_cast<uint2*>(out + row * d + i) = make_uint2(pack_bf16(y0, y1), pack_bf16(y2, y3));
     }
   }
+}
+
+// rscale[m] = 1 / sqrt(sum_p ss[p][m] / d + eps): the inverse RMS from the
+// per-part sums of squares a residual GEMM left (parts in a fixed order).
+__global__ __launch_bounds__(256) void norm_scale_kernel(const float* __restrict__ ss, int parts, int m, int d,
+                                                         float* __restrict__ rscale) {
+  const long row = long(blockIdx.x) * 256 + threadIdx.x;
+  if (row >= m) return;
+  float t = 0.f;
+  for (int p = 0; p < parts; ++p) t += ss[long(p) * m + row];
+  rscale[row] = 1.f / sqrtf(t / float(d) + 1e-5f);
 }
 
 }  // namespace
@@ -718,6 +819,96 @@ extern "C" int sfl_gemm_qkv_rope(const void* a, const void* w_qkv, int m, int se
   g.v_cache = static_cast<uint16_t*>(v_cache);
   g.vec16 = aligned16(q_out) && aligned16(k_cache) && aligned16(v_cache);
   return launch_gemm<G_QKV>(g, static_cast<hipStream_t>(stream), what);
+}
+
+// The fused-norm entry points need the 32x32 kernels (K % 64 == 0, 32-bit offsets).
+static bool gemm32_path(int m, int n, int k) {
+  return k % K2 == 0 && long(m) * k < (1L << 30) && long(n) * k < (1L << 30);
+}
+
+extern "C" int sfl_gemm_qkv_rope_scaled(const void* a_xg, const void* w_qkv, const float* rscale, int m, int seq,
+                                        int d_model, int heads, const float* cos_t, const float* sin_t,
+                                        void* q_out, void* k_cache, void* v_cache, int capacity, void* stream) {
+  const char* what = "gemm_qkv_rope_scaled";
+  if (!rscale) return set_error(SFL_ERR_INVALID, "%s: null pointer argument", what);
+  if (!gemm32_path(m, 3 * d_model, d_model))
+    return set_error(SFL_ERR_UNSUPPORTED, "%s: d_model must be a multiple of %d", what, K2);
+  if (!a_xg || !w_qkv || !cos_t || !sin_t || !q_out || !k_cache || !v_cache)
+    return set_error(SFL_ERR_INVALID, "%s: null pointer argument", what);
+  if (seq < 1 || m % seq) return set_error(SFL_ERR_INVALID, "%s: rows must be batch * seq", what);
+  if (heads < 1 || d_model % heads || (d_model / heads) % 16)
+    return set_error(SFL_ERR_UNSUPPORTED, "%s: head dim must be a multiple of 16", what);
+  if (seq > capacity) return set_error(SFL_ERR_INVALID, "%s: seq exceeds the cache capacity", what);
+  GemmArgs g{};
+  g.a = static_cast<const uint16_t*>(a_xg); g.w = static_cast<const uint16_t*>(w_qkv);
+  g.m = m; g.n = 3 * d_model; g.k = d_model;
+  g.cos_t = cos_t; g.sin_t = sin_t; g.seq = seq; g.heads = heads; g.head_dim = d_model / heads;
+  g.d_model = d_model; g.cap = capacity;
+  g.q_out = static_cast<uint16_t*>(q_out); g.k_cache = static_cast<uint16_t*>(k_cache);
+  g.v_cache = static_cast<uint16_t*>(v_cache);
+  g.vec16 = aligned16(q_out) && aligned16(k_cache) && aligned16(v_cache);
+  g.row_scale = rscale;
+  return launch_gemm<G_QKV>(g, static_cast<hipStream_t>(stream), what);
+}
+
+extern "C" int sfl_gemm_swiglu_scaled(const void* a_xg, const void* w13_interleaved, const float* rscale,
+                                      void* h_out, int m, int d_ff, int k, void* stream) {
+  const char* what = "gemm_swiglu_scaled";
+  if (!a_xg || !w13_interleaved || !rscale || !h_out)
+    return set_error(SFL_ERR_INVALID, "%s: null pointer argument", what);
+  if (d_ff % 8) return set_error(SFL_ERR_UNSUPPORTED, "%s: d_ff must be a multiple of 8", what);
+  if (!gemm32_path(m, 2 * d_ff, k)) return set_error(SFL_ERR_UNSUPPORTED, "%s: K must be a multiple of %d", what, K2);
+  GemmArgs g{};
+  g.a = static_cast<const uint16_t*>(a_xg); g.w = static_cast<const uint16_t*>(w13_interleaved);
+  g.m = m; g.n = 2 * d_ff; g.k = k; g.h_out = static_cast<uint16_t*>(h_out);
+  g.vec16 = aligned16(h_out);
+  g.row_scale = rscale;
+  return launch_gemm<G_SWIGLU>(g, static_cast<hipStream_t>(stream), what);
+}
+
+extern "C" int sfl_gemm_residual_norm(const void* a, const void* w, float* x, int m, int n, int k,
+                                      const void* gain_next, void* act_xg, float* ss_parts, void* stream) {
+  const char* what = "gemm_residual_norm";
+  if (!a || !w || !x || !gain_next || !act_xg || !ss_parts)
+    return set_error(SFL_ERR_INVALID, "%s: null pointer argument", what);
+  if (m < 1 || n < 1 || k < 1) return set_error(SFL_ERR_INVALID, "%s: sizes must be positive", what);
+  if (n % 4) return set_error(SFL_ERR_UNSUPPORTED, "%s: N must be a multiple of 4", what);
+  if (!gemm32_path(m, n, k)) return set_error(SFL_ERR_UNSUPPORTED, "%s: K must be a multiple of %d", what, K2);
+  if (reinterpret_cast<uintptr_t>(x) % 16 || reinterpret_cast<uintptr_t>(act_xg) % 8 ||
+      reinterpret_cast<uintptr_t>(gain_next) % 8)
+    return set_error(SFL_ERR_INVALID, "%s: x must be 16-byte and act / gain 8-byte aligned", what);
+  GemmArgs g{};
+  g.a = static_cast<const uint16_t*>(a); g.w = static_cast<const uint16_t*>(w);
+  g.m = m; g.n = n; g.k = k; g.c = x; g.c_f32 = 1; g.accumulate = 1;
+  g.norm_gain = static_cast<const uint16_t*>(gain_next);
+  g.norm_act = static_cast<uint16_t*>(act_xg);
+  g.norm_ss = ss_parts;
+  g.vec16 = aligned16(act_xg) && n % 8 == 0;  // rows of act start 16-byte aligned
+  return launch_gemm<G_PLAIN>(g, static_cast<hipStream_t>(stream), what);
+}
+
+extern "C" int sfl_norm_scale(const float* ss_parts, int parts, int m, int d_model, float* rscale, void* stream) {
+  if (!ss_parts || !rscale) return set_error(SFL_ERR_INVALID, "norm_scale: null pointer argument");
+  if (parts < 1 || m < 1 || d_model < 1) return set_error(SFL_ERR_INVALID, "norm_scale: sizes must be positive");
+  hipLaunchKernelGGL(norm_scale_kernel, dim3(unsigned((m + 255) / 256)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), ss_parts, parts, m, d_model, rscale);
+  return check_launch("norm_scale");
+}
+
+extern "C" int sfl_rmsnorm_rows_scaled(const float* x, const void* w, void* act_xg, float* rscale, int m,
+                                       int d_model, int dtype, void* stream) {
+  const char* what = "rmsnorm_rows_scaled";
+  if (!x || !w || !act_xg || !rscale) return set_error(SFL_ERR_INVALID, "%s: null pointer argument", what);
+  if (m < 1 || d_model < 1) return set_error(SFL_ERR_INVALID, "%s: sizes must be positive", what);
+  if (dtype != SFL_DTYPE_BF16) return set_error(SFL_ERR_UNSUPPORTED, "%s: dtype must be BF16", what);
+  if (d_model % 4 || d_model > 4 * kWave * kNormVec || reinterpret_cast<uintptr_t>(x) % 16 ||
+      reinterpret_cast<uintptr_t>(act_xg) % 8)
+    return set_error(SFL_ERR_UNSUPPORTED, "%s: d_model must be a multiple of 4 and at most %d, x 16-byte and "
+                     "act 8-byte aligned", what, 4 * kWave * kNormVec);
+  hipLaunchKernelGGL((rmsnorm_rows_wave_kernel<bf16_t, true>), dim3((m + 3) / 4), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), x, static_cast<const bf16_t*>(w),
+                     static_cast<uint16_t*>(act_xg), m, d_model, rscale);
+  return check_launch(what);
 }
 
 extern "C" int sfl_gemm_swiglu(const void* a, const void* w13_interleaved, void* h_out, int m, int d_ff,

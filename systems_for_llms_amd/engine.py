@@ -140,6 +140,10 @@ class DecodeSession:
         self.hidden = torch.zeros((blocks, ROW_BLOCK * f), device=dev, dtype=torch.float32)
         self.act_code = _lib.DTYPE_BF16X2 if dt == torch.bfloat16 else _lib.DTYPE_F32X
         self.deterministic = deterministic
+        # GEMM prefill with each layer's RMSNorm folded into the GEMMs beside it
+        # (where the 32x32 MFMA kernels take every shape); see ``prefill``.
+        self.fold_prefill_norm = True
+        self.prefill_norm_folded = False  # whether the last prefill did
         self.splits = splits or auto_splits(batch, h, cap)
         self.pmax = torch.empty((batch, h, self.splits), device=dev, dtype=torch.float32)
         self.psum = torch.empty_like(self.pmax)
@@ -294,17 +298,50 @@ class DecodeSession:
         call = _lib.call
         call("sfl_embed_rows", ids.data_ptr(), self.model.token_embeddings.weight.data_ptr(), x.data_ptr(),
              m_rows, d, code, st)
-        for layer, blk in enumerate(self.model.layers):
+        # Folded norms: a layer's GEMM input is bf16(x * g) and the GEMM scales its
+        # products by 1 / rms(x); the residual GEMM that updates x also writes the
+        # next norm's input and per-128-feature sums of x^2 (one more small kernel
+        # turns them into the scales), so no pass of its own re-reads x.
+        self.prefill_norm_folded = fold = self._fold_norm(m_rows)
+        layers = self.model.layers
+        if fold:
+            parts = -(-d // 128)
+            ss = torch.empty((parts, m_rows), device=dev, dtype=torch.float32)
+            rsc = torch.empty((m_rows,), device=dev, dtype=torch.float32)
+            call("sfl_rmsnorm_rows_scaled", x.data_ptr(), layers[0].attn_norm.weight.data_ptr(), act.data_ptr(),
+                 rsc.data_ptr(), m_rows, d, code, st)
+        for layer, blk in enumerate(layers):
             kc, vc = self.k_cache[layer], self.v_cache[layer]
-            call("sfl_rmsnorm_rows", x.data_ptr(), blk.attn_norm.weight.data_ptr(), act.data_ptr(), m_rows, d, code, st)
-            call("sfl_gemm_qkv_rope", act.data_ptr(), self.wqkv[layer].data_ptr(), m_rows, t, d, h,
-                 self.cos.data_ptr(), self.sin.data_ptr(), q.data_ptr(), kc.data_ptr(), vc.data_ptr(), self.cap, st)
+            if fold:
+                call("sfl_gemm_qkv_rope_scaled", act.data_ptr(), self.wqkv[layer].data_ptr(), rsc.data_ptr(), m_rows,
+                     t, d, h, self.cos.data_ptr(), self.sin.data_ptr(), q.data_ptr(), kc.data_ptr(), vc.data_ptr(),
+                     self.cap, st)
+            else:
+                call("sfl_rmsnorm_rows", x.data_ptr(), blk.attn_norm.weight.data_ptr(), act.data_ptr(), m_rows, d,
+                     code, st)
+                call("sfl_gemm_qkv_rope", act.data_ptr(), self.wqkv[layer].data_ptr(), m_rows, t, d, h,
+                     self.cos.data_ptr(), self.sin.data_ptr(), q.data_ptr(), kc.data_ptr(), vc.data_ptr(), self.cap,
+                     st)
             causal_prefill(q, kc[:, :, :t], vc[:, :, :t], attn.transpose(1, 2))
-            call("sfl_gemm_bf16", attn.data_ptr(), blk.attn.output_proj.weight.data_ptr(), x.data_ptr(),
-                 m_rows, d, d, 0, 1, st)
-            call("sfl_rmsnorm_rows", x.data_ptr(), blk.ffn_norm.weight.data_ptr(), act.data_ptr(), m_rows, d, code, st)
-            call("sfl_gemm_swiglu", act.data_ptr(), w13[layer].data_ptr(), hid.data_ptr(), m_rows, f, d, st)
-            call("sfl_gemm_bf16", hid.data_ptr(), blk.ffn.w2.weight.data_ptr(), x.data_ptr(), m_rows, d, f, 0, 1, st)
+            if fold:
+                call("sfl_gemm_residual_norm", attn.data_ptr(), blk.attn.output_proj.weight.data_ptr(), x.data_ptr(),
+                     m_rows, d, d, blk.ffn_norm.weight.data_ptr(), act.data_ptr(), ss.data_ptr(), st)
+                call("sfl_norm_scale", ss.data_ptr(), parts, m_rows, d, rsc.data_ptr(), st)
+                call("sfl_gemm_swiglu_scaled", act.data_ptr(), w13[layer].data_ptr(), rsc.data_ptr(), hid.data_ptr(),
+                     m_rows, f, d, st)
+            else:
+                call("sfl_gemm_bf16", attn.data_ptr(), blk.attn.output_proj.weight.data_ptr(), x.data_ptr(),
+                     m_rows, d, d, 0, 1, st)
+                call("sfl_rmsnorm_rows", x.data_ptr(), blk.ffn_norm.weight.data_ptr(), act.data_ptr(), m_rows, d,
+                     code, st)
+                call("sfl_gemm_swiglu", act.data_ptr(), w13[layer].data_ptr(), hid.data_ptr(), m_rows, f, d, st)
+            if fold and layer + 1 < len(layers):
+                call("sfl_gemm_residual_norm", hid.data_ptr(), blk.ffn.w2.weight.data_ptr(), x.data_ptr(), m_rows,
+                     d, f, layers[layer + 1].attn_norm.weight.data_ptr(), act.data_ptr(), ss.data_ptr(), st)
+                call("sfl_norm_scale", ss.data_ptr(), parts, m_rows, d, rsc.data_ptr(), st)
+            else:
+                call("sfl_gemm_bf16", hid.data_ptr(), blk.ffn.w2.weight.data_ptr(), x.data_ptr(), m_rows, d, f, 0, 1,
+                     st)
         logits = None
         if all_logits:
             call("sfl_rmsnorm_rows", x.data_ptr(), self.model.ln_final.weight.data_ptr(), act.data_ptr(),
@@ -324,6 +361,13 @@ class DecodeSession:
                 raise RuntimeError(f"{fn.__name__} failed ({status}): "
                                    f"{_lib.lib().sfl_last_error().decode(errors='replace')}")
         return logits
+
+    def _fold_norm(self, m_rows: int) -> bool:
+        """Whether ``prefill`` folds the norms: the 32x32 MFMA GEMMs take every shape
+        (K multiples of 64, operands under 2^30 elements) and the norm kernel d_model."""
+        d, f, lim = self.d, self.d_ff, 1 << 30
+        return (self.fold_prefill_norm and d % 64 == 0 and f % 64 == 0 and d <= 2048
+                and m_rows * max(d, f) < lim and 3 * d * d < lim and 2 * f * d < lim)
 
     def set_position(self, position: int) -> None:
         """Rewind/advance every row to ``position`` (the cache below it is kept) and re-embed."""

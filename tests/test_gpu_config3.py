@@ -8,7 +8,8 @@ known in advance. Two rows (0 and 15, the first and last of the batch) are
 recomputed on the CPU by the KV-cached oracle (``transformer.py:121-139``
 semantics) in fp32, and with the kernels' storage formats (the bf16-storage
 floor: bf16 weights and KV cache; bf16 GEMM inputs over the prompt chunk, as
-the prefill stores them; fp32 inputs over the decode chunk, as the decode
+the prefill stores them, the norm inputs as bf16(x * g) with the 1 / rms
+scale applied to the products (the norm folded into the GEMMs); fp32 inputs over the decode chunk, as the decode
 GEMVs keep them). All 1023 decode positions of both rows are compared. The
 prefill re-rounds bf16 activations at every stage, so exact computations
 drift apart chaotically from rare 1-ulp flips; row 0 is recomputed with
@@ -49,6 +50,8 @@ def test_config3_prefill_and_decode_to_4096_teacher_forced():
     assert torch.equal(session.tokens[:, :CONTEXT - 1].cpu(), seq)
     assert torch.equal(session.predicted[:, PROMPT + 1:CONTEXT].cpu(), session.logits[:, PROMPT:CONTEXT - 1]
                        .argmax(-1).cpu())
+    folded = session.prefill_norm_folded
+    assert folded  # d_model 1024 and d_ff 2752 are multiples of 64
     del session, model
     torch.cuda.empty_cache()
 
@@ -62,7 +65,7 @@ def test_config3_prefill_and_decode_to_4096_teacher_forced():
     for wide, batch in ((False, rows), (True, rows[:1])):
         cache = om.KVCacheOracle(om.round_weights(sd), cfg, batch.shape[0], CONTEXT, kv_dtype=torch.bfloat16)
         with om.accumulate_in(torch.float64 if wide else None):
-            cache.step(batch[:, :PROMPT], act_dtype=torch.bfloat16)
+            cache.step(batch[:, :PROMPT], act_dtype=torch.bfloat16, norm_fold=folded)
             floors.append(cache.step(batch[:, PROMPT:]))
         del cache
     floor, wide = floors

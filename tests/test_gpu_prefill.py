@@ -196,6 +196,57 @@ def test_rmsnorm_rows_matches_reference(m, d, dtype):
     assert not out[m].any(), "wrote past the last row"
 
 
+@pytest.mark.parametrize("m,d", [(1, 64), (7, 96), (130, 1024), (33, 2048)])
+def test_rmsnorm_rows_scaled_splits_the_norm(m, d):
+    """The folded norm's input side: bf16(x * w) exactly as the CPU rounds it, and 1 / rms(x)."""
+    g = torch.Generator().manual_seed(m * d)
+    x = 3 * torch.randn((m, d), generator=g)
+    w = (1 + 0.5 * torch.randn(d, generator=g)).bfloat16()
+    gx, gw = x.cuda(), w.cuda()
+    act = torch.full((m + 1, d), 7.0, device="cuda", dtype=torch.bfloat16)
+    rsc = torch.full((m + 1,), -1.0, device="cuda")
+    _lib.call("sfl_rmsnorm_rows_scaled", gx.data_ptr(), gw.data_ptr(), act.data_ptr(), rsc.data_ptr(), m, d, 1,
+              _lib.stream_handle())
+    assert torch.equal(act[:m].cpu(), (x * w.float()).bfloat16())
+    torch.testing.assert_close(rsc[:m].cpu(), 1 / torch.sqrt((x * x).mean(-1) + om.EPS), rtol=2e-6, atol=0)
+    assert bool((act[m] == 7).all()) and rsc[m].item() == -1.0
+
+
+# The residual GEMM that also prepares the next RMSNorm: x += A W^T, then
+# bf16(x * gain) and per-token sums of x^2 over each 128-feature part, on the
+# 128 x 128 tiles (ragged features, a last part of 64) and the 256 x 384 tiles
+# (ragged tokens and features), with guard rows around every output; N % 8 ==
+# 4 takes the 8-byte stores of the norm input instead of 16-byte ones.
+@pytest.mark.parametrize("m,n,k", [(200, 192, 320), (300, 196, 64), (1000, 1024, 64), (24577, 1088, 128)])
+def test_gemm_residual_norm_and_norm_scale(m, n, k):
+    g = torch.Generator().manual_seed(m + n + k + 7)
+    a = torch.randn((m, k), generator=g).bfloat16()
+    w = torch.randn((n, k), generator=g).bfloat16()
+    x0 = torch.randn((m, n), generator=g)
+    gain = (1 + 0.5 * torch.randn(n, generator=g)).bfloat16()
+    parts = -(-n // 128)
+    xg = torch.full((m + 2, n), float("nan"), device="cuda")
+    xg[1:-1] = x0.cuda()
+    act = torch.full((m + 1, n), 7.0, device="cuda", dtype=torch.bfloat16)
+    ss = torch.full((parts * m + 64,), -1.0, device="cuda")
+    rsc = torch.full((m + 1,), -1.0, device="cuda")
+    ga, gw, gg = a.cuda(), w.cuda(), gain.cuda()
+    st = _lib.stream_handle()
+    _lib.call("sfl_gemm_residual_norm", ga.data_ptr(), gw.data_ptr(), xg[1:].data_ptr(), m, n, k, gg.data_ptr(),
+              act.data_ptr(), ss.data_ptr(), st)
+    _lib.call("sfl_norm_scale", ss.data_ptr(), parts, m, n, rsc.data_ptr(), st)
+    x1 = xg[1:-1].cpu()
+    assert bool(xg[0].isnan().all()) and bool(xg[-1].isnan().all()), "wrote outside x"
+    torch.testing.assert_close(x1, x0 + a.float() @ w.float().t(), atol=1e-3 * k ** 0.5, rtol=1e-4)
+    assert torch.equal(act[:m].cpu(), (x1 * gain.float()).bfloat16())
+    assert bool((act[m] == 7).all())
+    sq = torch.nn.functional.pad(x1 * x1, (0, parts * 128 - n)).view(m, parts, 128).sum(-1).t()
+    torch.testing.assert_close(ss[:parts * m].view(parts, m).cpu(), sq, rtol=1e-5, atol=1e-6 * sq.max().item())
+    assert bool((ss[parts * m:] == -1).all())
+    torch.testing.assert_close(rsc[:m].cpu(), 1 / torch.sqrt((x1 * x1).mean(-1) + om.EPS), rtol=1e-5, atol=0)
+    assert rsc[m].item() == -1.0
+
+
 def gpu_model(cfg, sd):
     model = TransformerLM.from_config(cfg, device="cuda", dtype=torch.bfloat16)
     model.load_state_dict(sd)
@@ -226,14 +277,15 @@ def test_tiny_golden_bf16_forward_step_path(golden):
     assert err <= 2e-2
 
 
-def format_floor(sd, cfg, seq, prompt, wide=False):
+def format_floor(sd, cfg, seq, prompt, wide=False, fold=False):
     """The bf16-storage floor of a GEMM prefill of ``prompt`` tokens followed by decode steps:
     bf16 weights and KV cache; bf16 GEMM inputs and probabilities over the prompt chunk only.
-    ``wide``: the same with float64-accumulated products (the drift yardstick)."""
+    ``wide``: the same with float64-accumulated products (the drift yardstick); ``fold``: the
+    prefill stored its norm inputs as bf16(x * g) (the folded-norm path)."""
     cache = om.KVCacheOracle(om.round_weights(sd), cfg, seq.shape[0], seq.shape[1], kv_dtype=torch.bfloat16)
     with om.accumulate_in(torch.float64 if wide else None):
-        return torch.cat([cache.step(seq[:, :prompt], act_dtype=torch.bfloat16), cache.step(seq[:, prompt:])],
-                         dim=1)
+        return torch.cat([cache.step(seq[:, :prompt], act_dtype=torch.bfloat16, norm_fold=fold),
+                          cache.step(seq[:, prompt:])], dim=1)
 
 
 def test_config2_prefill_then_decode_teacher_forced():
@@ -245,13 +297,14 @@ def test_config2_prefill_then_decode_teacher_forced():
     seq = seeded_prompt(cfg.vocab_size, 8, ctx, 2027)
     torch.set_num_threads(16)
     ref = om.KVCacheOracle(sd, cfg, 8, ctx).step(seq)
-    floor = format_floor(sd, cfg, seq, 512)
-    wide = format_floor(sd, cfg, seq, 512, wide=True)  # the drift over the same rows the gates compare
     model = gpu_model(cfg, sd)
     session = DecodeSession(model, 8, ctx, record_logits=True)
     all_logits = session.prefill(seq[:, :512].cuda(), all_logits=True, forced=seq.cuda())
     session.run(ctx - 1 - 512, use_graph=True)  # positions 512 .. ctx - 2 predict tokens 513 .. ctx - 1
     torch.cuda.synchronize()
+    assert session.prefill_norm_folded  # d_model and d_ff are multiples of 64
+    floor = format_floor(sd, cfg, seq, 512, fold=True)
+    wide = format_floor(sd, cfg, seq, 512, wide=True, fold=True)  # the drift over the same rows the gates compare
     pre = all_logits.cpu()
     dec = session.logits[:, 512:ctx - 1].float().cpu()
     bf16_gate("config2 prefill (positions 0..511)", pre, ref[:, :512], floor[:, :512],
@@ -353,6 +406,112 @@ def test_prefill_layer_stages_match_the_bf16_format_oracle(config):
                2e-3)
     x2_ref = x1.cpu() + om._linear(hid.float().cpu(), sdr[p + "ffn.w2.weight"])
     torch.testing.assert_close(x.cpu(), x2_ref, atol=1e-5, rtol=1e-5)
+
+
+@pytest.mark.parametrize("config", ["scale-100m-s1024", "scale-324m-s4096"])
+def test_prefill_folded_norm_stages_match_the_bf16_format_oracle(config):
+    """One prefill layer with its norms folded into the GEMMs, each stage fed the GPU's own
+    inputs: the norm inputs bf16(x * g) bit-exact, the scales 1 / rms(x) and fp32 residual
+    updates to fp32 rounding, the scaled GEMM outputs up to rare 1-ulp flips; with unit
+    scales the scaled GEMMs are the plain ones, bit for bit."""
+    cfg = load_model_config(config)
+    sd = seeded_state_dict(cfg, 1337)
+    sdr = om.round_weights(sd)
+    b, t = 2, 512
+    ids = seeded_prompt(cfg.vocab_size, b, t, 2027)
+    model = gpu_model(cfg, sd)
+    session = DecodeSession(model, b, t)
+    d, h, f = cfg.d_model, cfg.num_heads, cfg.d_ff
+    dk, m, parts = d // h, b * t, -(-d // 128)
+    x = torch.empty((m, d), device="cuda")
+    act = torch.empty((m, d), device="cuda", dtype=torch.bfloat16)
+    q = torch.empty((b, h, t, dk), device="cuda", dtype=torch.bfloat16)
+    attn = torch.empty((b, t, h, dk), device="cuda", dtype=torch.bfloat16)
+    hid = torch.empty((m, f), device="cuda", dtype=torch.bfloat16)
+    ss = torch.empty((parts, m), device="cuda")
+    rsc = torch.empty((m,), device="cuda")
+    ones = torch.ones((m,), device="cuda")
+    blk, nxt, kc, vc = model.layers[0], model.layers[1], session.k_cache[0], session.v_cache[0]
+    w13 = session.weights.w13()[0]
+    gid = ids.cuda().view(-1)
+    st = _lib.stream_handle()
+    call = _lib.call
+
+    def qkv(scale):
+        args = (session.wqkv[0].data_ptr(),) + ((scale.data_ptr(),) if scale is not None else ())
+        call("sfl_gemm_qkv_rope_scaled" if scale is not None else "sfl_gemm_qkv_rope", act.data_ptr(), *args, m, t,
+             d, h, session.cos.data_ptr(), session.sin.data_ptr(), q.data_ptr(), kc.data_ptr(), vc.data_ptr(),
+             session.cap, st)
+        return q.clone(), kc[:, :, :t].clone(), vc[:, :, :t].clone()
+
+    def swiglu(scale):
+        if scale is None:
+            call("sfl_gemm_swiglu", act.data_ptr(), w13.data_ptr(), hid.data_ptr(), m, f, d, st)
+        else:
+            call("sfl_gemm_swiglu_scaled", act.data_ptr(), w13.data_ptr(), scale.data_ptr(), hid.data_ptr(), m, f,
+                 d, st)
+        return hid.clone()
+
+    call("sfl_embed_rows", gid.data_ptr(), model.token_embeddings.weight.data_ptr(), x.data_ptr(), m, d, 1, st)
+    x0 = x.clone()
+    call("sfl_rmsnorm_rows_scaled", x.data_ptr(), blk.attn_norm.weight.data_ptr(), act.data_ptr(), rsc.data_ptr(),
+         m, d, 1, st)
+    act1, r1 = act.clone(), rsc.clone()
+    plain, unit = qkv(None), qkv(ones)
+    for p_, u_ in zip(plain, unit):
+        assert torch.equal(p_, u_), "unit scales change the q/k/v GEMM"
+    q1, k1, v1 = qkv(rsc)
+    from systems_for_llms_amd.attention import causal_prefill
+    causal_prefill(q, kc[:, :, :t], vc[:, :, :t], attn.transpose(1, 2))
+    call("sfl_gemm_residual_norm", attn.data_ptr(), blk.attn.output_proj.weight.data_ptr(), x.data_ptr(), m, d, d,
+         blk.ffn_norm.weight.data_ptr(), act.data_ptr(), ss.data_ptr(), st)
+    x1, act2, ss2 = x.clone(), act.clone(), ss.clone()
+    call("sfl_norm_scale", ss.data_ptr(), parts, m, d, rsc.data_ptr(), st)
+    r2 = rsc.clone()
+    assert torch.equal(swiglu(None), swiglu(ones)), "unit scales change the SwiGLU GEMM"
+    hid2 = swiglu(rsc)
+    call("sfl_gemm_residual_norm", hid.data_ptr(), blk.ffn.w2.weight.data_ptr(), x.data_ptr(), m, d, f,
+         nxt.attn_norm.weight.data_ptr(), act.data_ptr(), ss.data_ptr(), st)
+    call("sfl_norm_scale", ss.data_ptr(), parts, m, d, rsc.data_ptr(), st)
+    torch.cuda.synchronize()
+
+    torch.set_num_threads(16)
+    bf, p = torch.bfloat16, "layers.0."
+    cos, sin = om.rope_tables(cfg.rope_theta, dk, cfg.context_length)
+    pos = torch.arange(t)
+
+    def inv_rms(xx):
+        return 1 / torch.sqrt((xx * xx).mean(-1) + om.EPS)
+
+    def split_norm(name, xx, gain, act_, ss_, r_):
+        assert torch.equal(act_.cpu(), (xx * gain).bfloat16()), f"{name}: norm input is not bf16(x * g)"
+        if ss_ is not None:
+            sq = (xx * xx).view(m, parts, 128).sum(-1).t()
+            torch.testing.assert_close(ss_.cpu(), sq, rtol=1e-5, atol=1e-6 * sq.max().item())
+        torch.testing.assert_close(r_.cpu(), inv_rms(xx), rtol=1e-5, atol=0)
+
+    x0c = x0.cpu()
+    assert torch.equal(x0c, sdr["token_embeddings.weight"][ids].reshape(m, d))
+    split_norm("attention norm", x0c, sdr[p + "attn_norm.weight"], act1, None, r1)
+    a1, s1 = act1.float().cpu().view(b, t, d), r1.cpu().view(b, t, 1)
+
+    def proj(name):
+        return om._split_heads(om._linear(a1, sdr[p + f"attn.{name}_proj.weight"]) * s1, h)
+    _ulp_close("q (scaled, RoPE)", q1, om._round(om.rope(proj("q"), cos, sin, pos), bf), 2e-3)
+    _ulp_close("k cache (scaled, RoPE)", k1, om._round(om.rope(proj("k"), cos, sin, pos), bf), 2e-3)
+    _ulp_close("v cache (scaled)", v1, om._round(proj("v"), bf), 2e-3)
+    x1c = x1.cpu()
+    torch.testing.assert_close(x1c, x0c + om._linear(attn.float().cpu().view(m, d), sdr[p + "attn.output_proj.weight"]),
+                               atol=1e-5, rtol=1e-5)
+    split_norm("ffn norm", x1c, sdr[p + "ffn_norm.weight"], act2, ss2, r2)
+    a2, s2 = act2.float().cpu(), r2.cpu()[:, None]
+    g1 = om._linear(a2, sdr[p + "ffn.w1.weight"]) * s2
+    g3 = om._linear(a2, sdr[p + "ffn.w3.weight"]) * s2
+    _ulp_close("SwiGLU hidden (scaled)", hid2, om._round(g1 * torch.sigmoid(g1) * g3, bf), 2e-3)
+    x2c = x.cpu()
+    torch.testing.assert_close(x2c, x1c + om._linear(hid2.float().cpu(), sdr[p + "ffn.w2.weight"]), atol=1e-5,
+                               rtol=1e-5)
+    split_norm("next layer's attention norm", x2c, sdr["layers.1.attn_norm.weight"], act, ss, rsc)
 
 
 def test_generate_bf16_uses_prefill_and_matches_step_path():

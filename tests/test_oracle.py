@@ -126,6 +126,31 @@ def test_storage_format_floors_are_consistent(golden):
     assert not torch.equal(mixed[:, 7:], full[:, 7:])
 
 
+def test_folded_norm_floor_is_the_same_model_rounded_elsewhere(golden):
+    """``norm_fold`` (GEMM input x * w, products scaled by 1 / rms afterwards) is RMSNorm
+    reassociated: with fp32 storage it equals the unfolded cache to fp32 rounding (a dropped,
+    inverted or misplaced factor fails this), with bf16 storage it moves the floor by rounding only."""
+    meta, arrays = golden
+    cfg = _tiny(meta)
+    sd = om.round_weights(seeded_state_dict(cfg, meta["tiny"]["seed"]))
+    # Gains away from one, so that x * w and rmsnorm(x) * w differ as stored values.
+    g = torch.Generator().manual_seed(5)
+    for name in sd:
+        if name.endswith("norm.weight"):
+            sd[name] = (1.0 + 0.5 * torch.randn(sd[name].shape, generator=g)).to(torch.bfloat16).float()
+    ids = torch.from_numpy(arrays["tiny_ids"])
+
+    def run(act_dtype, fold):
+        cache = om.KVCacheOracle(sd, cfg, ids.shape[0], kv_dtype=torch.bfloat16)
+        return torch.cat([cache.step(ids[:, :7], act_dtype=act_dtype, norm_fold=fold), cache.step(ids[:, 7:])],
+                         dim=1)
+
+    torch.testing.assert_close(run(torch.float32, True), run(torch.float32, False), atol=2e-6, rtol=2e-5)
+    folded, plain = run(torch.bfloat16, True), run(torch.bfloat16, False)
+    assert not torch.equal(folded, plain)
+    assert (folded - plain).abs().max().item() < 5e-2 * plain.abs().max().item()
+
+
 def test_stored_probability_attention_is_softmax_up_to_its_rounding():
     """The prefill floor's tiled lazy-maximum attention: with fp32 probabilities it is exact
     softmax attention (the running maximum only bounds the exponents), also when scores jump
