@@ -17,7 +17,10 @@ def bf16_gate(name, got, ref, floor, targets=None, envelope=None):
       drift apart chaotically -- a 1-ulp flip from fp32 reassociation changes
       the next stage's rounding of its whole row -- so ``envelope``, a pair
       (floor rows, the same rows recomputed with float64 accumulation), sets
-      the bound instead: twice that drift, and its agreement less 0.5%;
+      the bound instead: twice that drift, and its agreement less 0.5%. A
+      window of fewer than 100 positions cannot resolve 1%, so one pick that
+      differs from the floor's is allowed there (its logits still within the
+      max-abs bound, i.e. a near-tie; the floor's top-2 margin is printed);
     * the north-star gate against fp32 (max-abs 2e-2, >= 99% greedy agreement).
       It is printed for every config. Where it is missed, the test requires
       that the storage formats alone (the floor) miss it too -- on the flat
@@ -33,6 +36,9 @@ def bf16_gate(name, got, ref, floor, targets=None, envelope=None):
         kernel_atol = max(KERNEL_ATOL, 2.0 * drift)
         kernel_agree = min(KERNEL_AGREE, drift_agree - 0.005)
         drift_note = f" | floor vs float64-accumulated floor: max-abs {drift:.5f} agreement {drift_agree:.4f}"
+    samples = got.shape[:-1].numel()
+    if samples < 100:  # a window this short cannot resolve 1%: one flip is allowed
+        kernel_agree = min(kernel_agree, 1.0 - 1.0 / samples)
     targets = ref.argmax(-1) if targets is None else targets
     err = (got - ref).abs().max().item()
     floor_err = (floor - ref).abs().max().item()
@@ -47,6 +53,11 @@ def bf16_gate(name, got, ref, floor, targets=None, envelope=None):
           f"vs fp32: max-abs {floor_err:.4f} agreement {floor_agree:.4f} -> "
           f"{'met' if floor_strict else 'MISSED'} | kernels vs floor: max-abs {kernel_err:.5f} "
           f"agreement {k_agree:.4f} (gate {kernel_atol:.5f}, {kernel_agree:.4f})" + drift_note)
+    flips = got.argmax(-1) != floor.argmax(-1)
+    if flips.any():  # the floor's top-2 gap where the kernels pick another token
+        top2 = floor[flips].topk(2, dim=-1).values
+        print(f"{name}: {int(flips.sum())} of {samples} picks differ from the floor's, its top-2 margins there: "
+              + " ".join(f"{m:.5f}" for m in (top2[:, 0] - top2[:, 1]).tolist()))
     assert kernel_err <= kernel_atol, f"{name}: kernels move the logits {kernel_err} from the storage floor"
     assert k_agree >= kernel_agree, f"{name}: kernels agree with the storage floor on only {k_agree}"
     if not strict:
