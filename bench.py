@@ -338,7 +338,7 @@ def profile_target_gemm(reps: int = 10) -> int:
     kc = torch.empty((BATCH, h, CONTEXT, d // h), device="cuda", dtype=torch.bfloat16)
     vc = torch.empty_like(kc)
     from systems_for_llms_amd.model import rope_tables
-    cos, sin = (c.cuda() for c in rope_tables(10000.0, d // h, CONTEXT))
+    cos, sin = (c.t().contiguous().cuda() for c in rope_tables(10000.0, d // h, CONTEXT))  # feature-major
     st = _lib.stream_handle()
     calls = {
         "q/k/v": lambda: _lib.call("sfl_gemm_qkv_rope", act.data_ptr(), w["qkv"].data_ptr(), m, t, d, h, cos.data_ptr(),

@@ -300,7 +300,10 @@ int sfl_masked_attention_kernel_info(int head_dim, int dtype, int n, long k_row_
 int sfl_gemm_bf16(const void* a, const void* w, void* c, int m, int n, int k, int c_dtype,
                   int accumulate, void* stream);
 
-/* q/k/v = A W_qkv^T with RoPE at position (row % seq) from the fp32 table;
+/* q/k/v = A W_qkv^T with RoPE at position (row % seq) from the fp32 tables
+ * cos_t / sin_t in feature-major layout [head_dim / 2, capacity] (the
+ * reference's [positions, head_dim / 2] table of attention.py:31-42
+ * transposed: lanes holding consecutive tokens read consecutive floats);
  * q to [m/seq, heads, seq, head_dim] bf16, k/v written at positions 0..seq-1
  * of the [m/seq, heads, capacity, head_dim] bf16 cache. */
 int sfl_gemm_qkv_rope(const void* a, const void* w_qkv, int m, int seq, int d_model, int heads,
@@ -345,8 +348,8 @@ int sfl_gemm_residual_norm(const void* a, const void* w, float* x, int m, int n,
 /* rscale[r] = 1 / sqrt(sum_p ss_parts[p][r] / d_model + 1e-5), parts summed in order. */
 int sfl_norm_scale(const float* ss_parts, int parts, int m, int d_model, float* rscale, void* stream);
 
-/* sfl_gemm_qkv_rope on act_xg, each token's products scaled by rscale[r]
- * before RoPE and the bf16 stores. */
+/* sfl_gemm_qkv_rope on act_xg (same feature-major tables), each token's
+ * products scaled by rscale[r] before RoPE and the bf16 stores. */
 int sfl_gemm_qkv_rope_scaled(const void* a_xg, const void* w_qkv, const float* rscale, int m, int seq,
                              int d_model, int heads, const float* cos_t, const float* sin_t, void* q_out,
                              void* k_cache, void* v_cache, int capacity, void* stream);

@@ -119,9 +119,13 @@ __device__ __forceinline__ QkvTok qkv_tok(const GemmArgs& g, int m) {
 // dim+3 of one head: two rotation pairs) of token qt; v features pass through.
 __device__ __forceinline__ void rope4(const GemmArgs& g, float (&y)[4], const QkvFeat& qf, const QkvTok& qt) {
   if (qf.section >= 2) return;
-  const int half = g.head_dim / 2;
-  const float2 c = *reinterpret_cast<const float2*>(g.cos_t + long(qt.t) * half + qf.dim / 2);
-  const float2 s = *reinterpret_cast<const float2*>(g.sin_t + long(qt.t) * half + qf.dim / 2);
+  // Feature-major tables [head_dim / 2][cap]: the 32 lanes of a group hold 32
+  // consecutive tokens, so each load reads consecutive floats (row-major
+  // tables put the 32 tokens on 32 cache lines: 345 -> 330 us on the 324M
+  // q/k/v shape, same values).
+  const long r0 = long(qf.dim / 2) * g.cap + qt.t;
+  const float2 c = make_float2(g.cos_t[r0], g.cos_t[r0 + g.cap]);
+  const float2 s = make_float2(g.sin_t[r0], g.sin_t[r0 + g.cap]);
   const float e0 = y[0], o0 = y[1], e1 = y[2], o1 = y[3];
   y[0] = e0 * c.x - o0 * s.x;
   y[1] = e0 * s.x + o0 * c.x;

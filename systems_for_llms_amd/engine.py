@@ -119,6 +119,8 @@ class DecodeSession:
         from .model import rope_tables
         cos, sin = rope_tables(model.theta, self.dk, cap)
         self.cos, self.sin = cos.to(dev), sin.to(dev)
+        # The prefill GEMMs take the tables feature-major ([dk/2, cap]).
+        self.cos_fm, self.sin_fm = self.cos.t().contiguous(), self.sin.t().contiguous()
         # Packed copies shared by every session of this model while its parameters are
         # unchanged; the session keeps a reference, so its captured launches stay valid.
         self.weights = w = decode_weights(model)
@@ -314,14 +316,14 @@ class DecodeSession:
             kc, vc = self.k_cache[layer], self.v_cache[layer]
             if fold:
                 call("sfl_gemm_qkv_rope_scaled", act.data_ptr(), self.wqkv[layer].data_ptr(), rsc.data_ptr(), m_rows,
-                     t, d, h, self.cos.data_ptr(), self.sin.data_ptr(), q.data_ptr(), kc.data_ptr(), vc.data_ptr(),
-                     self.cap, st)
+                     t, d, h, self.cos_fm.data_ptr(), self.sin_fm.data_ptr(), q.data_ptr(), kc.data_ptr(),
+                     vc.data_ptr(), self.cap, st)
             else:
                 call("sfl_rmsnorm_rows", x.data_ptr(), blk.attn_norm.weight.data_ptr(), act.data_ptr(), m_rows, d,
                      code, st)
                 call("sfl_gemm_qkv_rope", act.data_ptr(), self.wqkv[layer].data_ptr(), m_rows, t, d, h,
-                     self.cos.data_ptr(), self.sin.data_ptr(), q.data_ptr(), kc.data_ptr(), vc.data_ptr(), self.cap,
-                     st)
+                     self.cos_fm.data_ptr(), self.sin_fm.data_ptr(), q.data_ptr(), kc.data_ptr(), vc.data_ptr(),
+                     self.cap, st)
             causal_prefill(q, kc[:, :, :t], vc[:, :, :t], attn.transpose(1, 2))
             if fold:
                 call("sfl_gemm_residual_norm", attn.data_ptr(), blk.attn.output_proj.weight.data_ptr(), x.data_ptr(),

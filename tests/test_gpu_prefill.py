@@ -104,7 +104,8 @@ def test_gemm_large_grid_bf16_epilogues(aligned):
     w3 = (torch.randn((f, d), generator=g) * 0.03).bfloat16()
     w13 = torch.stack([w1.view(f // 8, 8, d), w3.view(f // 8, 8, d)], dim=1).reshape(2 * f, d).contiguous()
     cos, sin = om.rope_tables(10000.0, dk, cap)
-    ga, gqkv, g13, gcos, gsin = a.cuda(), wqkv.cuda(), w13.cuda(), cos.cuda(), sin.cuda()
+    ga, gqkv, g13 = a.cuda(), wqkv.cuda(), w13.cuda()
+    gcos, gsin = cos.t().contiguous().cuda(), sin.t().contiguous().cuda()  # feature-major
     q = _bf16_out((b, h, t, dk), aligned)
     kc, vc = _bf16_out((b, h, cap, dk), aligned), _bf16_out((b, h, cap, dk), aligned)
     hid = _bf16_out((m, f), aligned)
@@ -153,7 +154,8 @@ def test_gemm_qkv_rope_head_dims_across_feature_blocks(dk, h, b, t):
     q = torch.zeros((b, h, t, dk), device="cuda", dtype=torch.bfloat16)
     kc = torch.zeros((b, h, cap, dk), device="cuda", dtype=torch.bfloat16)
     vc = torch.zeros_like(kc)
-    gcos, gsin, ga, gw = cos.cuda(), sin.cuda(), a.cuda(), wqkv.cuda()
+    gcos, gsin = cos.t().contiguous().cuda(), sin.t().contiguous().cuda()  # feature-major
+    ga, gw = a.cuda(), wqkv.cuda()
     _lib.call("sfl_gemm_qkv_rope", ga.data_ptr(), gw.data_ptr(), m, t, d, h, gcos.data_ptr(), gsin.data_ptr(),
               q.data_ptr(), kc.data_ptr(), vc.data_ptr(), cap, _lib.stream_handle())
     torch.cuda.synchronize()
@@ -363,8 +365,8 @@ def test_prefill_layer_stages_match_the_bf16_format_oracle(config):
     x0 = x.clone()
     call("sfl_rmsnorm_rows", x.data_ptr(), blk.attn_norm.weight.data_ptr(), act.data_ptr(), m, d, 1, st)
     act1 = act.clone()
-    call("sfl_gemm_qkv_rope", act.data_ptr(), session.wqkv[0].data_ptr(), m, t, d, h, session.cos.data_ptr(),
-         session.sin.data_ptr(), q.data_ptr(), kc.data_ptr(), vc.data_ptr(), session.cap, st)
+    call("sfl_gemm_qkv_rope", act.data_ptr(), session.wqkv[0].data_ptr(), m, t, d, h, session.cos_fm.data_ptr(),
+         session.sin_fm.data_ptr(), q.data_ptr(), kc.data_ptr(), vc.data_ptr(), session.cap, st)
     from systems_for_llms_amd.attention import causal_prefill
     causal_prefill(q, kc[:, :, :t], vc[:, :, :t], attn.transpose(1, 2))
     call("sfl_gemm_bf16", attn.data_ptr(), blk.attn.output_proj.weight.data_ptr(), x.data_ptr(), m, d, d, 0, 1, st)
@@ -440,7 +442,7 @@ def test_prefill_folded_norm_stages_match_the_bf16_format_oracle(config):
     def qkv(scale):
         args = (session.wqkv[0].data_ptr(),) + ((scale.data_ptr(),) if scale is not None else ())
         call("sfl_gemm_qkv_rope_scaled" if scale is not None else "sfl_gemm_qkv_rope", act.data_ptr(), *args, m, t,
-             d, h, session.cos.data_ptr(), session.sin.data_ptr(), q.data_ptr(), kc.data_ptr(), vc.data_ptr(),
+             d, h, session.cos_fm.data_ptr(), session.sin_fm.data_ptr(), q.data_ptr(), kc.data_ptr(), vc.data_ptr(),
              session.cap, st)
         return q.clone(), kc[:, :, :t].clone(), vc[:, :, :t].clone()
 
