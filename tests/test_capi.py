@@ -46,3 +46,39 @@ def test_argument_errors_are_reported_without_a_launch():
         _lib.call("sfl_decode_attention", p, p, p, p, p, p, p, p, 1, 3, 2, 16, 64, 1, 0.125, 1, 1, 1, None)
     with pytest.raises(RuntimeError, match="head dim"):
         _lib.call("sfl_decode_attention", p, p, p, p, p, p, p, p, 1, 2, 2, 16, 48, 1, 0.125, 1, 1, 1, None)
+
+
+def test_folded_norm_entry_points_reject_bad_arguments_without_a_launch():
+    """Every call here fails an argument check before anything reaches HIP."""
+    import ctypes
+
+    from systems_for_llms_amd import _lib
+
+    if not _lib.LIB_PATH.exists():
+        pytest.skip("libsfl.so not built")
+    buf = ctypes.create_string_buffer(256)
+    p = (ctypes.addressof(buf) + 15) // 16 * 16  # 16-byte aligned host address (never dereferenced)
+    with pytest.raises(RuntimeError, match="null pointer"):
+        _lib.call("sfl_gemm_residual_norm", p, p, p, 64, 128, 64, None, p, p, None)
+    with pytest.raises(RuntimeError, match="multiple of 4"):
+        _lib.call("sfl_gemm_residual_norm", p, p, p, 64, 130, 64, p, p, p, None)
+    with pytest.raises(RuntimeError, match="multiple of 64"):
+        _lib.call("sfl_gemm_residual_norm", p, p, p, 64, 128, 72, p, p, p, None)
+    with pytest.raises(RuntimeError, match="16-byte"):
+        _lib.call("sfl_gemm_residual_norm", p, p, p + 4, 64, 128, 64, p, p, p, None)
+    with pytest.raises(RuntimeError, match="sizes must be positive"):
+        _lib.call("sfl_norm_scale", p, 0, 64, 128, p, None)
+    with pytest.raises(RuntimeError, match="dtype must be BF16"):
+        _lib.call("sfl_rmsnorm_rows_scaled", p, p, p, p, 4, 128, 0, None)
+    with pytest.raises(RuntimeError, match="at most 2048"):
+        _lib.call("sfl_rmsnorm_rows_scaled", p, p, p, p, 4, 4096, 1, None)
+    with pytest.raises(RuntimeError, match="null pointer"):
+        _lib.call("sfl_gemm_qkv_rope_scaled", p, p, None, 64, 64, 128, 2, p, p, p, p, p, 64, None)
+    with pytest.raises(RuntimeError, match="multiple of 64"):
+        _lib.call("sfl_gemm_qkv_rope_scaled", p, p, p, 64, 64, 96, 2, p, p, p, p, p, 64, None)
+    with pytest.raises(RuntimeError, match="batch \\* seq"):
+        _lib.call("sfl_gemm_qkv_rope_scaled", p, p, p, 65, 64, 128, 2, p, p, p, p, p, 64, None)
+    with pytest.raises(RuntimeError, match="multiple of 8"):
+        _lib.call("sfl_gemm_swiglu_scaled", p, p, p, p, 64, 100, 128, None)
+    with pytest.raises(RuntimeError, match="multiple of 64"):
+        _lib.call("sfl_gemm_swiglu_scaled", p, p, p, p, 64, 128, 72, None)
