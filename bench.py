@@ -320,7 +320,9 @@ def profile_target_masked(reps: int = 20) -> int:
 
 def profile_target_gemm(reps: int = 10) -> int:
     """Counter-collection target: the prefill GEMMs of the 324M model at M = 16 x 3072 tokens
-    (q/k/v + RoPE + cache write, output_proj, w1/w3 + SwiGLU, w2, lm_head), ``reps`` calls each."""
+    through the entry points the prefill calls (q/k/v scaled by 1/rms + RoPE + cache write,
+    output_proj and w2 adding into x and writing the next norm's input and sums of squares,
+    w1/w3 scaled + SwiGLU; then the all-positions lm_head), ``reps`` calls each."""
     import torch
 
     from systems_for_llms_amd import _lib
@@ -333,6 +335,10 @@ def profile_target_gemm(reps: int = 10) -> int:
          for name, shape in (("qkv", (3 * d, d)), ("o", (d, d)), ("w13", (2 * f, d)), ("w2", (d, f)),
                              ("head", (v, d)))}
     x = torch.zeros((m, d), device="cuda")
+    gain = torch.ones((d,), device="cuda", dtype=torch.bfloat16)
+    xg = torch.empty((m, d), device="cuda", dtype=torch.bfloat16)  # the next norm's input
+    ss = torch.empty((-(-d // 128), m), device="cuda")
+    rsc = torch.ones((m,), device="cuda")
     logits = torch.empty((m, v), device="cuda")
     q = torch.empty((BATCH, h, t, d // h), device="cuda", dtype=torch.bfloat16)
     kc = torch.empty((BATCH, h, CONTEXT, d // h), device="cuda", dtype=torch.bfloat16)
@@ -341,13 +347,15 @@ def profile_target_gemm(reps: int = 10) -> int:
     cos, sin = (c.t().contiguous().cuda() for c in rope_tables(10000.0, d // h, CONTEXT))  # feature-major
     st = _lib.stream_handle()
     calls = {
-        "q/k/v": lambda: _lib.call("sfl_gemm_qkv_rope", act.data_ptr(), w["qkv"].data_ptr(), m, t, d, h, cos.data_ptr(),
-                                   sin.data_ptr(), q.data_ptr(), kc.data_ptr(), vc.data_ptr(), CONTEXT, st),
-        "output_proj": lambda: _lib.call("sfl_gemm_bf16", act.data_ptr(), w["o"].data_ptr(), x.data_ptr(), m, d, d,
-                                         0, 1, st),
-        "w1/w3": lambda: _lib.call("sfl_gemm_swiglu", act.data_ptr(), w["w13"].data_ptr(), hid.data_ptr(), m, f, d,
-                                   st),
-        "w2": lambda: _lib.call("sfl_gemm_bf16", hid.data_ptr(), w["w2"].data_ptr(), x.data_ptr(), m, d, f, 0, 1, st),
+        "q/k/v": lambda: _lib.call("sfl_gemm_qkv_rope_scaled", act.data_ptr(), w["qkv"].data_ptr(), rsc.data_ptr(),
+                                   m, t, d, h, cos.data_ptr(), sin.data_ptr(), q.data_ptr(), kc.data_ptr(),
+                                   vc.data_ptr(), CONTEXT, st),
+        "output_proj": lambda: _lib.call("sfl_gemm_residual_norm", act.data_ptr(), w["o"].data_ptr(), x.data_ptr(),
+                                         m, d, d, gain.data_ptr(), xg.data_ptr(), ss.data_ptr(), st),
+        "w1/w3": lambda: _lib.call("sfl_gemm_swiglu_scaled", act.data_ptr(), w["w13"].data_ptr(), rsc.data_ptr(),
+                                   hid.data_ptr(), m, f, d, st),
+        "w2": lambda: _lib.call("sfl_gemm_residual_norm", hid.data_ptr(), w["w2"].data_ptr(), x.data_ptr(), m, d, f,
+                                gain.data_ptr(), xg.data_ptr(), ss.data_ptr(), st),
         "lm_head": lambda: _lib.call("sfl_gemm_bf16", act.data_ptr(), w["head"].data_ptr(), logits.data_ptr(), m, v,
                                      d, 0, 0, st),
     }
