@@ -341,7 +341,10 @@ int sfl_rmsnorm_rows_scaled(const float* x, const void* w, void* act_xg, float* 
 
 /* x += A W^T (fp32, as sfl_gemm_bf16 with accumulate) and, from the updated
  * x: act_xg = bf16(x * gain_next) and ss_parts[p][r] = sum of x[r][f]^2 over
- * the features f of part p = f / 128 (ceil(n / 128) parts). n % 4 == 0. */
+ * the features f of part p = f / 128 (ceil(n / 128) parts). n % 4 == 0.
+ * act_xg must not overlap a (other workgroups may still be reading A while
+ * one writes its outputs); each part's sum has a fixed order, so results are
+ * the same from call to call. */
 int sfl_gemm_residual_norm(const void* a, const void* w, float* x, int m, int n, int k, const void* gain_next,
                            void* act_xg, float* ss_parts, void* stream);
 
