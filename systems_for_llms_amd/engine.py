@@ -256,7 +256,7 @@ class DecodeSession:
     # -- prefill ------------------------------------------------------------
     @torch.no_grad()
     def prefill(self, prompt: torch.Tensor, all_logits: bool = False,
-                forced: torch.Tensor | None = None) -> torch.Tensor | None:
+                forced: torch.Tensor | None = None, logits_dtype=torch.float32) -> torch.Tensor | None:
         """Process ``prompt [B, T]`` with MFMA GEMMs and masked attention, then pick token T.
 
         Fills the KV cache at positions 0..T-1, computes the logits of position
@@ -266,12 +266,17 @@ class DecodeSession:
         reference's ``forward``). bf16 models only; fp32 models use ``start`` +
         ``run`` (one position per step). ``forced [B, L]`` (L > T, starting with
         the prompt) makes the following positions up to L teacher-forced.
+        ``logits_dtype`` (float32 or bfloat16) is the type the all-positions
+        lm_head GEMM stores: bfloat16 rounds its fp32 sums once, as a cast of
+        the fp32 logits would, with half the stores and no cast pass.
         """
         if self.dtype != torch.bfloat16:
             raise TypeError("GEMM prefill needs a bfloat16 model; use start() + run() for float32")
         b, t = prompt.shape
         if b != self.batch or not 0 < t <= self.cap:
             raise ValueError("prompt must be [batch, T] with 0 < T <= capacity")
+        if logits_dtype not in (torch.float32, torch.bfloat16):
+            raise TypeError("logits_dtype must be torch.float32 or torch.bfloat16")
         low, high = torch.aminmax(prompt)
         if low.item() < 0 or high.item() >= self.vocab:
             raise ValueError("token ids must be in [0, vocab_size)")
@@ -348,9 +353,9 @@ class DecodeSession:
         if all_logits:
             call("sfl_rmsnorm_rows", x.data_ptr(), self.model.ln_final.weight.data_ptr(), act.data_ptr(),
                  m_rows, d, code, st)
-            logits = torch.empty((m_rows, v), device=dev, dtype=torch.float32)
+            logits = torch.empty((m_rows, v), device=dev, dtype=logits_dtype)
             call("sfl_gemm_bf16", act.data_ptr(), self.model.lm_head.weight.data_ptr(), logits.data_ptr(),
-                 m_rows, v, d, 0, 0, st)
+                 m_rows, v, d, int(logits_dtype == torch.bfloat16), 0, st)
             logits = logits.view(b, t, v)
         # Hand the last position to the decode head: pick token T and advance.
         self.x.copy_(x.view(b, t, d)[:, t - 1])

@@ -239,8 +239,8 @@ class TransformerLM(nn.Module):
         if self._gemm_prefill():
             # One pass of MFMA GEMMs and masked attention over the whole prompt.
             session = self.decode_session(ids.shape[0], t, deterministic=self.deterministic)
-            logits = session.prefill(ids, all_logits=True)
-            return logits.to(torch.bfloat16).reshape(*lead, t, self.vocab_size)
+            logits = session.prefill(ids, all_logits=True, logits_dtype=torch.bfloat16)
+            return logits.reshape(*lead, t, self.vocab_size)
         session = self.decode_session(ids.shape[0], t, record_logits=True, deterministic=self.deterministic)
         session.start(ids)
         session.run(t)

@@ -516,6 +516,23 @@ def test_prefill_folded_norm_stages_match_the_bf16_format_oracle(config):
     split_norm("next layer's attention norm", x2c, sdr["layers.1.attn_norm.weight"], act, ss, rsc)
 
 
+def test_prefill_bf16_logits_are_the_rounded_fp32_logits():
+    """The all-positions lm_head stores bf16 directly for forward(): bit-equal to rounding
+    the fp32 logits (one round-to-nearest-even of the same fp32 sums); forward() returns them."""
+    cfg = ModelConfig(vocab_size=500, context_length=96, d_model=256, num_layers=2, num_heads=4,
+                      d_ff=512, rope_theta=10000.0)
+    model = gpu_model(cfg, seeded_state_dict(cfg, 23))
+    ids = seeded_prompt(cfg.vocab_size, 3, 80, 24).cuda()
+    session = DecodeSession(model, 3, 96)
+    f32 = session.prefill(ids, all_logits=True)
+    b16 = session.prefill(ids, all_logits=True, logits_dtype=torch.bfloat16)
+    assert f32.dtype == torch.float32 and b16.dtype == torch.bfloat16
+    assert torch.equal(b16, f32.to(torch.bfloat16))
+    assert torch.equal(model(ids), b16)
+    with pytest.raises(TypeError):
+        session.prefill(ids, all_logits=True, logits_dtype=torch.float16)
+
+
 def test_generate_bf16_uses_prefill_and_matches_step_path():
     cfg = ModelConfig(vocab_size=500, context_length=96, d_model=256, num_layers=2, num_heads=4,
                       d_ff=512, rope_theta=10000.0)
