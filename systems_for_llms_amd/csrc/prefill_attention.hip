@@ -224,6 +224,7 @@ __global__ __launch_bounds__(kThreads) void masked_attention_kernel(AttnArgs a) 
   }
 
   float m_run = -INFINITY, l_run = 0.f;
+  float m_lim = -INFINITY, m_sub = 0.f;  // m_run + kLazyMax and the subtracted maximum
   f32x4 oacc[DT];
 #pragma unroll
   for (int t = 0; t < DT; ++t) oacc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -283,15 +284,25 @@ __global__ __launch_bounds__(kThreads) void masked_attention_kernel(AttnArgs a) 
         sacc[j] = mfma16<T>(ka, qreg[ks], sacc[j]);
       }
     }
-    const bool tail = k0 + BK > n || qrow >= n;
+    // Unscaled scores (the scale goes into the exponent). Full tiles inside the
+    // sequence need no mask (rows past n are never stored); the branch is
+    // wave-uniform. Other tiles evaluate the mask without branches: with the
+    // short-circuit allowed() inside a per-lane branch, selecting the unchanged
+    // accumulator value made the compiler write -inf into that accumulator
+    // register for every lane of the branch, the admissible ones included.
+    const bool fast = full && k0 + BK <= n;
     float sv[16];
+    if (fast) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+      for (int e = 0; e < 16; ++e) sv[e] = sacc[e / 4][e % 4];
+    } else {
+      const int64_t dq = a.m.docs ? a.m.docs[min(qrow, n - 1)] : 0;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int key = k0 + 16 * j + 4 * grp + i;
-        const bool ok = (full && !tail) ? true : (full ? (key < n && qrow < n) : allowed(a.m, qrow, key, n));
-        sv[4 * j + i] = ok ? sacc[j][i] * a.scale_log2 : -INFINITY;
+      for (int e = 0; e < 16; ++e) {
+        const int key = k0 + 16 * (e / 4) + 4 * grp + e % 4;
+        const int64_t dk = a.m.docs ? a.m.docs[min(key, n - 1)] : 0;
+        const bool ok = full ? (key < n) & (qrow < n) : allowed_flat(a.m, qrow, key, n, dq, dk);
+        sv[e] = ok ? sacc[e / 4][e % 4] : -INFINITY;
       }
     }
     float mx = sv[0];
@@ -299,34 +310,41 @@ __global__ __launch_bounds__(kThreads) void masked_attention_kernel(AttnArgs a) 
     for (int e = 1; e < 16; ++e) mx = fmaxf(mx, sv[e]);
     mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
     mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
-    const float m_new = fmaxf(m_run, mx);
-    const float ms = m_new == -INFINITY ? 0.f : m_new;
-    const float alpha = exp2f(m_run - ms);
+    // The softmax of the other kernels of this file: a lazy running maximum
+    // (it moves only when a tile's maximum exceeds it by more than kLazyMax
+    // log2 units), p = 2^(s * c - m) with one FMA, p stored in T for the P V
+    // product, and the row sum taken over those stored values, so the output
+    // is exactly sum(p v) / sum(p) of the weights the product used.
+    const float cs = a.scale_log2;
+    const bool grow = mx * cs > m_lim;  // false for a fully masked row (mx = -inf)
+    float alpha = 1.f;
+    if (grow) {
+      alpha = exp2f(m_run - mx * cs);  // 0 for the first admissible tile
+      m_run = mx * cs;
+      m_lim = m_run + kLazyMax;
+      m_sub = m_run;
+    }
+    if (__ballot(alpha != 1.f)) {  // wave-uniform: skip the rescale while no maximum moves
+#pragma unroll
+      for (int t = 0; t < DT; ++t) oacc[t] *= alpha;
+    }
+    uint32_t pk[8];
     float psum = 0.f;
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      sv[e] = exp2f(sv[e] - ms);
-      psum += sv[e];
+    for (int e = 0; e < 8; ++e) {
+      pk[e] = pack2<T>(exp2f(fmaf(sv[2 * e], cs, -m_sub)), exp2f(fmaf(sv[2 * e + 1], cs, -m_sub)));
+      psum = add_pair<T>(pk[e], psum);
     }
     psum += __shfl_xor(psum, 16, kWave);
     psum += __shfl_xor(psum, 32, kWave);
     l_run = l_run * alpha + psum;
-    m_run = m_new;
-#pragma unroll
-    for (int t = 0; t < DT; ++t) oacc[t] *= alpha;
 
     // O^T += V^T P^T. Step s covers subtiles 2s and 2s+1; element e of the
-    // lane's operands is key 16*(2s + e/4) + 4*grp + e%4 for both operands.
+    // lane's operands is key 16*(2s + e/4) + 4*grp + e%4 for both operands
+    // (the pair (4*(2s + e/2) + (2e)%4, +1) of sv is pk[4s + e]).
 #pragma unroll
     for (int s2 = 0; s2 < 2; ++s2) {
-      uint32_t pb[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float lo = sv[4 * (2 * s2 + e / 2) + (2 * e) % 4];
-        const float hi = sv[4 * (2 * s2 + e / 2) + (2 * e) % 4 + 1];
-        pb[e] = uint32_t(to_bits<T>(lo)) | (uint32_t(to_bits<T>(hi)) << 16);
-      }
-      const u32x4 pop = {pb[0], pb[1], pb[2], pb[3]};
+      const u32x4 pop = {pk[4 * s2], pk[4 * s2 + 1], pk[4 * s2 + 2], pk[4 * s2 + 3]};
 #pragma unroll
       for (int t = 0; t < DT; ++t) {
         const uint16_t* vrow = vt_s + (16 * t + col) * LDV;
@@ -348,7 +366,7 @@ __global__ __launch_bounds__(kThreads) void masked_attention_kernel(AttnArgs a) 
     *reinterpret_cast<uint2*>(op + 16 * t + 4 * grp) = make_uint2(lo, hi);
   }
   if (a.lse && grp == 0) {
-    const float lse = l_run > 0.f ? (m_run + log2f(l_run)) * 0.6931471805599453f : -INFINITY;
+    const float lse = l_run > 0.f ? (m_sub + log2f(l_run)) * 0.6931471805599453f : -INFINITY;
     a.lse[(long(b) * a.heads + h) * n + qrow] = lse;
   }
 }
@@ -417,33 +435,36 @@ __device__ __forceinline__ void tile_math(const AttnArgs& a, const u32x4 (&kc)[4
     mx = fmaxf(mx, sv[15]);
     mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
     mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+    // The lazy maximum and stored-probability row sums of masked_attention32_kernel:
+    // m_run (the subtracted maximum) moves only when the tile's maximum exceeds
+    // it by more than kLazyMax log2 units, and l sums the T-rounded probabilities
+    // that the P V product uses.
     const float c = a.scale_log2;
-    const float m_new = fmaxf(m_run[qs], mx * c);
-    const float ms = m_new == -INFINITY ? 0.f : m_new;
-    const float alpha = __builtin_amdgcn_exp2f(m_run[qs] - ms);
+    const bool grow = mx * c > m_run[qs] + kLazyMax;  // false for a fully masked row
+    const float alpha = grow ? __builtin_amdgcn_exp2f(m_run[qs] - mx * c) : 1.f;
+    if (grow) m_run[qs] = mx * c;
+    const float ms = m_run[qs] == -INFINITY ? 0.f : m_run[qs];
+    uint32_t pk[8];
     float psum = 0.f;
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      sv[e] = __builtin_amdgcn_exp2f(fmaf(sv[e], c, -ms));
-      psum += sv[e];
+    for (int e = 0; e < 8; ++e) {
+      pk[e] = pack2<T>(__builtin_amdgcn_exp2f(fmaf(sv[2 * e], c, -ms)),
+                       __builtin_amdgcn_exp2f(fmaf(sv[2 * e + 1], c, -ms)));
+      psum = add_pair<T>(pk[e], psum);
     }
     psum += __shfl_xor(psum, 16, kWave);
     psum += __shfl_xor(psum, 32, kWave);
     l_run[qs] = l_run[qs] * alpha + psum;
-    m_run[qs] = m_new;
-    if (__ballot(alpha != 1.f)) {  // wave-uniform: skip the rescale once the maxima settle
+    if (__ballot(alpha != 1.f)) {  // wave-uniform: skip the rescale while no maximum moves
 #pragma unroll
       for (int t = 0; t < DT; ++t) oacc[qs][t] *= alpha;
     }
 
-    // O^T += V^T P^T; the key order makes the B operand the lane's own probabilities.
+    // O^T += V^T P^T; the key order makes the B operand the lane's own probabilities
+    // (element e of step s2 is the pair pk[4 s2 + e]).
 #pragma unroll
     for (int s2 = 0; s2 < 2; ++s2) {
-      uint32_t pb[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        pb[e] = pack2<T>(sv[4 * (2 * s2 + e / 2) + (2 * e) % 4], sv[4 * (2 * s2 + e / 2) + (2 * e) % 4 + 1]);
-      const u32x4 pop = {pb[0], pb[1], pb[2], pb[3]};
+      const u32x4 pop = {pk[4 * s2], pk[4 * s2 + 1], pk[4 * s2 + 2], pk[4 * s2 + 3]};
 #pragma unroll
       for (int t = 0; t < DT; ++t) oacc[qs][t] = mfma16<T>(vop[s2][t], pop, oacc[qs][t]);
     }

@@ -61,6 +61,10 @@ def test_config3_prefill_and_decode_to_4096_teacher_forced():
     ref_cache.step(rows[:, :PROMPT])
     ref = ref_cache.step(rows[:, PROMPT:])
     del ref_cache
+    rw_cache = om.KVCacheOracle(om.round_weights(sd), cfg, len(ROWS), CONTEXT)  # fp32 on the bf16 weights
+    rw_cache.step(rows[:, :PROMPT])
+    rw = rw_cache.step(rows[:, PROMPT:])
+    del rw_cache
     floors = []
     for wide, batch in ((False, rows), (True, rows[:1])):
         cache = om.KVCacheOracle(om.round_weights(sd), cfg, batch.shape[0], CONTEXT, kv_dtype=torch.bfloat16)
@@ -71,5 +75,8 @@ def test_config3_prefill_and_decode_to_4096_teacher_forced():
     floor, wide = floors
     first, last = slice(0, 64), slice(-32, None)
     for name, sl in (("3072..3135", first), ("4063..4094", last), ("3072..4094", slice(None))):
+        # Cap 5e-2 against fp32 on the unrounded seeds: rounding the 24 layers' weights to
+        # bf16 alone (the floor) moves these logits by 0.038-0.046; the strict 2e-2 bound
+        # holds against fp32 on the bf16 weights themselves.
         bf16_gate(f"config3 rows 0,15, positions {name}", got[:, sl], ref[:, sl], floor[:, sl],
-                  envelope=(floor[:1, sl], wide[:, sl]))
+                  envelope=(floor[:1, sl], wide[:, sl]), ref_bf16_weights=rw[:, sl], cap=(5e-2, 0.95))

@@ -299,6 +299,7 @@ def test_config2_prefill_then_decode_teacher_forced():
     seq = seeded_prompt(cfg.vocab_size, 8, ctx, 2027)
     torch.set_num_threads(16)
     ref = om.KVCacheOracle(sd, cfg, 8, ctx).step(seq)
+    rw = om.KVCacheOracle(om.round_weights(sd), cfg, 8, ctx).step(seq)
     model = gpu_model(cfg, sd)
     session = DecodeSession(model, 8, ctx, record_logits=True)
     all_logits = session.prefill(seq[:, :512].cuda(), all_logits=True, forced=seq.cuda())
@@ -307,15 +308,42 @@ def test_config2_prefill_then_decode_teacher_forced():
     assert session.prefill_norm_folded  # d_model and d_ff are multiples of 64
     floor = format_floor(sd, cfg, seq, 512, fold=True)
     wide = format_floor(sd, cfg, seq, 512, wide=True, fold=True)  # the drift over the same rows the gates compare
+    unfolded = format_floor(sd, cfg, seq, 512, fold=False)
     pre = all_logits.cpu()
     dec = session.logits[:, 512:ctx - 1].float().cpu()
     bf16_gate("config2 prefill (positions 0..511)", pre, ref[:, :512], floor[:, :512],
-              envelope=(floor[:, :512], wide[:, :512]))
+              envelope=(floor[:, :512], wide[:, :512]), ref_bf16_weights=rw[:, :512],
+              unfolded_floor=unfolded[:, :512])
     bf16_gate(f"config2 decode after prefill (positions 512..{ctx - 2})", dec, ref[:, 512:ctx - 1],
-              floor[:, 512:ctx - 1], envelope=(floor[:, 512:ctx - 1], wide[:, 512:ctx - 1]))
+              floor[:, 512:ctx - 1], envelope=(floor[:, 512:ctx - 1], wide[:, 512:ctx - 1]),
+              ref_bf16_weights=rw[:, 512:ctx - 1], unfolded_floor=unfolded[:, 512:ctx - 1])
     # The decode head after prefill (fp32 inputs) equals the prefill's own last-position
     # logits (bf16 GEMM inputs) up to the rounding of the final norm's output.
     torch.testing.assert_close(session.logits[:, 511].float().cpu(), pre[:, 511], atol=2e-2, rtol=0)
+
+
+@pytest.mark.parametrize("fold", [True, False])
+def test_pilot_prefill_with_and_without_folded_norms(fold):
+    """22.7M pilot model (head dim 32), batch 4, 200 prompt tokens, all-positions logits: the
+    prefill with its norms folded into the GEMMs and the one with separate norm passes, each
+    against the storage floor of its own rounding points and the fp32 references (the gates
+    of config 2)."""
+    cfg = load_model_config("pilot-22m-s256")
+    sd = seeded_state_dict(cfg, 7)
+    seq = seeded_prompt(cfg.vocab_size, 4, 200, 8)
+    model = gpu_model(cfg, sd)
+    session = DecodeSession(model, 4, 256)
+    session.fold_prefill_norm = fold
+    got = session.prefill(seq.cuda(), all_logits=True).cpu()
+    assert session.prefill_norm_folded == fold  # d_model 512 and d_ff 1344 are multiples of 64
+    torch.set_num_threads(16)
+    ref = om.KVCacheOracle(sd, cfg, 4, 256).step(seq)
+    rw = om.KVCacheOracle(om.round_weights(sd), cfg, 4, 256).step(seq)
+    floor = format_floor(sd, cfg, seq, 200, fold=fold)
+    wide = format_floor(sd, cfg, seq, 200, wide=True, fold=fold)
+    unfolded = format_floor(sd, cfg, seq, 200, fold=False) if fold else None
+    bf16_gate(f"pilot prefill, norms {'folded' if fold else 'separate'}", got, ref, floor, envelope=(floor, wide),
+              ref_bf16_weights=rw, unfolded_floor=unfolded)
 
 
 def _ulp_close(name, got, ref, max_frac, cancel=2 ** -17):
@@ -337,7 +365,7 @@ def _ulp_close(name, got, ref, max_frac, cancel=2 ** -17):
     assert worst <= 0, f"{name}: a difference exceeds one bf16 ulp"
 
 
-@pytest.mark.parametrize("config", ["scale-100m-s1024", "scale-324m-s4096"])
+@pytest.mark.parametrize("config", ["pilot-22m-s256", "scale-100m-s1024", "scale-324m-s4096"])
 def test_prefill_layer_stages_match_the_bf16_format_oracle(config):
     """Each stage of one prefill layer, fed the GPU's own inputs, against the bf16-format oracle:
     bf16 outputs equal up to rare 1-ulp flips (fp32 reassociation at a rounding boundary), fp32
@@ -346,7 +374,7 @@ def test_prefill_layer_stages_match_the_bf16_format_oracle(config):
     cfg = load_model_config(config)
     sd = seeded_state_dict(cfg, 1337)
     sdr = om.round_weights(sd)
-    b, t = 2, 512
+    b, t = 2, min(512, cfg.context_length)
     ids = seeded_prompt(cfg.vocab_size, b, t, 2027)
     model = gpu_model(cfg, sd)
     session = DecodeSession(model, b, t)
@@ -410,20 +438,22 @@ def test_prefill_layer_stages_match_the_bf16_format_oracle(config):
     torch.testing.assert_close(x.cpu(), x2_ref, atol=1e-5, rtol=1e-5)
 
 
-@pytest.mark.parametrize("config", ["scale-100m-s1024", "scale-324m-s4096"])
+@pytest.mark.parametrize("config", ["pilot-22m-s256", "scale-100m-s1024", "scale-324m-s4096"])
 def test_prefill_folded_norm_stages_match_the_bf16_format_oracle(config):
-    """One prefill layer with its norms folded into the GEMMs, each stage fed the GPU's own
+    """Every layer of a prefill with its norms folded into the GEMMs, each stage fed the GPU's own
     inputs: the norm inputs bf16(x * g) bit-exact, the scales 1 / rms(x) and fp32 residual
-    updates to fp32 rounding, the scaled GEMM outputs up to rare 1-ulp flips; with unit
-    scales the scaled GEMMs are the plain ones, bit for bit."""
+    updates to fp32 rounding, the scaled GEMM outputs up to rare 1-ulp flips, the attention (head
+    dim 32 on the pilot, 64 otherwise) with its probabilities stored in bf16 as the oracle's
+    stored-probability floor computes it; with unit scales the scaled GEMMs are the plain ones,
+    bit for bit (layer 0)."""
     cfg = load_model_config(config)
     sd = seeded_state_dict(cfg, 1337)
     sdr = om.round_weights(sd)
-    b, t = 2, 512
+    b, t = 2, min(512, cfg.context_length)
     ids = seeded_prompt(cfg.vocab_size, b, t, 2027)
     model = gpu_model(cfg, sd)
     session = DecodeSession(model, b, t)
-    d, h, f = cfg.d_model, cfg.num_heads, cfg.d_ff
+    d, h, f, nl = cfg.d_model, cfg.num_heads, cfg.d_ff, cfg.num_layers
     dk, m, parts = d // h, b * t, -(-d // 128)
     x = torch.empty((m, d), device="cuda")
     act = torch.empty((m, d), device="cuda", dtype=torch.bfloat16)
@@ -433,87 +463,113 @@ def test_prefill_folded_norm_stages_match_the_bf16_format_oracle(config):
     ss = torch.empty((parts, m), device="cuda")
     rsc = torch.empty((m,), device="cuda")
     ones = torch.ones((m,), device="cuda")
-    blk, nxt, kc, vc = model.layers[0], model.layers[1], session.k_cache[0], session.v_cache[0]
-    w13 = session.weights.w13()[0]
+    w13 = session.weights.w13()
     gid = ids.cuda().view(-1)
     st = _lib.stream_handle()
     call = _lib.call
+    from systems_for_llms_amd.attention import causal_prefill
 
-    def qkv(scale):
-        args = (session.wqkv[0].data_ptr(),) + ((scale.data_ptr(),) if scale is not None else ())
+    def qkv(layer, scale):
+        kc, vc = session.k_cache[layer], session.v_cache[layer]
+        args = (session.wqkv[layer].data_ptr(),) + ((scale.data_ptr(),) if scale is not None else ())
         call("sfl_gemm_qkv_rope_scaled" if scale is not None else "sfl_gemm_qkv_rope", act.data_ptr(), *args, m, t,
              d, h, session.cos_fm.data_ptr(), session.sin_fm.data_ptr(), q.data_ptr(), kc.data_ptr(), vc.data_ptr(),
              session.cap, st)
         return q.clone(), kc[:, :, :t].clone(), vc[:, :, :t].clone()
 
-    def swiglu(scale):
+    def swiglu(layer, scale):
         if scale is None:
-            call("sfl_gemm_swiglu", act.data_ptr(), w13.data_ptr(), hid.data_ptr(), m, f, d, st)
+            call("sfl_gemm_swiglu", act.data_ptr(), w13[layer].data_ptr(), hid.data_ptr(), m, f, d, st)
         else:
-            call("sfl_gemm_swiglu_scaled", act.data_ptr(), w13.data_ptr(), scale.data_ptr(), hid.data_ptr(), m, f,
-                 d, st)
+            call("sfl_gemm_swiglu_scaled", act.data_ptr(), w13[layer].data_ptr(), scale.data_ptr(), hid.data_ptr(), m,
+                 f, d, st)
         return hid.clone()
 
+    # The prefill's own launch sequence (engine.DecodeSession.prefill with folded norms), every
+    # intermediate kept: layer i's inputs are the GPU's outputs of layer i - 1.
     call("sfl_embed_rows", gid.data_ptr(), model.token_embeddings.weight.data_ptr(), x.data_ptr(), m, d, 1, st)
-    x0 = x.clone()
-    call("sfl_rmsnorm_rows_scaled", x.data_ptr(), blk.attn_norm.weight.data_ptr(), act.data_ptr(), rsc.data_ptr(),
-         m, d, 1, st)
-    act1, r1 = act.clone(), rsc.clone()
-    plain, unit = qkv(None), qkv(ones)
-    for p_, u_ in zip(plain, unit):
-        assert torch.equal(p_, u_), "unit scales change the q/k/v GEMM"
-    q1, k1, v1 = qkv(rsc)
-    from systems_for_llms_amd.attention import causal_prefill
-    causal_prefill(q, kc[:, :, :t], vc[:, :, :t], attn.transpose(1, 2))
-    call("sfl_gemm_residual_norm", attn.data_ptr(), blk.attn.output_proj.weight.data_ptr(), x.data_ptr(), m, d, d,
-         blk.ffn_norm.weight.data_ptr(), act.data_ptr(), ss.data_ptr(), st)
-    x1, act2, ss2 = x.clone(), act.clone(), ss.clone()
-    call("sfl_norm_scale", ss.data_ptr(), parts, m, d, rsc.data_ptr(), st)
-    r2 = rsc.clone()
-    assert torch.equal(swiglu(None), swiglu(ones)), "unit scales change the SwiGLU GEMM"
-    hid2 = swiglu(rsc)
-    call("sfl_gemm_residual_norm", hid.data_ptr(), blk.ffn.w2.weight.data_ptr(), x.data_ptr(), m, d, f,
-         nxt.attn_norm.weight.data_ptr(), act.data_ptr(), ss.data_ptr(), st)
-    call("sfl_norm_scale", ss.data_ptr(), parts, m, d, rsc.data_ptr(), st)
-    torch.cuda.synchronize()
+    call("sfl_rmsnorm_rows_scaled", x.data_ptr(), model.layers[0].attn_norm.weight.data_ptr(), act.data_ptr(),
+         rsc.data_ptr(), m, d, 1, st)
+    recs = []
+    for layer in range(nl):
+        blk = model.layers[layer]
+        # ss1: the previous w2 GEMM's sums of squares behind r1 (layer 0's scale comes from the norm pass)
+        rec = {"x0": x.clone(), "act1": act.clone(), "r1": rsc.clone(), "ss1": ss.clone()}
+        if layer == 0:
+            plain, unit = qkv(0, None), qkv(0, ones)
+            for p_, u_ in zip(plain, unit):
+                assert torch.equal(p_, u_), "unit scales change the q/k/v GEMM"
+        rec["q"], rec["k"], rec["v"] = qkv(layer, rsc)
+        kc, vc = session.k_cache[layer], session.v_cache[layer]
+        causal_prefill(q, kc[:, :, :t], vc[:, :, :t], attn.transpose(1, 2))
+        rec["attn"] = attn.clone()
+        call("sfl_gemm_residual_norm", attn.data_ptr(), blk.attn.output_proj.weight.data_ptr(), x.data_ptr(), m, d,
+             d, blk.ffn_norm.weight.data_ptr(), act.data_ptr(), ss.data_ptr(), st)
+        rec["x1"], rec["act2"], rec["ss2"] = x.clone(), act.clone(), ss.clone()
+        call("sfl_norm_scale", ss.data_ptr(), parts, m, d, rsc.data_ptr(), st)
+        rec["r2"] = rsc.clone()
+        if layer == 0:
+            assert torch.equal(swiglu(0, None), swiglu(0, ones)), "unit scales change the SwiGLU GEMM"
+        rec["hid"] = swiglu(layer, rsc)
+        if layer + 1 < nl:
+            call("sfl_gemm_residual_norm", hid.data_ptr(), blk.ffn.w2.weight.data_ptr(), x.data_ptr(), m, d, f,
+                 model.layers[layer + 1].attn_norm.weight.data_ptr(), act.data_ptr(), ss.data_ptr(), st)
+            call("sfl_norm_scale", ss.data_ptr(), parts, m, d, rsc.data_ptr(), st)
+        else:  # the last layer's w2 only adds into x (the final norm is a separate pass)
+            call("sfl_gemm_bf16", hid.data_ptr(), blk.ffn.w2.weight.data_ptr(), x.data_ptr(), m, d, f, 0, 1, st)
+        torch.cuda.synchronize()
+        recs.append({k: v.cpu() for k, v in rec.items()})
+    x_end = x.cpu()
 
     torch.set_num_threads(16)
-    bf, p = torch.bfloat16, "layers.0."
+    bf = torch.bfloat16
     cos, sin = om.rope_tables(cfg.rope_theta, dk, cfg.context_length)
     pos = torch.arange(t)
+    mask = torch.tril(torch.ones(t, t, dtype=torch.bool))
 
     def inv_rms(xx):
         return 1 / torch.sqrt((xx * xx).mean(-1) + om.EPS)
 
     def split_norm(name, xx, gain, act_, ss_, r_):
-        assert torch.equal(act_.cpu(), (xx * gain).bfloat16()), f"{name}: norm input is not bf16(x * g)"
+        assert torch.equal(act_, (xx * gain).bfloat16()), f"{name}: norm input is not bf16(x * g)"
         if ss_ is not None:
             sq = (xx * xx).view(m, parts, 128).sum(-1).t()
-            torch.testing.assert_close(ss_.cpu(), sq, rtol=1e-5, atol=1e-6 * sq.max().item())
-        torch.testing.assert_close(r_.cpu(), inv_rms(xx), rtol=1e-5, atol=0)
+            torch.testing.assert_close(ss_, sq, rtol=1e-5, atol=1e-6 * sq.max().item())
+        torch.testing.assert_close(r_, inv_rms(xx), rtol=1e-5, atol=0)
 
-    x0c = x0.cpu()
-    assert torch.equal(x0c, sdr["token_embeddings.weight"][ids].reshape(m, d))
-    split_norm("attention norm", x0c, sdr[p + "attn_norm.weight"], act1, None, r1)
-    a1, s1 = act1.float().cpu().view(b, t, d), r1.cpu().view(b, t, 1)
+    assert torch.equal(recs[0]["x0"], sdr["token_embeddings.weight"][ids].reshape(m, d))
+    for layer, rec in enumerate(recs):
+        p = f"layers.{layer}."
+        tag = f"layer {layer}"
+        if layer == 0:
+            split_norm(f"{tag} attention norm", rec["x0"], sdr[p + "attn_norm.weight"], rec["act1"], None, rec["r1"])
+        a1, s1 = rec["act1"].float().view(b, t, d), rec["r1"].view(b, t, 1)
 
-    def proj(name):
-        return om._split_heads(om._linear(a1, sdr[p + f"attn.{name}_proj.weight"]) * s1, h)
-    _ulp_close("q (scaled, RoPE)", q1, om._round(om.rope(proj("q"), cos, sin, pos), bf), 2e-3)
-    _ulp_close("k cache (scaled, RoPE)", k1, om._round(om.rope(proj("k"), cos, sin, pos), bf), 2e-3)
-    _ulp_close("v cache (scaled)", v1, om._round(proj("v"), bf), 2e-3)
-    x1c = x1.cpu()
-    torch.testing.assert_close(x1c, x0c + om._linear(attn.float().cpu().view(m, d), sdr[p + "attn.output_proj.weight"]),
-                               atol=1e-5, rtol=1e-5)
-    split_norm("ffn norm", x1c, sdr[p + "ffn_norm.weight"], act2, ss2, r2)
-    a2, s2 = act2.float().cpu(), r2.cpu()[:, None]
-    g1 = om._linear(a2, sdr[p + "ffn.w1.weight"]) * s2
-    g3 = om._linear(a2, sdr[p + "ffn.w3.weight"]) * s2
-    _ulp_close("SwiGLU hidden (scaled)", hid2, om._round(g1 * torch.sigmoid(g1) * g3, bf), 2e-3)
-    x2c = x.cpu()
-    torch.testing.assert_close(x2c, x1c + om._linear(hid2.float().cpu(), sdr[p + "ffn.w2.weight"]), atol=1e-5,
-                               rtol=1e-5)
-    split_norm("next layer's attention norm", x2c, sdr["layers.1.attn_norm.weight"], act, ss, rsc)
+        def proj(name):
+            return om._split_heads(om._linear(a1, sdr[p + f"attn.{name}_proj.weight"]) * s1, h)
+        _ulp_close(f"{tag} q (scaled, RoPE)", rec["q"], om._round(om.rope(proj("q"), cos, sin, pos), bf), 2e-3)
+        _ulp_close(f"{tag} k cache (scaled, RoPE)", rec["k"], om._round(om.rope(proj("k"), cos, sin, pos), bf), 2e-3)
+        _ulp_close(f"{tag} v cache (scaled)", rec["v"], om._round(proj("v"), bf), 2e-3)
+        qg, kg, vg = rec["q"].float(), rec["k"].float(), rec["v"].float()
+        stored = om._round(om._merge_heads(om.attention_core(qg, kg, vg, mask, bf)), bf)
+        _ulp_close(f"{tag} attention (bf16 probabilities, head dim {dk})", rec["attn"].view(b, t, d), stored, 2e-3,
+                   cancel=2 ** -8)
+        x1c = rec["x1"]
+        torch.testing.assert_close(x1c, rec["x0"] + om._linear(rec["attn"].float().view(m, d),
+                                                               sdr[p + "attn.output_proj.weight"]),
+                                   atol=1e-5, rtol=1e-5)
+        split_norm(f"{tag} ffn norm", x1c, sdr[p + "ffn_norm.weight"], rec["act2"], rec["ss2"], rec["r2"])
+        a2, s2 = rec["act2"].float(), rec["r2"][:, None]
+        g1 = om._linear(a2, sdr[p + "ffn.w1.weight"]) * s2
+        g3 = om._linear(a2, sdr[p + "ffn.w3.weight"]) * s2
+        _ulp_close(f"{tag} SwiGLU hidden (scaled)", rec["hid"], om._round(g1 * torch.sigmoid(g1) * g3, bf), 2e-3)
+        x2c = recs[layer + 1]["x0"] if layer + 1 < nl else x_end
+        torch.testing.assert_close(x2c, x1c + om._linear(rec["hid"].float(), sdr[p + "ffn.w2.weight"]), atol=1e-5,
+                                   rtol=1e-5)
+        if layer + 1 < nl:
+            nxt = recs[layer + 1]
+            split_norm(f"layer {layer + 1} attention norm", x2c, sdr[f"layers.{layer + 1}.attn_norm.weight"],
+                       nxt["act1"], nxt["ss1"], nxt["r1"])
 
 
 def test_prefill_bf16_logits_are_the_rounded_fp32_logits():
