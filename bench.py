@@ -269,6 +269,38 @@ def profile_target_attention(reps: int = 24) -> int:
 
 
 
+def profile_target_decode(steps: int = 4) -> int:
+    """Counter-collection target: ``steps`` eager decode steps of the 324M model at B=16
+    and attention length 3584 (every launch of the step: the q/k/v, SwiGLU, w2 and
+    lm_head GEMVs, the fused attention, the token step), then one device copy of
+    256 MiB whose HBM traffic is known (256 MiB read + 256 MiB written). The cache
+    holds zeros (traffic and time do not depend on its values); every GEMV streams
+    its weights from HBM as in the decode loop, since a step reads more than the
+    256 MB last-level cache holds. Run it under ``rocprofv3 --pmc FETCH_SIZE`` and
+    ``--pmc WRITE_SIZE``, or ``--kernel-trace --stats``."""
+    import torch
+
+    from systems_for_llms_amd.config import load_model_config
+    from systems_for_llms_amd.engine import DecodeSession
+    from systems_for_llms_amd.model import TransformerLM
+    from systems_for_llms_amd.weights import seeded_state_dict
+
+    cfg = load_model_config("scale-324m-s4096")
+    model = TransformerLM.from_config(cfg, device="cuda", dtype=torch.bfloat16)
+    model.load_state_dict(seeded_state_dict(cfg, WEIGHT_SEED))
+    session = DecodeSession(model.eval(), BATCH, CONTEXT)
+    session.set_position(MEAN_LEN - 1)  # attention length MEAN_LEN at the first step
+    for _ in range(steps):
+        session.step()
+    src = torch.ones(256 << 20, device="cuda", dtype=torch.uint8)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"profile target: {steps} eager decode steps (324M, B={BATCH}, attention lengths {MEAN_LEN}.."
+        f"{MEAN_LEN + steps - 1}) + one 256 MiB copy")
+    return 0
+
+
 def profile_target_gqa(reps: int = 40) -> int:
     """Kernel-trace target for grouped-query decode attention on the matrix cores.
 
@@ -379,11 +411,13 @@ def main() -> int:
     parser.add_argument("--no-reference-shapes", action="store_true",
                         help="skip timing the reference's published attention shapes")
     parser.add_argument("--attention-reps", type=int, default=50)
-    parser.add_argument("--profile-target", choices=["attention", "gqa", "masked", "gemm"], default=None,
-                        help="run only a profiling target (profile_target_attention, _gqa, _masked, _gemm)")
+    parser.add_argument("--profile-target", choices=["attention", "decode", "gqa", "masked", "gemm"], default=None,
+                        help="run only a profiling target (profile_target_attention, _decode, _gqa, _masked, _gemm)")
     args = parser.parse_args()
     if args.profile_target == "attention":
         return profile_target_attention()
+    if args.profile_target == "decode":
+        return profile_target_decode()
     if args.profile_target == "gqa":
         return profile_target_gqa()
     if args.profile_target == "masked":

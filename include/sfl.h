@@ -14,7 +14,8 @@
  * entry points weights and the KV cache use the model dtype; the residual
  * stream x and q are fp32; the GEMV inputs that other kernels produce (the
  * attention output, the SwiGLU hidden state, x * g) are in the activation
- * layout: SFL_DTYPE_F32X for F32 models and SFL_DTYPE_BF16X2 for BF16 models.
+ * layout: SFL_DTYPE_F32X for F32 models, SFL_DTYPE_BF16X2 for BF16 models and
+ * SFL_DTYPE_F16X2 for F16 models.
  */
 #ifndef SFL_H_
 #define SFL_H_
@@ -40,6 +41,9 @@ enum {
    * Buffers hold whole 16-row blocks: ceil(B/16) * 16 * K * 4 bytes. */
   SFL_DTYPE_BF16X2 = 3,
   SFL_DTYPE_F32X = 4,
+  /* F16X2: the BF16X2 layout for F16 models; hi = the value rounded to fp16,
+   * lo = the remainder rounded to fp16. */
+  SFL_DTYPE_F16X2 = 5,
 };
 
 enum {
@@ -70,8 +74,8 @@ const char* sfl_last_error(void);
  * ceil(cap/splits) keys (decode.cu:50-52); chunks past a row's length do no
  * work. D in {16, 32, 64, 128}; Hq/Hkv in {1, 2, 4, 8}; splits in [1, 1024].
  * kv_dtype: element type of k and v (F32, BF16 or F16); q_dtype: kv_dtype or
- * F32; out_dtype: kv_dtype, F32, BF16X2 or F32X (the last two: the GEMV
- * activation layout of [B, Hq*D]). Softmax state is fp32. Cache rows at
+ * F32; out_dtype: kv_dtype, F32, BF16X2, F16X2 or F32X (the last three: the
+ * GEMV activation layout of [B, Hq*D]). Softmax state is fp32. Cache rows at
  * positions >= lengths[b] are never read into the result (they may hold
  * anything, NaN included). Hq/Hkv >= 4 with D 64 or 128, q_dtype ==
  * kv_dtype in {BF16, F16}, 16-byte aligned q/k/v and cap*D*2 < 2^31 run
@@ -114,10 +118,10 @@ long sfl_decode_attention_static_scratch_bytes(void);
  * the projection to x with fp32 atomics, so the summation order varies from
  * call to call.
  *   q        [batch, heads, head_dim] fp32 (RoPE applied)
- *   k, v     [batch, heads, capacity, head_dim] in the model dtype (F32 or BF16)
+ *   k, v     [batch, heads, capacity, head_dim] in the model dtype (F32, BF16 or F16)
  *   lengths  [batch] int32; w_out: output_proj packed by sfl_pack_gemv_weights
  *   x        fp32 [batch, heads*head_dim], updated in place (16-byte aligned)
- * head_dim: a power of two in [32, 128] (bf16) or [16, 128] (fp32).
+ * head_dim: a power of two in [32, 128] (bf16, fp16) or [16, 128] (fp32).
  */
 int sfl_decode_attention_out_proj(const float* q, const void* k, const void* v,
                                   const int32_t* lengths, const void* w_out, float* x, int batch,
@@ -125,7 +129,7 @@ int sfl_decode_attention_out_proj(const float* q, const void* k, const void* v,
                                   void* stream);
 
 
-/* ---- decode step of the llmlab decoder (model dtype F32 or BF16) ----------
+/* ---- decode step of the llmlab decoder (model dtype F32, BF16 or F16) -----
  * One step processes one token per sequence for `batch` <= 65536 sequences.
  * The GEMVs run one workgroup per 16 output features and block of 16 batch
  * rows; the blocks of one weight tile share an XCD, so the weights stream
@@ -221,13 +225,14 @@ int sfl_embedding_gather(const int64_t* tokens, long token_stride, const int32_t
 
 /*
  * Greedy step: argmax over the lm_head tiles (first maximal index, as
- * torch.argmax), then, with np = pos[b] + 1: predicted[b, np] = argmax;
+ * torch.argmax) -- best_val/best_idx [tiles, best_stride] as sfl_rmsnorm_lm_head
+ * wrote them, with the same best_stride (>= batch) -- then, with np = pos[b] + 1: predicted[b, np] = argmax;
  * tokens[b, np] = argmax unless np < prompt_len[b] (the prompt token is kept);
  * x[b] = emb[tokens[b, np]] (fp32, d_model % 16 == 0); pos[b] = np; lengths[b] = np + 1.
  * Nothing changes for a row whose np would reach capacity. The reference has
  * no token loop; its greedy continuation is argmax(TransformerLM.forward(ids)[:, -1]).
  */
-int sfl_next_token(const float* best_val, const int32_t* best_idx, int tiles, int64_t* tokens,
+int sfl_next_token(const float* best_val, const int32_t* best_idx, int tiles, int best_stride, int64_t* tokens,
                    int64_t* predicted, long token_stride, const int32_t* prompt_len, int32_t* pos,
                    int32_t* lengths, const void* emb, float* x, int batch, int d_model,
                    int capacity, int dtype, void* stream);

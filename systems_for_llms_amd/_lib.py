@@ -18,6 +18,7 @@ LIB_PATH = Path(__file__).resolve().parent / "lib" / "libsfl.so"
 DTYPE_CODES = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
 DTYPE_BF16X2 = 3  # split-bf16 values in the decode GEMVs' activation layout
 DTYPE_F32X = 4    # fp32 values in the decode GEMVs' activation layout
+DTYPE_F16X2 = 5   # split-fp16 values in the decode GEMVs' activation layout
 
 P = c_void_p
 SIGNATURES: dict[str, list] = {
@@ -35,7 +36,7 @@ SIGNATURES: dict[str, list] = {
     "sfl_rmsnorm_lm_head": [P, P, P, P, c_long, P, c_long, P, P, c_int, c_int, c_int, c_int, c_int, P],
     "sfl_lm_head_tiles": [c_int],
     "sfl_embedding_gather": [P, c_long, P, P, P, c_int, c_int, c_int, P],
-    "sfl_next_token": [P, P, c_int, P, P, c_long, P, P, P, P, P, c_int, c_int, c_int, c_int, P],
+    "sfl_next_token": [P, P, c_int, c_int, P, P, c_long, P, P, P, P, P, c_int, c_int, c_int, c_int, P],
     "sfl_masked_attention": [P, P, P, P, P, c_int, c_int, c_int, c_int, POINTER(c_long), POINTER(c_long),
                              POINTER(c_long), POINTER(c_long), c_float, c_int, c_int, c_int, c_int, P,
                              c_int, P, P, P, c_int, c_int, P],

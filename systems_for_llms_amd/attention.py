@@ -208,14 +208,18 @@ def _record_launch_metadata(q, k, v, spec, implementation, destination):
     destination.update({
         "kernel_name": info.name.decode(),
         "n_regs": info.registers,
-        "n_spills": info.private_bytes // 4,  # spilled 32-bit values per lane
+        # hipFuncGetAttributes reports the whole private segment (spills, stack and
+        # private arrays), not a spill count: n_spills is exact only when it is 0.
+        "n_spills": 0 if info.private_bytes == 0 else None,
         "private_segment_bytes": info.private_bytes,
         "shared_memory_bytes": info.shared_bytes,
         "threads": info.threads,
         "block_q": TILE, "block_k": TILE, "queries_per_workgroup": info.queries_per_workgroup,
         "implementation": implementation,
         "source": "hipFuncGetAttributes of the gfx950 kernel; not rocprof profiling",
-        "asm_sha256": {"libsfl.so": _lib.library_sha256()},
+        # No assembly text is kept: the compiled kernels are identified by the library.
+        "asm_sha256": {},
+        "library_sha256": _lib.library_sha256(),
     })
 
 

@@ -31,9 +31,11 @@ namespace sfl {
 namespace {
 
 // Tag types of the outputs in the decode GEMVs' activation layout (act_format.hpp):
-// split-bf16 values (BF16X2) and fp32 values (F32X); and of the fused output
-// projection, x[b] += attention(b) . W_o^T, accumulated into x with atomics.
+// split-bf16 values (BF16X2), split-fp16 values (F16X2) and fp32 values (F32X);
+// and of the fused output projection, x[b] += attention(b) . W_o^T, accumulated
+// into x with atomics.
 struct split_t {};
+struct split16_t {};
 struct f32x_t {};
 struct resid_t {};
 
@@ -379,6 +381,10 @@ __device__ __forceinline__ void store_out(void* out, long f, int, float v) {
 template <>
 __device__ __forceinline__ void store_out<split_t>(void* out, long f, int K, float v) {
   store_act1<bf16_t>(static_cast<unsigned char*>(out), int(f / K), int(f % K), K, v);
+}
+template <>
+__device__ __forceinline__ void store_out<split16_t>(void* out, long f, int K, float v) {
+  store_act1<f16_t>(static_cast<unsigned char*>(out), int(f / K), int(f % K), K, v);
 }
 template <>
 __device__ __forceinline__ void store_out<f32x_t>(void* out, long f, int K, float v) {
@@ -779,6 +785,7 @@ int attn_out(const DecodeCall& c, int out_dtype) {
   switch (out_dtype) {
     case SFL_DTYPE_F32: return attn_dims<T, TQ, float>(c);
     case SFL_DTYPE_BF16X2: return attn_dims<T, TQ, split_t>(c);
+    case SFL_DTYPE_F16X2: return attn_dims<T, TQ, split16_t>(c);
     case SFL_DTYPE_F32X: return attn_dims<T, TQ, f32x_t>(c);
     default: return attn_dims<T, TQ, T>(c);
   }
@@ -814,9 +821,9 @@ extern "C" int sfl_decode_attention_out_proj(const float* q, const void* k, cons
     return set_error(SFL_ERR_INVALID, "%s: batch, heads and capacity must be positive", what);
   if (!(scale > 0.f) || !__builtin_isfinite(scale))
     return set_error(SFL_ERR_INVALID, "%s: scale must be finite and positive", what);
-  if (dtype != SFL_DTYPE_F32 && dtype != SFL_DTYPE_BF16)
-    return set_error(SFL_ERR_UNSUPPORTED, "%s: model dtype must be F32 or BF16", what);
-  const int kc = dtype == SFL_DTYPE_BF16 ? 32 : 16;
+  if (dtype != SFL_DTYPE_F32 && dtype != SFL_DTYPE_BF16 && dtype != SFL_DTYPE_F16)
+    return set_error(SFL_ERR_UNSUPPORTED, "%s: model dtype must be F32, BF16 or F16", what);
+  const int kc = dtype == SFL_DTYPE_F32 ? 16 : 32;
   if (head_dim % kc || head_dim > 128 || (head_dim & (head_dim - 1)))
     return set_error(SFL_ERR_UNSUPPORTED, "%s: head dim %d must be a power of two in [%d, 128]", what, head_dim, kc);
   if (reinterpret_cast<uintptr_t>(x) % 16 || reinterpret_cast<uintptr_t>(w_out) % 16)
@@ -825,7 +832,9 @@ extern "C" int sfl_decode_attention_out_proj(const float* q, const void* k, cons
                heads, capacity, head_dim, 1, scale, static_cast<hipStream_t>(stream)};
   c.x = x;
   c.d_model = heads * head_dim;
-  return dtype == SFL_DTYPE_BF16 ? proj_dims<bf16_t>(c) : proj_dims<float>(c);
+  if (dtype == SFL_DTYPE_BF16) return proj_dims<bf16_t>(c);
+  if (dtype == SFL_DTYPE_F16) return proj_dims<f16_t>(c);
+  return proj_dims<float>(c);
 }
 
 namespace {
@@ -921,12 +930,14 @@ extern "C" int sfl_decode_attention(const void* q, const void* k, const void* v,
     return set_error(SFL_ERR_UNSUPPORTED, "decode_attention: unsupported dtype %d", kv_dtype);
   if (q_dtype != kv_dtype && q_dtype != SFL_DTYPE_F32)
     return set_error(SFL_ERR_UNSUPPORTED, "decode_attention: q dtype must equal the KV dtype or be F32");
-  const bool act_out = out_dtype == SFL_DTYPE_BF16X2 || out_dtype == SFL_DTYPE_F32X;
+  const bool split_out = out_dtype == SFL_DTYPE_BF16X2 || out_dtype == SFL_DTYPE_F16X2;
+  const bool act_out = split_out || out_dtype == SFL_DTYPE_F32X;
   if (out_dtype != kv_dtype && out_dtype != SFL_DTYPE_F32 && !act_out)
-    return set_error(SFL_ERR_UNSUPPORTED, "decode_attention: out dtype must be the KV dtype, F32, BF16X2 or F32X");
-  if (act_out && (q_heads * head_dim) % (out_dtype == SFL_DTYPE_BF16X2 ? 32 : 16))
-    return set_error(SFL_ERR_UNSUPPORTED, "decode_attention: %s output needs q_heads*head_dim %% %d == 0",
-                     out_dtype == SFL_DTYPE_BF16X2 ? "BF16X2" : "F32X", out_dtype == SFL_DTYPE_BF16X2 ? 32 : 16);
+    return set_error(SFL_ERR_UNSUPPORTED,
+                     "decode_attention: out dtype must be the KV dtype, F32, BF16X2, F16X2 or F32X");
+  if (act_out && (q_heads * head_dim) % (split_out ? 32 : 16))
+    return set_error(SFL_ERR_UNSUPPORTED, "decode_attention: activation-layout output needs q_heads*head_dim %% %d == 0",
+                     split_out ? 32 : 16);
   const DecodeCall c{q, k, v, lengths, partial_max, partial_sum, partial_out, out, batch, q_heads,
                      kv_heads, capacity, head_dim, splits, scale, static_cast<hipStream_t>(stream)};
   int rc;
@@ -942,6 +953,7 @@ extern "C" int sfl_decode_attention(const void* q, const void* k, const void* v,
     case SFL_DTYPE_BF16: return merge_dims<bf16_t>(c);
     case SFL_DTYPE_F16: return merge_dims<f16_t>(c);
     case SFL_DTYPE_F32X: return merge_dims<f32x_t>(c);
+    case SFL_DTYPE_F16X2: return merge_dims<split16_t>(c);
     default: return merge_dims<split_t>(c);
   }
 }

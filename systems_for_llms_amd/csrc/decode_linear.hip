@@ -15,10 +15,11 @@
 // pairs, SwiGLU pairs and vector stores stay in-lane.
 //
 // Precision: weights and the KV cache are in the model dtype; activations,
-// the residual stream and every epilogue stay in fp32. For bf16 weights each
-// fp32 activation is split into hi + lo bf16 halves and multiplied by two
-// MFMAs (the GEMV is bandwidth-bound, so the second MFMA is free), which keeps
-// ~16 mantissa bits of the activation instead of 8.
+// the residual stream and every epilogue stay in fp32. For 16-bit weights each
+// fp32 activation is split into hi + lo halves of the weight type and
+// multiplied by two MFMAs (the GEMV is bandwidth-bound, so the second MFMA is
+// free), which keeps ~16 (bf16) or ~22 (fp16) mantissa bits of the activation
+// instead of 8 or 11.
 //
 // RMSNorm is folded into its consumers (layers.py:133-141): RMSNorm(x) W^T =
 // (1/rms(x)) * ((x * g) W^T). The residual stream x stays a plain fp32 [B, K]
@@ -43,6 +44,7 @@ namespace sfl {
 namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 enum Epi { EPI_QKV = 0, EPI_RESIDUAL = 1, EPI_SWIGLU = 2, EPI_LOGITS = 3 };
@@ -94,6 +96,13 @@ __device__ __forceinline__ f32x4 mfma_chunk<bf16_t>(const uint4& a, const u32x4&
                                                  __builtin_bit_cast(bf16x8, b), acc, 0, 0, 0);
 }
 
+template <>
+__device__ __forceinline__ f32x4 mfma_chunk<f16_t>(const uint4& a, const u32x4& b, f32x4 acc) {
+  const u32x4 av = {a.x, a.y, a.z, a.w};
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, av), __builtin_bit_cast(f16x8, b), acc, 0,
+                                                0, 0);
+}
+
 // fp32: the lane's 4 consecutive k values feed 4 MFMA steps; A and B use the
 // same (lane group, step) -> k mapping, so the contraction is exact.
 template <>
@@ -117,6 +126,12 @@ __device__ __forceinline__ void store4<bf16_t>(bf16_t* dst, const float* v) {
   const uint32_t hi = uint32_t(f32_to_bf16_bits(v[2])) | (uint32_t(f32_to_bf16_bits(v[3])) << 16);
   *reinterpret_cast<uint2*>(dst) = make_uint2(lo, hi);
 }
+template <>
+__device__ __forceinline__ void store4<f16_t>(f16_t* dst, const float* v) {
+  const uint32_t lo = uint32_t(f32_to_f16_bits(v[0])) | (uint32_t(f32_to_f16_bits(v[1])) << 16);
+  const uint32_t hi = uint32_t(f32_to_f16_bits(v[2])) | (uint32_t(f32_to_f16_bits(v[3])) << 16);
+  *reinterpret_cast<uint2*>(dst) = make_uint2(lo, hi);
+}
 
 __device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
   return v > bv || (v == bv && i < bi);
@@ -128,6 +143,7 @@ __device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
 template <typename T> struct ActChunk;
 template <> struct ActChunk<float> { uint4 v; };
 template <> struct ActChunk<bf16_t> { uint4 hi, lo; };
+template <> struct ActChunk<f16_t> { uint4 hi, lo; };
 
 template <typename T>
 __device__ __forceinline__ ActChunk<T> load_act(const unsigned char* p);
@@ -137,6 +153,10 @@ __device__ __forceinline__ ActChunk<float> load_act<float>(const unsigned char* 
 }
 template <>
 __device__ __forceinline__ ActChunk<bf16_t> load_act<bf16_t>(const unsigned char* p) {
+  return {load16(p), load16(p + kActLoOffset)};
+}
+template <>
+__device__ __forceinline__ ActChunk<f16_t> load_act<f16_t>(const unsigned char* p) {
   return {load16(p), load16(p + kActLoOffset)};
 }
 
@@ -150,21 +170,33 @@ __device__ __forceinline__ f32x4 mfma_act<bf16_t>(const uint4& w, const ActChunk
   return mfma_chunk<bf16_t>(w, bl, acc);
 }
 template <>
+__device__ __forceinline__ f32x4 mfma_act<f16_t>(const uint4& w, const ActChunk<f16_t>& x, bool live, f32x4 acc) {
+  const u32x4 bh = {live ? x.hi.x : 0u, live ? x.hi.y : 0u, live ? x.hi.z : 0u, live ? x.hi.w : 0u};
+  const u32x4 bl = {live ? x.lo.x : 0u, live ? x.lo.y : 0u, live ? x.lo.z : 0u, live ? x.lo.w : 0u};
+  acc = mfma_chunk<f16_t>(w, bh, acc);
+  return mfma_chunk<f16_t>(w, bl, acc);
+}
+template <>
 __device__ __forceinline__ f32x4 mfma_act<float>(const uint4& w, const ActChunk<float>& x, bool live, f32x4 acc) {
   const u32x4 b = {live ? x.v.x : 0u, live ? x.v.y : 0u, live ? x.v.z : 0u, live ? x.v.w : 0u};
   return mfma_chunk<float>(w, b, acc);
 }
 
 // A normalized consumer's source: one lane's fp32 values of x for a chunk and
-// the matching gains (bf16 weights: 8 values, fp32: 4).
+// the matching gains (16-bit weights: 8 values, fp32: 4).
 template <typename T> struct NormChunk;
 template <> struct NormChunk<bf16_t> { float4 x0, x1; uint4 g; };
+template <> struct NormChunk<f16_t> { float4 x0, x1; uint4 g; };
 template <> struct NormChunk<float> { float4 x; float4 g; };
 
 template <typename T>
 __device__ __forceinline__ NormChunk<T> load_norm(const float* x, const T* g);
 template <>
 __device__ __forceinline__ NormChunk<bf16_t> load_norm<bf16_t>(const float* x, const bf16_t* g) {
+  return {*reinterpret_cast<const float4*>(x), *reinterpret_cast<const float4*>(x + 4), load16(g)};
+}
+template <>
+__device__ __forceinline__ NormChunk<f16_t> load_norm<f16_t>(const float* x, const f16_t* g) {
   return {*reinterpret_cast<const float4*>(x), *reinterpret_cast<const float4*>(x + 4), load16(g)};
 }
 template <>
@@ -191,6 +223,22 @@ __device__ __forceinline__ ActChunk<bf16_t> norm_operand<bf16_t>(const NormChunk
   ActChunk<bf16_t> r;
   r.hi = make_uint4((hb[0] >> 16) | hb[1], (hb[2] >> 16) | hb[3], (hb[4] >> 16) | hb[5], (hb[6] >> 16) | hb[7]);
   r.lo = make_uint4((lb[0] >> 16) | lb[1], (lb[2] >> 16) | lb[3], (lb[4] >> 16) | lb[5], (lb[6] >> 16) | lb[7]);
+  return r;
+}
+template <>
+__device__ __forceinline__ ActChunk<f16_t> norm_operand<f16_t>(const NormChunk<f16_t>& s, float& ss) {
+  const float x[8] = {s.x0.x, s.x0.y, s.x0.z, s.x0.w, s.x1.x, s.x1.y, s.x1.z, s.x1.w};
+  float g[8];
+  unpack16<f16_t>(s.g, g);
+  uint32_t hb[8], lb[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    ss = fmaf(x[i], x[i], ss);
+    split_act<f16_t>(x[i] * g[i], hb[i], lb[i]);
+  }
+  ActChunk<f16_t> r;
+  r.hi = make_uint4(hb[0] | (hb[1] << 16), hb[2] | (hb[3] << 16), hb[4] | (hb[5] << 16), hb[6] | (hb[7] << 16));
+  r.lo = make_uint4(lb[0] | (lb[1] << 16), lb[2] | (lb[3] << 16), lb[4] | (lb[5] << 16), lb[6] | (lb[7] << 16));
   return r;
 }
 template <>
@@ -492,9 +540,9 @@ int check_common(const char* what, int batch, int n, int k, int dtype, bool vec4
     return set_error(SFL_ERR_INVALID, "%s: batch must be in [1, %d]", what, kMaxRows);
   if (n < 1 || k < 1) return set_error(SFL_ERR_INVALID, "%s: sizes must be positive", what);
   if (vec4 && n % 4) return set_error(SFL_ERR_UNSUPPORTED, "%s: N must be a multiple of 4", what);
-  if (dtype != SFL_DTYPE_F32 && dtype != SFL_DTYPE_BF16)
-    return set_error(SFL_ERR_UNSUPPORTED, "%s: model dtype must be F32 or BF16", what);
-  const int kc = dtype == SFL_DTYPE_BF16 ? chunk_k<bf16_t>() : chunk_k<float>();
+  if (dtype != SFL_DTYPE_F32 && dtype != SFL_DTYPE_BF16 && dtype != SFL_DTYPE_F16)
+    return set_error(SFL_ERR_UNSUPPORTED, "%s: model dtype must be F32, BF16 or F16", what);
+  const int kc = dtype == SFL_DTYPE_F32 ? chunk_k<float>() : chunk_k<bf16_t>();
   if (k % kc) return set_error(SFL_ERR_UNSUPPORTED, "%s: K=%d must be a multiple of %d", what, k, kc);
   return SFL_OK;
 }
@@ -510,6 +558,7 @@ template <int E>
 int dispatch_linear(LinearArgs a, int dtype, hipStream_t s, const char* what) {
   if (a.ksplit < 1) a.ksplit = 1;
   if (dtype == SFL_DTYPE_BF16) return launch_linear<bf16_t, E>(a, s, what);
+  if (dtype == SFL_DTYPE_F16) return launch_linear<f16_t, E>(a, s, what);
   return launch_linear<float, E>(a, s, what);
 }
 
@@ -578,7 +627,7 @@ extern "C" int sfl_rmsnorm_swiglu(const float* x, const void* gain, const void* 
   if (!x || !gain || !w1 || !w3 || !h_out) return set_error(SFL_ERR_INVALID, "%s: null pointer argument", what);
   if (int rc = check_common(what, batch, d_ff, d_model, dtype)) return rc;
   if (int rc = check_normed(what, x, gain)) return rc;
-  const int kc = dtype == SFL_DTYPE_BF16 ? chunk_k<bf16_t>() : chunk_k<float>();
+  const int kc = dtype == SFL_DTYPE_F32 ? chunk_k<float>() : chunk_k<bf16_t>();
   if (d_ff % kc)  // h is written in the activation layout, whole chunks per row
     return set_error(SFL_ERR_UNSUPPORTED, "%s: d_ff=%d must be a multiple of %d", what, d_ff, kc);
   LinearArgs a{};
@@ -614,16 +663,17 @@ extern "C" int sfl_pack_gemv_weights(const void* w, void* packed, int n, int k, 
   const char* what = "pack_gemv_weights";
   if (!w || !packed) return set_error(SFL_ERR_INVALID, "%s: null pointer argument", what);
   if (n < 1 || k < 1) return set_error(SFL_ERR_INVALID, "%s: sizes must be positive", what);
-  if (dtype != SFL_DTYPE_F32 && dtype != SFL_DTYPE_BF16)
-    return set_error(SFL_ERR_UNSUPPORTED, "%s: dtype must be F32 or BF16", what);
-  const int kc = dtype == SFL_DTYPE_BF16 ? chunk_k<bf16_t>() : chunk_k<float>();
+  if (dtype != SFL_DTYPE_F32 && dtype != SFL_DTYPE_BF16 && dtype != SFL_DTYPE_F16)
+    return set_error(SFL_ERR_UNSUPPORTED, "%s: dtype must be F32, BF16 or F16", what);
+  const bool half = dtype != SFL_DTYPE_F32;  // 16-bit values pack alike whatever their format
+  const int kc = half ? chunk_k<bf16_t>() : chunk_k<float>();
   if (k % kc) return set_error(SFL_ERR_UNSUPPORTED, "%s: K=%d must be a multiple of %d", what, k, kc);
   if (reinterpret_cast<uintptr_t>(w) % 16 || reinterpret_cast<uintptr_t>(packed) % 16)
     return set_error(SFL_ERR_INVALID, "%s: pointers must be 16-byte aligned", what);
-  const long units = sfl_packed_gemv_elems(n, k) / (16 / (dtype == SFL_DTYPE_BF16 ? 2 : 4));
+  const long units = sfl_packed_gemv_elems(n, k) / (16 / (half ? 2 : 4));
   const unsigned blocks = unsigned(std::min<long>((units + 255) / 256, 4096));
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (dtype == SFL_DTYPE_BF16)
+  if (half)
     hipLaunchKernelGGL(pack_weights_kernel<bf16_t>, dim3(blocks), dim3(256), 0, s, static_cast<const bf16_t*>(w),
                        static_cast<uint4*>(packed), n, k);
   else

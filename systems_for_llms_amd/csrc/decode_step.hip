@@ -33,7 +33,7 @@ __global__ __launch_bounds__(256) void embed_kernel(const int64_t* __restrict__ 
 // embedding into x (fp32) and advance pos/lengths.
 template <typename T>
 __global__ __launch_bounds__(64) void next_token_kernel(
-    const float* __restrict__ best_val, const int32_t* __restrict__ best_idx, int tiles, int batch,
+    const float* __restrict__ best_val, const int32_t* __restrict__ best_idx, int tiles, int best_stride,
     int64_t* __restrict__ tokens, int64_t* __restrict__ predicted, long stride,
     const int32_t* __restrict__ prompt_len, int32_t* __restrict__ pos, int32_t* __restrict__ lengths,
     const T* __restrict__ emb, float* __restrict__ x, int d, int cap) {
@@ -53,8 +53,8 @@ __global__ __launch_bounds__(64) void next_token_kernel(
 #pragma unroll
     for (int j = 0; j < kScan; ++j) {  // unconditional loads from clamped tiles
       const long t = min(t0 + lane + j * kWave, tiles - 1);
-      v[j] = best_val[t * batch + b];
-      ix[j] = best_idx[t * batch + b];
+      v[j] = best_val[t * best_stride + b];
+      ix[j] = best_idx[t * best_stride + b];
     }
 #pragma unroll
     for (int j = 0; j < kScan; ++j)
@@ -105,16 +105,19 @@ extern "C" int sfl_embedding_gather(const int64_t* tokens, long token_stride, co
   if (dtype == SFL_DTYPE_BF16)
     hipLaunchKernelGGL(embed_kernel<bf16_t>, dim3(batch), dim3(256), 0, s, tokens, token_stride, pos,
                        static_cast<const bf16_t*>(emb), x, d_model);
+  else if (dtype == SFL_DTYPE_F16)
+    hipLaunchKernelGGL(embed_kernel<f16_t>, dim3(batch), dim3(256), 0, s, tokens, token_stride, pos,
+                       static_cast<const f16_t*>(emb), x, d_model);
   else if (dtype == SFL_DTYPE_F32)
     hipLaunchKernelGGL(embed_kernel<float>, dim3(batch), dim3(256), 0, s, tokens, token_stride, pos,
                        static_cast<const float*>(emb), x, d_model);
   else
-    return set_error(SFL_ERR_UNSUPPORTED, "embedding_gather: model dtype must be F32 or BF16");
+    return set_error(SFL_ERR_UNSUPPORTED, "embedding_gather: model dtype must be F32, BF16 or F16");
   return check_launch("embedding_gather");
 }
 
 extern "C" int sfl_next_token(const float* best_val, const int32_t* best_idx, int tiles,
-                              int64_t* tokens, int64_t* predicted, long token_stride,
+                              int best_stride, int64_t* tokens, int64_t* predicted, long token_stride,
                               const int32_t* prompt_len, int32_t* pos, int32_t* lengths,
                               const void* emb, float* x, int batch, int d_model, int capacity,
                               int dtype, void* stream) {
@@ -125,16 +128,21 @@ extern "C" int sfl_next_token(const float* best_val, const int32_t* best_idx, in
   if (d_model % 16) return set_error(SFL_ERR_UNSUPPORTED, "next_token: d_model must be a multiple of 16");
   if (token_stride < capacity)
     return set_error(SFL_ERR_INVALID, "next_token: token_stride must be >= capacity");
+  if (best_stride < batch) return set_error(SFL_ERR_INVALID, "next_token: best_stride must be >= batch");
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (dtype == SFL_DTYPE_BF16)
     hipLaunchKernelGGL(next_token_kernel<bf16_t>, dim3(batch), dim3(64), 0, s, best_val, best_idx, tiles,
-                       batch, tokens, predicted, token_stride, prompt_len, pos, lengths,
+                       best_stride, tokens, predicted, token_stride, prompt_len, pos, lengths,
                        static_cast<const bf16_t*>(emb), x, d_model, capacity);
+  else if (dtype == SFL_DTYPE_F16)
+    hipLaunchKernelGGL(next_token_kernel<f16_t>, dim3(batch), dim3(64), 0, s, best_val, best_idx, tiles,
+                       best_stride, tokens, predicted, token_stride, prompt_len, pos, lengths,
+                       static_cast<const f16_t*>(emb), x, d_model, capacity);
   else if (dtype == SFL_DTYPE_F32)
     hipLaunchKernelGGL(next_token_kernel<float>, dim3(batch), dim3(64), 0, s, best_val, best_idx, tiles,
-                       batch, tokens, predicted, token_stride, prompt_len, pos, lengths,
+                       best_stride, tokens, predicted, token_stride, prompt_len, pos, lengths,
                        static_cast<const float*>(emb), x, d_model, capacity);
   else
-    return set_error(SFL_ERR_UNSUPPORTED, "next_token: model dtype must be F32 or BF16");
+    return set_error(SFL_ERR_UNSUPPORTED, "next_token: model dtype must be F32, BF16 or F16");
   return check_launch("next_token");
 }

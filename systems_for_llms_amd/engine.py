@@ -47,6 +47,18 @@ def residual_ksplit(n: int, target_groups: int = 256) -> int:
     return max(1, min(16, target_groups // max(1, n // 16)))
 
 
+def default_deterministic(dtype) -> bool:
+    """Whether a session runs the one-writer decode path when the caller does not say.
+
+    float32 models do: their greedy ids are checked for identity with the
+    reference, so they must not depend on the order in which the fused path's
+    fp32 atomics add the heads' output projections (or w2's K parts) into x.
+    16-bit models take the faster fused path; its run-to-run differences are
+    fp32 reassociation, far below their storage rounding.
+    """
+    return dtype == torch.float32
+
+
 def parameter_version(model) -> tuple:
     """Changes whenever a parameter is replaced or modified in place (``Tensor._version``)."""
     return tuple((p.data_ptr(), p._version, p.dtype, p.device) for p in model.parameters())
@@ -95,12 +107,12 @@ def decode_weights(model) -> DecodeWeights:
 
 class DecodeSession:
     def __init__(self, model, batch: int, capacity: int | None = None, *, splits: int | None = None,
-                 record_logits: bool = False, deterministic: bool = False):
+                 record_logits: bool = False, deterministic: bool | None = None):
         param = model.lm_head.weight
         if param.device.type != "cuda":
             raise RuntimeError("systems_for_llms_amd runs on the GPU: move the model to a HIP device first")
-        if param.dtype not in (torch.float32, torch.bfloat16):
-            raise TypeError("model dtype must be float32 or bfloat16")
+        if param.dtype not in (torch.float32, torch.bfloat16, torch.float16):
+            raise TypeError("model dtype must be float32, bfloat16 or float16")
         _lib.lib()
         cap = capacity or model.context_length
         if not 0 < cap <= model.context_length:
@@ -140,7 +152,9 @@ class DecodeSession:
         blocks = -(-batch // ROW_BLOCK)
         self.attn = torch.zeros((blocks, ROW_BLOCK * d), device=dev, dtype=torch.float32)
         self.hidden = torch.zeros((blocks, ROW_BLOCK * f), device=dev, dtype=torch.float32)
-        self.act_code = _lib.DTYPE_BF16X2 if dt == torch.bfloat16 else _lib.DTYPE_F32X
+        self.act_code = {torch.bfloat16: _lib.DTYPE_BF16X2, torch.float16: _lib.DTYPE_F16X2}.get(dt, _lib.DTYPE_F32X)
+        if deterministic is None:
+            deterministic = default_deterministic(dt)
         self.deterministic = deterministic
         # GEMM prefill with each layer's RMSNorm folded into the GEMMs beside it
         # (where the 32x32 MFMA kernels take every shape); see ``prefill``.
@@ -165,7 +179,7 @@ class DecodeSession:
         # deterministic=True keeps output_proj and w2 as plain GEMVs whose every output
         # has one writer, so repeated runs give bit-identical logits.
         self.fused_out_proj = not deterministic and self.splits == 1 \
-            and self.dk % (32 if dt == torch.bfloat16 else 16) == 0 and self.dk <= 128 and self.dk & (self.dk - 1) == 0
+            and self.dk % (16 if dt == torch.float32 else 32) == 0 and self.dk <= 128 and self.dk & (self.dk - 1) == 0
         self.ksplit = 1 if deterministic else residual_ksplit(d)
         self.position = 0  # host mirror of every row's position (all rows move together)
         self.graph = None
@@ -218,7 +232,7 @@ class DecodeSession:
                     x, m.ln_final.weight.data_ptr(), self.p_head.data_ptr(), logits, cap * v, pos, v,
                     bufs["best_val"].data_ptr(), bufs["best_idx"].data_ptr(), nb, nb, d, v, code)),
                 (lib.sfl_next_token, (
-                    bufs["best_val"].data_ptr(), bufs["best_idx"].data_ptr(), self.tiles,
+                    bufs["best_val"].data_ptr(), bufs["best_idx"].data_ptr(), self.tiles, nb,
                     self.tokens[r0:].data_ptr(), self.predicted[r0:].data_ptr(), cap,
                     self.prompt_len[r0:].data_ptr(), pos, lengths, m.token_embeddings.weight.data_ptr(), x,
                     nb, d, cap, code))]

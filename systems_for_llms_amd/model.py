@@ -147,8 +147,10 @@ class TransformerLM(nn.Module):
         self.attention_backend = attention_backend
         self.activation_checkpointing = activation_checkpointing
         # Not in the reference: True keeps every decode output at one writer (no fp32
-        # atomics), so repeated forward/generate calls give bit-identical results.
-        self.deterministic = False
+        # atomics), so repeated forward/generate calls give bit-identical results;
+        # None (the default) chooses it for float32 models, whose greedy ids must not
+        # depend on the order of fp32 additions, and the faster fused path otherwise.
+        self.deterministic = None
         self.token_embeddings = Embedding(vocab_size, d_model, device, dtype)
         self.layers = nn.ModuleList([
             TransformerBlock(d_model, num_heads, d_ff, rope_theta, context_length, device, dtype,
@@ -209,7 +211,7 @@ class TransformerLM(nn.Module):
             raise ValueError("sequence length must be between 1 and context_length")
 
     def decode_session(self, batch: int, capacity: int, *, record_logits: bool = False,
-                       deterministic: bool = False) -> "_engine.DecodeSession":
+                       deterministic: bool | None = None) -> "_engine.DecodeSession":
         """A ``DecodeSession`` of at least ``capacity`` positions for ``batch`` sequences.
 
         The last session is kept and reused by later calls with the same batch,
@@ -219,6 +221,8 @@ class TransformerLM(nn.Module):
         repeated ``forward``/``generate`` calls neither repack weights nor
         reallocate the KV cache.
         """
+        if deterministic is None:
+            deterministic = _engine.default_deterministic(self.lm_head.weight.dtype)
         session = getattr(self, "_sfl_session", None)
         reuse = (session is not None and session.batch == batch and capacity <= session.cap
                  and (session.logits is not None) == record_logits and session.deterministic == deterministic
@@ -228,6 +232,18 @@ class TransformerLM(nn.Module):
             session = self._sfl_session = _engine.DecodeSession(
                 self, batch=batch, capacity=capacity, record_logits=record_logits, deterministic=deterministic)
         return session
+
+    def release_sessions(self) -> None:
+        """Free the device memory ``forward``/``generate`` keep between calls.
+
+        The last ``DecodeSession`` (its KV cache ``[L, B, H, cap, dk]``, and on
+        the step path a ``[B, cap, vocab]`` fp32 logits buffer) and the packed
+        decode weights (about one more copy of the projection weights) stay
+        allocated so that repeated calls reuse them; this drops both. The next
+        call makes them again.
+        """
+        self._sfl_session = None
+        self._sfl_decode_weights = None
 
     @torch.no_grad()
     def forward(self, input_ids: torch.Tensor) -> torch.Tensor:
@@ -244,8 +260,10 @@ class TransformerLM(nn.Module):
         session = self.decode_session(ids.shape[0], t, record_logits=True, deterministic=self.deterministic)
         session.start(ids)
         session.run(t)
-        # The reference returns logits in the parameter dtype (transformer.py:138).
-        return session.logits[:, :t].to(self.lm_head.weight.dtype).reshape(*lead, t, self.vocab_size)
+        # The reference returns logits in the parameter dtype (transformer.py:138), a new
+        # tensor every call: copy out of the session's buffer, which the next call reuses.
+        logits = session.logits[:, :t].to(self.lm_head.weight.dtype, copy=True)
+        return logits.reshape(*lead, t, self.vocab_size)
 
     @torch.no_grad()
     def generate(self, input_ids: torch.Tensor, max_new_tokens: int, *, use_graph: bool = True,

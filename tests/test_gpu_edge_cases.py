@@ -69,7 +69,7 @@ def test_lm_head_argmax_ties_lowest_index_c_abi(dtype):
         st = _lib.stream_handle()
         _lib.call("sfl_rmsnorm_lm_head", x.data_ptr(), gain.data_ptr(), packed.data_ptr(), logits.data_ptr(),
                   VOCAB, None, 0, best_val.data_ptr(), best_idx.data_ptr(), batch, batch, D, VOCAB, code, st)
-        _lib.call("sfl_next_token", best_val.data_ptr(), best_idx.data_ptr(), tiles, tokens.data_ptr(),
+        _lib.call("sfl_next_token", best_val.data_ptr(), best_idx.data_ptr(), tiles, batch, tokens.data_ptr(),
                   predicted.data_ptr(), cap, prompt_len.data_ptr(), pos.data_ptr(), lengths.data_ptr(),
                   emb.data_ptr(), x_next.data_ptr(), batch, D, cap, code, st)
 

@@ -154,7 +154,7 @@ def test_launch_metadata_records_the_launched_kernels_resources(d):
         print(meta)
         assert meta["kernel_name"] == expected + " bf16"
         assert meta["queries_per_workgroup"] == (64 if d == 32 or "2 waves" in expected else 128)
-        assert 0 < meta["n_regs"] <= 512 and meta["n_spills"] * 4 == meta["private_segment_bytes"]
+        assert 0 < meta["n_regs"] <= 512 and meta["n_spills"] == (0 if meta["private_segment_bytes"] == 0 else None)
         assert meta["shared_memory_bytes"] > 0 and meta["threads"] in (128, 256)
-        assert len(meta["asm_sha256"]["libsfl.so"]) == 64
+        assert meta["asm_sha256"] == {} and len(meta["library_sha256"]) == 64
         assert "not rocprof" in meta["source"]

@@ -109,10 +109,11 @@ def test_config1_bf16_teacher_forced_logits_and_agreement(golden):
         assert err <= BF16_ATOL
     seq_cpu = seq.cpu()
     ref = om.forward(sd, cfg, seq_cpu)[0, p0:-1]
+    rw = om.forward(om.round_weights(sd), cfg, seq_cpu)[0, p0:-1]
     floor = om.forward(om.round_weights(sd), cfg, seq_cpu, kv_dtype=torch.bfloat16)[0, p0:-1]
     got = session.logits[0, p0:-1].float().cpu()
     # Teacher forced on the reference's own greedy sequence: targets are its tokens.
-    bf16_gate("config1", got, ref, floor, targets=seq_cpu[0, p0 + 1:])
+    bf16_gate("config1", got, ref, floor, targets=seq_cpu[0, p0 + 1:], ref_bf16_weights=rw)
 
 
 def test_config1_bf16_free_running_first_divergence(golden):
@@ -150,6 +151,7 @@ def test_config2_bf16_teacher_forced_against_cpu_oracle():
     seq = seeded_prompt(cfg.vocab_size, 8, prompt_len + extra, 2027)
     torch.set_num_threads(16)
     ref = om.KVCacheOracle(sd, cfg, 8, prompt_len + extra).step(seq)[:, prompt_len - 1:, :]
+    rw = om.KVCacheOracle(om.round_weights(sd), cfg, 8, prompt_len + extra).step(seq)[:, prompt_len - 1:, :]
     floor = om.forward(om.round_weights(sd), cfg, seq, kv_dtype=torch.bfloat16)[:, prompt_len - 1:, :]
     model = gpu_model(cfg, sd, torch.bfloat16)
     session = DecodeSession(model, 8, prompt_len + extra, record_logits=True)
@@ -157,7 +159,7 @@ def test_config2_bf16_teacher_forced_against_cpu_oracle():
     session.run(prompt_len + extra, use_graph=True)
     torch.cuda.synchronize()
     got = session.logits[:, prompt_len - 1:].float().cpu()
-    bf16_gate("config2", got, ref, floor)
+    bf16_gate("config2", got, ref, floor, ref_bf16_weights=rw)
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
@@ -171,7 +173,7 @@ def test_split_cache_path_matches_fused_path(dtype):
     ids = seeded_prompt(cfg.vocab_size, 3, 96, 32).cuda()
     runs = {}
     for splits in (1, 3):
-        session = DecodeSession(model, batch=3, capacity=96, splits=splits, record_logits=True)
+        session = DecodeSession(model, batch=3, capacity=96, splits=splits, record_logits=True, deterministic=False)
         assert session.fused_out_proj == (splits == 1)
         session.start(ids)
         session.run(95, use_graph=True)
@@ -237,3 +239,93 @@ def test_deterministic_decode_is_bit_reproducible(dtype):
     err = (runs[0] - runs[2]).abs().max().item()
     print(f"{dtype}: deterministic vs fused path max-abs {err:.2e}")
     assert err < (2e-5 if dtype == torch.float32 else 2e-3)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_forward_returns_a_new_tensor_every_call(dtype):
+    """forward() reuses its session, but each call returns logits of its own: a later call with
+    the same batch and a shorter sequence leaves the earlier result unchanged (the reference
+    returns a new tensor every call)."""
+    cfg = ModelConfig(vocab_size=500, context_length=64, d_model=256, num_layers=2, num_heads=4,
+                      d_ff=512, rope_theta=10000.0)
+    model = gpu_model(cfg, seeded_state_dict(cfg, 61), dtype)
+    x1 = seeded_prompt(cfg.vocab_size, 2, 40, 62).cuda()
+    x2 = seeded_prompt(cfg.vocab_size, 2, 30, 63).cuda()
+    a = model(x1)
+    kept = a.clone()
+    b = model(x2)
+    assert torch.equal(a, kept), "a later forward() changed an earlier result"
+    assert a.data_ptr() != b.data_ptr()
+    assert torch.equal(model(x1), kept) or dtype == torch.bfloat16  # the fp32 path is deterministic
+
+
+def test_decode_determinism_defaults_and_release():
+    """Unless told otherwise, float32 sessions run the one-writer (deterministic) path and bf16
+    sessions the fused one; release_sessions() drops the kept session and packed weights."""
+    cfg = ModelConfig(vocab_size=500, context_length=64, d_model=256, num_layers=2, num_heads=4,
+                      d_ff=512, rope_theta=10000.0)
+    for dtype, expected in ((torch.float32, True), (torch.bfloat16, False)):
+        model = gpu_model(cfg, seeded_state_dict(cfg, 71), dtype)
+        assert DecodeSession(model, 2, 64).deterministic == expected
+        assert DecodeSession(model, 2, 64, deterministic=not expected).deterministic == (not expected)
+        prompt = seeded_prompt(cfg.vocab_size, 2, 20, 72).cuda()
+        first = model.generate(prompt, 10)
+        assert model._sfl_session.deterministic == expected
+        if dtype == torch.float32:  # repeated runs give the same logits bit for bit
+            assert torch.equal(model(prompt), model(prompt))
+        model.release_sessions()
+        assert model._sfl_session is None and model._sfl_decode_weights is None
+        assert torch.equal(model.generate(prompt, 10), first) or dtype == torch.bfloat16
+
+
+def test_fp16_model_forward_and_generate_match_the_oracle():
+    """A float16 model (the reference's dtype=torch.float16, transformer.py:51-63): fp16 weights and
+    KV cache, the GEMVs' fp16 hi + lo activations. Logits against the oracle with the same storage
+    formats (fp16 weights and cache, fp32 arithmetic), the fp32 reference, and greedy ids."""
+    cfg = ModelConfig(vocab_size=500, context_length=96, d_model=256, num_layers=2, num_heads=4,
+                      d_ff=512, rope_theta=10000.0)
+    sd = seeded_state_dict(cfg, 81)
+    model = gpu_model(cfg, sd, torch.float16)
+    ids = seeded_prompt(cfg.vocab_size, 3, 96, 82)
+    logits = model(ids.cuda())
+    assert logits.dtype == torch.float16 and logits.shape == (3, 96, cfg.vocab_size)
+    logits = logits.float().cpu()
+    ref = om.forward(sd, cfg, ids)
+    floor = om.forward(om.round_weights(sd, torch.float16), cfg, ids, kv_dtype=torch.float16)
+    err, ferr = (logits - floor).abs().max().item(), (logits - ref).abs().max().item()
+    agree = (logits.argmax(-1) == ref.argmax(-1)).float().mean().item()
+    print(f"fp16 forward: vs fp16-storage floor max-abs {err:.2e}; vs fp32 {ferr:.2e}, agreement {agree:.4f}")
+    assert err <= 2e-3  # the floor up to fp32 reassociation and the logits' own fp16 rounding
+    assert ferr <= 2e-2
+    prompt = ids[:, :40].cuda()
+    out = model.generate(prompt, 50).cpu()
+    teacher = om.forward(sd, cfg, out)
+    agree = (teacher[:, 39:-1].argmax(-1) == out[:, 40:]).float().mean().item()
+    print(f"fp16 generate: teacher-forced agreement with the fp32 oracle {agree:.4f}")
+    assert agree >= 0.95
+
+
+def test_config1_fp16_teacher_forced_against_fp32(golden):
+    """Config 1 dims in float16: teacher-forced on the reference's greedy sequence, logits within the
+    north-star 2e-2 of fp32 on the fp16 weights (fp16 keeps 3 more mantissa bits than bf16)."""
+    meta, arrays = golden
+    c1 = meta["c1"]
+    cfg = load_model_config("pilot-22m-s256")
+    sd = seeded_state_dict(cfg, c1["seed"])
+    model = gpu_model(cfg, sd, torch.float16)
+    seq = torch.from_numpy(arrays["c1_ids"])
+    session = DecodeSession(model, 1, seq.shape[1], record_logits=True)
+    session.start(seq.cuda())
+    session.run(seq.shape[1] - 1, use_graph=True)
+    torch.cuda.synchronize()
+    p0 = c1["prompt_length"] - 1
+    got = session.logits[0, p0:-1].float().cpu()
+    ref = om.forward(sd, cfg, seq)[0, p0:-1]
+    rw = om.forward(om.round_weights(sd, torch.float16), cfg, seq)[0, p0:-1]
+    floor = om.forward(om.round_weights(sd, torch.float16), cfg, seq, kv_dtype=torch.float16)[0, p0:-1]
+    targets = seq[0, p0 + 1:]
+    err, rw_err, k_err = ((got - x).abs().max().item() for x in (ref, rw, floor))
+    agree = (got.argmax(-1) == targets).float().mean().item()
+    print(f"config1 fp16: vs fp32 max-abs {err:.4f} agreement {agree:.4f}; vs fp32 on the fp16 weights {rw_err:.4f}; "
+          f"vs the fp16-storage floor {k_err:.5f}")
+    assert rw_err <= BF16_ATOL and k_err <= 2e-3 and agree >= 0.97
