@@ -381,15 +381,14 @@ def profile_target_gemm(reps: int = 10) -> int:
     calls = {
         "q/k/v": lambda: _lib.call("sfl_gemm_qkv_rope_scaled", act.data_ptr(), w["qkv"].data_ptr(), rsc.data_ptr(),
                                    m, t, d, h, cos.data_ptr(), sin.data_ptr(), q.data_ptr(), kc.data_ptr(),
-                                   vc.data_ptr(), CONTEXT, st),
+                                   vc.data_ptr(), CONTEXT, 1, st),
         "output_proj": lambda: _lib.call("sfl_gemm_residual_norm", act.data_ptr(), w["o"].data_ptr(), x.data_ptr(),
-                                         m, d, d, gain.data_ptr(), xg.data_ptr(), ss.data_ptr(), st),
+                                         m, d, d, gain.data_ptr(), xg.data_ptr(), ss.data_ptr(), 1, st),
         "w1/w3": lambda: _lib.call("sfl_gemm_swiglu_scaled", act.data_ptr(), w["w13"].data_ptr(), rsc.data_ptr(),
-                                   hid.data_ptr(), m, f, d, st),
+                                   hid.data_ptr(), m, f, d, 1, st),
         "w2": lambda: _lib.call("sfl_gemm_residual_norm", hid.data_ptr(), w["w2"].data_ptr(), x.data_ptr(), m, d, f,
-                                gain.data_ptr(), xg.data_ptr(), ss.data_ptr(), st),
-        "lm_head": lambda: _lib.call("sfl_gemm_bf16", act.data_ptr(), w["head"].data_ptr(), logits.data_ptr(), m, v,
-                                     d, 0, 0, st),
+                                gain.data_ptr(), xg.data_ptr(), ss.data_ptr(), 1, st),
+        "lm_head": lambda: _lib.call("sfl_gemm", act.data_ptr(), w["head"].data_ptr(), logits.data_ptr(), m, v, d, 1, 0, 0, st),
     }
     flops = {"q/k/v": 2 * m * 3 * d * d, "output_proj": 2 * m * d * d, "w1/w3": 2 * m * 2 * f * d,
              "w2": 2 * m * d * f, "lm_head": 2 * m * v * d}

@@ -291,81 +291,98 @@ int sfl_masked_attention_kernel_info(int head_dim, int dtype, int n, long k_row_
                                      long v_row_stride, int causal, int window_left,
                                      int window_right, int global_prefix, sfl_kernel_info* info);
 
-/* ---- prefill (bf16 weights) -------------------------------------------------
- * C^T = W A^T on bf16 MFMAs; A [M, K] bf16 row-major (one row per token),
- * W [N, K] bf16; K % 8 == 0. K % 64 == 0 runs 32x32x16 MFMA tiles of 256 x 384
- * (grids of >= 320 such tiles) or 128 x 128 features x tokens, other K the
- * 16x16x32 kernel on 128 x 128 tiles.
+/* ---- prefill (weights in bf16, fp16 or fp32) ---------------------------------
+ * C^T = W A^T on MFMAs; A [M, K] row-major (one row per token) and W [N, K]
+ * of one type `dtype`: SFL_DTYPE_BF16 or SFL_DTYPE_F16 (16-bit MFMAs; every
+ * 16-bit output of these calls has that type too; K % 8 == 0; K % 64 == 0 runs
+ * 32x32x16 MFMA tiles of 256 x 384 (grids of >= 320 such tiles) or 128 x 128
+ * features x tokens, other K the 16x16x32 kernel on 128 x 128 tiles), or, for
+ * sfl_gemm, sfl_gemm_qkv_rope and sfl_gemm_swiglu, SFL_DTYPE_F32 (fp32
+ * v_mfma_f32_32x32x2_f32 on 64 x 64 tiles: fp32 products and sums, every
+ * output fp32, K % 4 == 0, 16-byte aligned operands and outputs).
  * Replace, for a whole prompt, the Linear layers of one TransformerBlock and
  * the lm_head (src/llmlab/model/layers.py:34-35, attention.py:160-162,199-203,
  * layers.py:114-115, transformer.py:137-138).
  */
 
-/* C = A W^T as fp32 (accumulate = 1 adds into C: the residual update) or bf16. */
-int sfl_gemm_bf16(const void* a, const void* w, void* c, int m, int n, int k, int c_dtype,
-                  int accumulate, void* stream);
+/* C = A W^T as fp32 (c_dtype F32; accumulate = 1 adds into C: the residual
+ * update) or in the input type (c_dtype == dtype). */
+int sfl_gemm(const void* a, const void* w, void* c, int m, int n, int k, int dtype, int c_dtype,
+             int accumulate, void* stream);
 
 /* q/k/v = A W_qkv^T with RoPE at position (row % seq) from the fp32 tables
  * cos_t / sin_t in feature-major layout [head_dim / 2, capacity] (the
  * reference's [positions, head_dim / 2] table of attention.py:31-42
  * transposed: lanes holding consecutive tokens read consecutive floats);
- * q to [m/seq, heads, seq, head_dim] bf16, k/v written at positions 0..seq-1
- * of the [m/seq, heads, capacity, head_dim] bf16 cache. */
+ * q to [m/seq, heads, seq, head_dim], k/v written at positions 0..seq-1
+ * of the [m/seq, heads, capacity, head_dim] cache. */
 int sfl_gemm_qkv_rope(const void* a, const void* w_qkv, int m, int seq, int d_model, int heads,
                       const float* cos_t, const float* sin_t, void* q_out, void* k_cache,
-                      void* v_cache, int capacity, void* stream);
+                      void* v_cache, int capacity, int dtype, void* stream);
 
-/* h = silu(A W1^T) * (A W3^T) as bf16 [m, d_ff]; w13_interleaved [2*d_ff, k]
+/* h = silu(A W1^T) * (A W3^T) as [m, d_ff]; w13_interleaved [2*d_ff, k]
  * holds 8 rows of W1 then the same 8 rows of W3, repeatedly. */
 int sfl_gemm_swiglu(const void* a, const void* w13_interleaved, void* h_out, int m, int d_ff, int k,
-                    void* stream);
+                    int dtype, void* stream);
+
+/* Causal attention of a whole prompt in fp32 (attention.py:61-98 with the
+ * causal mask of :187-197), for the prefill of float32 models: q, k, v, o
+ * [B, H, N, D] fp32 addressed by per-tensor strides {batch, head, sequence}
+ * (elements; D contiguous; k, v and o rows 16-byte aligned), o = softmax(q k^T
+ * * scale) v over keys 0..i for query i, every product and sum in fp32.
+ * D in {16, 32, 64, 128}. */
+int sfl_causal_attention_f32(const float* q, const float* k, const float* v, float* o, int batch, int heads,
+                             int n, int head_dim, const long* q_strides, const long* k_strides,
+                             const long* v_strides, const long* o_strides, float scale, void* stream);
 
 /* x[r] = emb[ids[r]] in fp32 for r < m (Embedding.forward, layers.py:68-70);
- * ids in [0, vocab), unchecked as for sfl_embedding_gather. */
+ * emb F32, BF16 or F16; ids in [0, vocab), unchecked as for sfl_embedding_gather. */
 int sfl_embed_rows(const int64_t* ids, const void* emb, float* x, int m, int d_model, int dtype,
                    void* stream);
 
-/* out[r] = bf16(RMSNorm(x[r]) * w) for r < m (layers.py:133-141); dtype is w's. */
-int sfl_rmsnorm_rows(const float* x, const void* w, void* out_bf16, int m, int d_model, int dtype,
-                     void* stream);
+/* out[r] = RMSNorm(x[r]) * w for r < m (layers.py:133-141), rounded once to
+ * out_dtype; (w dtype, out_dtype) is (BF16, BF16), (F32, BF16), (F16, F16)
+ * or (F32, F32). */
+int sfl_rmsnorm_rows(const float* x, const void* w, void* out, int m, int d_model, int dtype,
+                     int out_dtype, void* stream);
 
 /* ---- prefill with the RMSNorm folded into the neighbouring GEMMs -------------
  * RMSNorm(x) W^T = (1 / rms(x)) ((x * w) W^T) per token: the norm's input side
- * is xg = bf16(x * w) plus a per-token scale r = 1 / rms(x) that the consuming
+ * is xg = T(x * w) plus a per-token scale r = 1 / rms(x) that the consuming
  * GEMM applies to its fp32 products, and the residual GEMM producing x writes
  * xg for the next norm and per-token sums of squares over each 128-feature
  * part, so no separate pass re-reads x. Same layers as above (layers.py:133-141
- * feeding attention.py:160-162 and layers.py:114-115); bf16, d_model and d_ff
- * multiples of 64 (the 32x32 MFMA kernels).
+ * feeding attention.py:160-162 and layers.py:114-115); T = bf16 or fp16 as
+ * `dtype` says, d_model and d_ff multiples of 64 (the 32x32 MFMA kernels).
  */
 
-/* act_xg[r] = bf16(x[r] * w), rscale[r] = 1 / sqrt(mean(x[r]^2) + 1e-5); w bf16
- * (dtype must be SFL_DTYPE_BF16), d_model <= 2048. */
+/* act_xg[r] = T(x[r] * w), rscale[r] = 1 / sqrt(mean(x[r]^2) + 1e-5); w of
+ * type `dtype` (BF16 or F16), d_model <= 2048. */
 int sfl_rmsnorm_rows_scaled(const float* x, const void* w, void* act_xg, float* rscale, int m, int d_model,
                             int dtype, void* stream);
 
-/* x += A W^T (fp32, as sfl_gemm_bf16 with accumulate) and, from the updated
- * x: act_xg = bf16(x * gain_next) and ss_parts[p][r] = sum of x[r][f]^2 over
+/* x += A W^T (fp32, as sfl_gemm with accumulate) and, from the updated
+ * x: act_xg = T(x * gain_next) and ss_parts[p][r] = sum of x[r][f]^2 over
  * the features f of part p = f / 128 (ceil(n / 128) parts). n % 4 == 0.
  * act_xg must not overlap a (other workgroups may still be reading A while
  * one writes its outputs); each part's sum has a fixed order, so results are
  * the same from call to call. */
 int sfl_gemm_residual_norm(const void* a, const void* w, float* x, int m, int n, int k, const void* gain_next,
-                           void* act_xg, float* ss_parts, void* stream);
+                           void* act_xg, float* ss_parts, int dtype, void* stream);
 
 /* rscale[r] = 1 / sqrt(sum_p ss_parts[p][r] / d_model + 1e-5), parts summed in order. */
 int sfl_norm_scale(const float* ss_parts, int parts, int m, int d_model, float* rscale, void* stream);
 
 /* sfl_gemm_qkv_rope on act_xg (same feature-major tables), each token's
- * products scaled by rscale[r] before RoPE and the bf16 stores. */
+ * products scaled by rscale[r] before RoPE and the 16-bit stores. */
 int sfl_gemm_qkv_rope_scaled(const void* a_xg, const void* w_qkv, const float* rscale, int m, int seq,
                              int d_model, int heads, const float* cos_t, const float* sin_t, void* q_out,
-                             void* k_cache, void* v_cache, int capacity, void* stream);
+                             void* k_cache, void* v_cache, int capacity, int dtype, void* stream);
 
 /* sfl_gemm_swiglu on act_xg, both products of a token scaled by rscale[r]
  * before silu(.) * (.). */
 int sfl_gemm_swiglu_scaled(const void* a_xg, const void* w13_interleaved, const float* rscale, void* h_out,
-                           int m, int d_ff, int k, void* stream);
+                           int m, int d_ff, int k, int dtype, void* stream);
 
 #ifdef __cplusplus
 }

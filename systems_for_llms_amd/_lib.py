@@ -42,16 +42,18 @@ SIGNATURES: dict[str, list] = {
                              c_int, P, P, P, c_int, c_int, P],
     "sfl_masked_attention_block": [],
     "sfl_masked_attention_kernel_info": [c_int, c_int, c_int, c_long, c_long, c_int, c_int, c_int, c_int, P],
-    "sfl_gemm_bf16": [P, P, P, c_int, c_int, c_int, c_int, c_int, P],
-    "sfl_gemm_qkv_rope": [P, P, c_int, c_int, c_int, c_int, P, P, P, P, P, c_int, P],
-    "sfl_gemm_swiglu": [P, P, P, c_int, c_int, c_int, P],
+    "sfl_gemm": [P, P, P, c_int, c_int, c_int, c_int, c_int, c_int, P],
+    "sfl_gemm_qkv_rope": [P, P, c_int, c_int, c_int, c_int, P, P, P, P, P, c_int, c_int, P],
+    "sfl_gemm_swiglu": [P, P, P, c_int, c_int, c_int, c_int, P],
     "sfl_embed_rows": [P, P, P, c_int, c_int, c_int, P],
-    "sfl_rmsnorm_rows": [P, P, P, c_int, c_int, c_int, P],
+    "sfl_rmsnorm_rows": [P, P, P, c_int, c_int, c_int, c_int, P],
     "sfl_rmsnorm_rows_scaled": [P, P, P, P, c_int, c_int, c_int, P],
-    "sfl_gemm_residual_norm": [P, P, P, c_int, c_int, c_int, P, P, P, P],
+    "sfl_gemm_residual_norm": [P, P, P, c_int, c_int, c_int, P, P, P, c_int, P],
     "sfl_norm_scale": [P, c_int, c_int, c_int, P, P],
-    "sfl_gemm_qkv_rope_scaled": [P, P, P, c_int, c_int, c_int, c_int, P, P, P, P, P, c_int, P],
-    "sfl_gemm_swiglu_scaled": [P, P, P, P, c_int, c_int, c_int, P],
+    "sfl_gemm_qkv_rope_scaled": [P, P, P, c_int, c_int, c_int, c_int, P, P, P, P, P, c_int, c_int, P],
+    "sfl_gemm_swiglu_scaled": [P, P, P, P, c_int, c_int, c_int, c_int, P],
+    "sfl_causal_attention_f32": [P, P, P, P, c_int, c_int, c_int, c_int, POINTER(c_long), POINTER(c_long),
+                                 POINTER(c_long), POINTER(c_long), c_float, P],
 }
 
 _LIB = None

@@ -224,12 +224,22 @@ def _record_launch_metadata(q, k, v, spec, implementation, destination):
 
 
 def causal_prefill(q, k, v, out):
-    """Causal attention of a prompt for the model's prefill (interval schedule, no LSE).
+    """Causal attention of a prompt for the model's prefill (no LSE).
 
-    ``q``, ``k``, ``v`` and ``out`` are ``[B, H, T, D]`` bf16 views with a
-    contiguous last dimension (``k``/``v`` straight out of the KV cache);
-    launches on the current stream without any host synchronisation.
+    ``q``, ``k``, ``v`` and ``out`` are ``[B, H, T, D]`` views with a
+    contiguous last dimension (``k``/``v`` straight out of the KV cache) in the
+    model dtype: 16-bit ones run the masked MFMA kernel on the interval
+    schedule, float32 ones the fp32 kernel; launches on the current stream
+    without any host synchronisation.
     """
+    if q.dtype == torch.float32:
+        import ctypes
+
+        strides = [(ctypes.c_long * 3)(*t.stride()[:3]) for t in (q, k, v, out)]
+        _lib.call("sfl_causal_attention_f32", q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), q.shape[0],
+                  q.shape[1], q.shape[2], q.shape[3], *strides, float(q.shape[-1] ** -0.5),
+                  _lib.stream_handle(q.device))
+        return out
     torch.ops.sfl.masked_attention(q, k, v, out, None, float(q.shape[-1] ** -0.5), True, -1, -1, 0, None,
                                    None, None, None, True)
     return out

@@ -1,9 +1,11 @@
-// Prefill projections as bf16 MFMA GEMMs with fused epilogues, plus the
+// Prefill projections as 16-bit MFMA GEMMs with fused epilogues, plus the
 // row-wise prefill helpers (embedding gather, RMSNorm).
 //
-// Every GEMM computes C^T[n][m] = sum_k W[n][k] * A[m][k] for A [M, K] bf16
-// activations (one row per token) and W [N, K] bf16 weights, both K-contiguous
-// as the reference's Linear stores them (src/llmlab/model/layers.py:34-35).
+// Every GEMM computes C^T[n][m] = sum_k W[n][k] * A[m][k] for A [M, K]
+// activations (one row per token) and W [N, K] weights, both K-contiguous as
+// the reference's Linear stores them (src/llmlab/model/layers.py:34-35), in
+// the model's 16-bit type T (bf16 or fp16; the kernels are templates on T,
+// whose 16-bit outputs are stored in T too).
 // Features are the MFMA rows, so each lane ends with 4 consecutive features
 // of one token: RoPE pairs and SwiGLU pairs are in-lane or one shuffle away
 // and stores are 8/16-byte vectors.
@@ -18,12 +20,13 @@
 //             position m % T, q to [B, H, T, dk] bf16, k/v to the KV cache.
 //   SWIGLU    W is W1/W3 interleaved in blocks of 8 rows; h = silu(a) * c
 //             (layers.py:114-115) as bf16 [M, d_ff].
+#include "attn_mfma.hpp"
+#include "gemm_f32.hpp"
 #include "lds_dma.hpp"
 
 namespace sfl {
 namespace {
 
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int TN = 128, TM = 128, TK = 64;
@@ -62,9 +65,29 @@ struct GemmArgs {
   int vec16;
 };
 
-__device__ __forceinline__ f32x4 mfma_bf16(const u32x4& a, const u32x4& b, f32x4 c) {
+template <typename T>
+__device__ __forceinline__ f32x4 mfma16(const u32x4& a, const u32x4& b, f32x4 c);
+template <>
+__device__ __forceinline__ f32x4 mfma16<bf16_t>(const u32x4& a, const u32x4& b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
 }
+template <>
+__device__ __forceinline__ f32x4 mfma16<f16_t>(const u32x4& a, const u32x4& b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+
+// One value rounded to T (round to nearest even), as raw bits.
+template <typename T> __device__ __forceinline__ uint16_t bits16(float v);
+template <> __device__ __forceinline__ uint16_t bits16<bf16_t>(float v) { return f32_to_bf16_bits(v); }
+template <> __device__ __forceinline__ uint16_t bits16<f16_t>(float v) { return f32_to_f16_bits(v); }
+
+// The low and high T values of a packed pair, as fp32.
+template <typename T> __device__ __forceinline__ float lo16(uint32_t w);
+template <typename T> __device__ __forceinline__ float hi16(uint32_t w);
+template <> __device__ __forceinline__ float lo16<bf16_t>(uint32_t w) { return bf16_lo(w); }
+template <> __device__ __forceinline__ float hi16<bf16_t>(uint32_t w) { return bf16_hi(w); }
+template <> __device__ __forceinline__ float lo16<f16_t>(uint32_t w) { return f16_bits_to_f32(uint16_t(w & 0xffffu)); }
+template <> __device__ __forceinline__ float hi16<f16_t>(uint32_t w) { return f16_bits_to_f32(uint16_t(w >> 16)); }
 
 // v, or zeros when !keep. Selected per component: a select of whole uint4
 // structs is lowered through scratch memory.
@@ -72,13 +95,6 @@ __device__ __forceinline__ uint4 keep16(const uint4& v, bool keep) {
   return make_uint4(keep ? v.x : 0u, keep ? v.y : 0u, keep ? v.z : 0u, keep ? v.w : 0u);
 }
 
-// Two values rounded to bf16 (round to nearest even, as f32_to_bf16_bits)
-// with one v_cvt_pk_bf16_f32.
-typedef __bf16 bf16x2_pk __attribute__((ext_vector_type(2)));
-typedef float f32x2_pk __attribute__((ext_vector_type(2)));
-__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_pk{lo, hi}), bf16x2_pk));
-}
 
 // Where a lane's 4 QKV features and its token go: section (0 q, 1 k, 2 v),
 // head, dim of the first feature; batch row and position of the token.
@@ -162,7 +178,7 @@ __device__ __forceinline__ uint4 pair8(const uint32_t (&a)[2], const uint32_t (&
 
 // Epilogue of one 16x16 MFMA tile: v holds features nt + 4*grp + (0..3) of
 // token m. Every lane must call it (the SwiGLU pairing shuffles).
-template <int E>
+template <typename T, int E>
 __device__ __forceinline__ void store_tile(const GemmArgs& g, const f32x4& v, int nt, int grp, int m,
                                            QkvFeat qf = QkvFeat{}, QkvTok qt = QkvTok{}) {
   const int n = nt + 4 * grp;
@@ -179,7 +195,7 @@ __device__ __forceinline__ void store_tile(const GemmArgs& g, const f32x4& v, in
     float h[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) h[e] = silu_mul(y[e], c3[e]);
-    *reinterpret_cast<uint2*>(g.h_out + long(m) * (g.n / 2) + f) = make_uint2(pack_bf16(h[0], h[1]), pack_bf16(h[2], h[3]));
+    *reinterpret_cast<uint2*>(g.h_out + long(m) * (g.n / 2) + f) = make_uint2(pack2<T>(h[0], h[1]), pack2<T>(h[2], h[3]));
   } else {
     if (m >= g.m || n >= g.n) return;
     if constexpr (E == G_PLAIN) {
@@ -196,21 +212,21 @@ __device__ __forceinline__ void store_tile(const GemmArgs& g, const f32x4& v, in
       } else {
         uint16_t* c = static_cast<uint16_t*>(g.c) + long(m) * g.n + n;
         if (n + 3 < g.n && (g.n & 3) == 0) {
-          *reinterpret_cast<uint2*>(c) = make_uint2(pack_bf16(y[0], y[1]), pack_bf16(y[2], y[3]));
+          *reinterpret_cast<uint2*>(c) = make_uint2(pack2<T>(y[0], y[1]), pack2<T>(y[2], y[3]));
         } else {
 #pragma unroll
           for (int e = 0; e < 4; ++e)
-            if (n + e < g.n) c[e] = f32_to_bf16_bits(y[e]);
+            if (n + e < g.n) c[e] = bits16<T>(y[e]);
         }
       }
     } else {  // G_QKV
       rope4(g, y, qf, qt);
-      *reinterpret_cast<uint2*>(qkv_dst(g, qf, qt)) = make_uint2(pack_bf16(y[0], y[1]), pack_bf16(y[2], y[3]));
+      *reinterpret_cast<uint2*>(qkv_dst(g, qf, qt)) = make_uint2(pack2<T>(y[0], y[1]), pack2<T>(y[2], y[3]));
     }
   }
 }
 
-template <int E>
+template <typename T, int E>
 __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
   __shared__ __align__(16) uint16_t ws[2][TN * LDT];
   __shared__ __align__(16) uint16_t as[2][TM * LDT];
@@ -269,7 +285,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = mfma_bf16(af[i], bfr[j], acc[i][j]);
+        for (int j = 0; j < 4; ++j) acc[i][j] = mfma16<T>(af[i], bfr[j], acc[i][j]);
     }
     if (kt + 1 < ksteps) {
       SFL_GEMM_SSTORE(buf ^ 1)
@@ -288,11 +304,11 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
     const QkvFeat feat = E == G_QKV ? qkv_feat(g, n0 + wn * 64 + i * 16 + 4 * grp) : QkvFeat{};
 #pragma unroll
     for (int j = 0; j < 4; ++j)
-      store_tile<E>(g, acc[i][j], n0 + wn * 64 + i * 16, grp, m0 + wm * 64 + j * 16 + col, feat, tok[j]);
+      store_tile<T, E>(g, acc[i][j], n0 + wn * 64 + i * 16, grp, m0 + wm * 64 + j * 16 + col, feat, tok[j]);
   }
 }
 
-// GEMM for K % 64 == 0 on v_mfma_f32_32x32x16_bf16 (on gfx950 the 32x32
+// GEMM for K % 64 == 0 on v_mfma_f32_32x32x16_{bf16,f16} (on gfx950 the 32x32
 // form sustains about twice the bf16 rate of the 16x16x32 form used above).
 // A workgroup of 4 waves (2 x 2) computes 128 features x 128 tokens; wave
 // (wn, wm) owns 2 x 2 MFMA tiles of 32x32. Operands reach LDS through buffer
@@ -307,11 +323,6 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmArgs g) {
 constexpr int K2 = 64;     // K step
 constexpr int TB = 128;    // features and tokens per workgroup
 
-typedef float f32x16 __attribute__((ext_vector_type(16)));
-
-__device__ __forceinline__ f32x16 mfma32_bf16(const u32x4& a, const u32x4& b, f32x16 c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
-}
 
 template <int TN_, int TM_, int SL_>
 struct Stage32 {
@@ -359,7 +370,7 @@ __device__ __forceinline__ int2 xcd_tile(int b, int tn, int tm) {
 // stages of 80 KB), 64 x 192 per wave (12 accumulator blocks, ~236 VGPRs, no
 // spills); per MFMA it stages 5/8 of the bytes of the 128 x 128 tile through
 // LDS and reads 2/3 of its LDS operand bytes.
-template <int E, int TBN, int TBM, int WN, int WM, int KS, int NS>
+template <typename T, int E, int TBN, int TBM, int WN, int WM, int KS, int NS>
 __global__ __launch_bounds__(64 * WN * WM) __attribute__((amdgpu_waves_per_eu(2)))
 void gemm32_kernel(GemmArgs g) {
   constexpr int NW = WN * WM;              // waves
@@ -422,7 +433,7 @@ void gemm32_kernel(GemmArgs g) {
       bfr[t] = u32x4{rb_.x, rb_.y, rb_.z, rb_.w};                                           \
     }                                                                                       \
     _Pragma("unroll") for (int i = 0; i < NBN; ++i)                                         \
-      _Pragma("unroll") for (int j = 0; j < NBM; ++j) acc[i][j] = mfma32_bf16(af[i], bfr[j], acc[i][j]); \
+      _Pragma("unroll") for (int j = 0; j < NBM; ++j) acc[i][j] = mfma32<T>(af[i], bfr[j], acc[i][j]); \
   }
 
   f32x16 acc[NBN][NBM];
@@ -515,7 +526,7 @@ void gemm32_kernel(GemmArgs g) {
 #pragma unroll
         for (int i = 0; i < NBN; ++i) {
           const int nt = n0 + (TBN / WN) * wn + 32 * i;
-          uint32_t pk[4][2];  // bf16(x * gain) of features nt + 8q + 4hf + (0..3)
+          uint32_t pk[4][2];  // T(x * gain) of features nt + 8q + 4hf + (0..3)
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
             const int n = nt + 8 * q + 4 * hf;
@@ -524,8 +535,8 @@ void gemm32_kernel(GemmArgs g) {
             const bool in = m < g.m && n < g.n;
             if (in) *reinterpret_cast<float4*>(c + long(m) * g.n + n) = v;
             if (norm) {
-              pk[q][0] = pack_bf16(v.x * bf16_lo(gw[i][q].x), v.y * bf16_hi(gw[i][q].x));
-              pk[q][1] = pack_bf16(v.z * bf16_lo(gw[i][q].y), v.w * bf16_hi(gw[i][q].y));
+              pk[q][0] = pack2<T>(v.x * lo16<T>(gw[i][q].x), v.y * hi16<T>(gw[i][q].x));
+              pk[q][1] = pack2<T>(v.z * lo16<T>(gw[i][q].y), v.w * hi16<T>(gw[i][q].y));
               if (in) ssq[j] += (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w);
             }
           }
@@ -604,8 +615,8 @@ void gemm32_kernel(GemmArgs g) {
             const float a1 = acc[i][j][4 * q + e] * rsc[j], a3 = acc[i][j][4 * q + 4 + e] * rsc[j];
             h[e] = silu_mul(a1, a3);
           }
-          pk[q / 2][0] = pack_bf16(h[0], h[1]);
-          pk[q / 2][1] = pack_bf16(h[2], h[3]);
+          pk[q / 2][0] = pack2<T>(h[0], h[1]);
+          pk[q / 2][1] = pack2<T>(h[2], h[3]);
         }
         if (g.vec16) {
           const uint4 v8 = pair8(pk[0], pk[1]);
@@ -636,8 +647,8 @@ void gemm32_kernel(GemmArgs g) {
                       : blk ? QkvFeat{fb.section, fb.head, fb.dim + 8 * (q + r) + 4 * hf}
                             : qkv_feat_at(g, fb, 8 * (q + r) + 4 * hf);
             if constexpr (E == G_QKV) rope4(g, y, feat[r], tok);
-            pk[r][0] = pack_bf16(y[0], y[1]);
-            pk[r][1] = pack_bf16(y[2], y[3]);
+            pk[r][0] = pack2<T>(y[0], y[1]);
+            pk[r][1] = pack2<T>(y[2], y[3]);
           }
           if (wide) {
             const uint4 v8 = pair8(pk[0], pk[1]);
@@ -673,7 +684,7 @@ void gemm32_kernel(GemmArgs g) {
                            acc[i][j][4 * q + 3] * rsc[j]};
           // store_tile's feature index is nt + 4 * grp: grp = 2q + hf.
           const QkvFeat feat = E == G_QKV ? qkv_feat_at(g, fb, 8 * q + 4 * hf) : QkvFeat{};
-          store_tile<E>(g, v, nt, 2 * q + hf, m, feat, tok);
+          store_tile<T, E>(g, v, nt, 2 * q + hf, m, feat, tok);
         }
       }
     }
@@ -682,8 +693,8 @@ void gemm32_kernel(GemmArgs g) {
 
 inline bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
 
-template <int E>
-int launch_gemm(const GemmArgs& g, hipStream_t s, const char* what) {
+template <typename T, int E>
+int launch_gemm_t(const GemmArgs& g, hipStream_t s, const char* what) {
   if (g.m < 1 || g.n < 1 || g.k < 1) return set_error(SFL_ERR_INVALID, "%s: sizes must be positive", what);
   if (g.k % 8) return set_error(SFL_ERR_UNSUPPORTED, "%s: K must be a multiple of 8", what);
   if (g.k % K2 == 0 && long(g.m) * g.k < (1L << 30) && long(g.n) * g.k < (1L << 30)) {
@@ -696,15 +707,23 @@ int launch_gemm(const GemmArgs& g, hipStream_t s, const char* what) {
     // were no better).
     const long big = long((g.n + 255) / 256) * ((g.m + 383) / 384);
     if (big >= 320)
-      hipLaunchKernelGGL((gemm32_kernel<E, 256, 384, 4, 2, 64, 2>), dim3(unsigned(big)), dim3(512), 0, s, g);
+      hipLaunchKernelGGL((gemm32_kernel<T, E, 256, 384, 4, 2, 64, 2>), dim3(unsigned(big)), dim3(512), 0, s, g);
     else
-      hipLaunchKernelGGL((gemm32_kernel<E, 128, 128, 2, 2, 64, 2>), dim3(unsigned(tiles)), dim3(kThreads), 0, s, g);
+      hipLaunchKernelGGL((gemm32_kernel<T, E, 128, 128, 2, 2, 64, 2>), dim3(unsigned(tiles)), dim3(kThreads), 0, s, g);
     return check_launch(what);
   }
   dim3 grid((g.n + TN - 1) / TN, (g.m + TM - 1) / TM);
   if (grid.y > 65535) return set_error(SFL_ERR_UNSUPPORTED, "%s: M too large", what);
-  hipLaunchKernelGGL((gemm_kernel<E>), grid, dim3(kThreads), 0, s, g);
+  hipLaunchKernelGGL((gemm_kernel<T, E>), grid, dim3(kThreads), 0, s, g);
   return check_launch(what);
+}
+
+// The GEMMs' 16-bit element type: SFL_DTYPE_BF16 or SFL_DTYPE_F16.
+template <int E>
+int launch_gemm(const GemmArgs& g, int dtype, hipStream_t s, const char* what) {
+  if (dtype == SFL_DTYPE_BF16) return launch_gemm_t<bf16_t, E>(g, s, what);
+  if (dtype == SFL_DTYPE_F16) return launch_gemm_t<f16_t, E>(g, s, what);
+  return set_error(SFL_ERR_UNSUPPORTED, "%s: dtype must be BF16 or F16", what);
 }
 
 // Prefill embedding gather: x[m] = emb[ids[m]] in fp32.
@@ -715,9 +734,10 @@ __global__ __launch_bounds__(256) void embed_rows_kernel(const int64_t* ids, con
   for (int i = threadIdx.x; i < d; i += blockDim.x) x[m * d + i] = load_scalar<T>(src + i);
 }
 
-// Prefill RMSNorm: out[m] = bf16(x[m] / sqrt(mean(x[m]^2) + eps) * w) (layers.py:133-141).
-template <typename T>
-__global__ __launch_bounds__(256) void rmsnorm_rows_kernel(const float* x, const T* w, uint16_t* out, int d) {
+// Prefill RMSNorm: out[m] = O(x[m] / sqrt(mean(x[m]^2) + eps) * w) (layers.py:133-141),
+// O the GEMMs' 16-bit type.
+template <typename T, typename O>
+__global__ __launch_bounds__(256) void rmsnorm_rows_kernel(const float* x, const T* w, O* out, int d) {
   __shared__ float part[4];
   const long m = blockIdx.x;
   const float* xr = x + m * d;
@@ -728,18 +748,18 @@ __global__ __launch_bounds__(256) void rmsnorm_rows_kernel(const float* x, const
   __syncthreads();
   const float total = part[0] + part[1] + part[2] + part[3];
   const float inv = 1.f / sqrtf(total / float(d) + 1e-5f);
-  for (int i = threadIdx.x; i < d; i += 256) out[m * d + i] = f32_to_bf16_bits((xr[i] * inv) * load_scalar<T>(w + i));
+  for (int i = threadIdx.x; i < d; i += 256) store_scalar<O>(out + m * d + i, (xr[i] * inv) * load_scalar<T>(w + i));
 }
 
 // The same for rows of d % 4 == 0 and d <= 4 * 64 * kNormVec with one wave per
 // row: the row is read once with 16-byte loads and kept in registers, the sum
 // of squares is a wave reduction (no LDS, no barrier), and each lane stores
-// four bf16 values at a time.
+// four 16-bit values at a time.
 constexpr int kNormVec = 8;
-// kScaled: out = bf16(x * w) and rscale[row] = 1 / rms(x), for a consumer GEMM
+// kScaled: out = O(x * w) and rscale[row] = 1 / rms(x), for a consumer GEMM
 // that applies the scale to its products.
-template <typename T, bool kScaled = false>
-__global__ __launch_bounds__(256) void rmsnorm_rows_wave_kernel(const float* x, const T* w, uint16_t* out, int m,
+template <typename T, typename O, bool kScaled = false>
+__global__ __launch_bounds__(256) void rmsnorm_rows_wave_kernel(const float* x, const T* w, O* out, int m,
                                                                int d, float* rscale = nullptr) {
   const long row = long(blockIdx.x) * 4 + threadIdx.x / kWave;
   const int lane = threadIdx.x % kWave;
@@ -769,7 +789,10 @@ __global__ __launch_bounds__(256) void rmsnorm_rows_wave_kernel(const float* x, 
       }
       y0 *= load_scalar<T>(w + i); y1 *= load_scalar<T>(w + i + 1);
       y2 *= load_scalar<T>(w + i + 2); y3 *= load_scalar<T>(w + i + 3);
-      *reinterpret_cast<uint2*>(out + row * d + i) = make_uint2(pack_bf16(y0, y1), pack_bf16(y2, y3));
+      if constexpr (sizeof(O) == 4)
+        *reinterpret_cast<float4*>(out + row * d + i) = make_float4(y0, y1, y2, y3);
+      else
+        *reinterpret_cast<uint2*>(out + row * d + i) = make_uint2(pack2<O>(y0, y1), pack2<O>(y2, y3));
     }
   }
 }
@@ -790,23 +813,35 @@ __global__ __launch_bounds__(256) void norm_scale_kernel(const float* __restrict
 
 using namespace sfl;
 
-extern "C" int sfl_gemm_bf16(const void* a, const void* w, void* c, int m, int n, int k, int c_dtype,
-                             int accumulate, void* stream) {
-  if (!a || !w || !c) return set_error(SFL_ERR_INVALID, "gemm_bf16: null pointer argument");
-  if (c_dtype != SFL_DTYPE_F32 && c_dtype != SFL_DTYPE_BF16)
-    return set_error(SFL_ERR_UNSUPPORTED, "gemm_bf16: output dtype must be F32 or BF16");
+// The GEMMs' 16-bit element type (A, W and 16-bit outputs).
+static bool gemm_dtype_ok(int dtype) { return dtype == SFL_DTYPE_BF16 || dtype == SFL_DTYPE_F16; }
+
+extern "C" int sfl_gemm(const void* a, const void* w, void* c, int m, int n, int k, int dtype, int c_dtype,
+                        int accumulate, void* stream) {
+  const char* what = "gemm";
+  if (!a || !w || !c) return set_error(SFL_ERR_INVALID, "%s: null pointer argument", what);
+  if (dtype == SFL_DTYPE_F32) {  // the fp32 MFMA GEMM (prefill_f32.hip)
+    if (c_dtype != SFL_DTYPE_F32) return set_error(SFL_ERR_UNSUPPORTED, "%s: F32 inputs need an F32 output", what);
+    F32GemmArgs f{};
+    f.a = static_cast<const float*>(a); f.w = static_cast<const float*>(w);
+    f.m = m; f.n = n; f.k = k; f.c = static_cast<float*>(c); f.accumulate = accumulate;
+    return launch_gemm_f32(f, F32_PLAIN, static_cast<hipStream_t>(stream), what);
+  }
+  if (!gemm_dtype_ok(dtype)) return set_error(SFL_ERR_UNSUPPORTED, "%s: dtype must be F32, BF16 or F16", what);
+  if (c_dtype != SFL_DTYPE_F32 && c_dtype != dtype)
+    return set_error(SFL_ERR_UNSUPPORTED, "%s: output dtype must be F32 or the input dtype", what);
   if (accumulate && c_dtype != SFL_DTYPE_F32)
-    return set_error(SFL_ERR_UNSUPPORTED, "gemm_bf16: accumulation needs an F32 output");
+    return set_error(SFL_ERR_UNSUPPORTED, "%s: accumulation needs an F32 output", what);
   GemmArgs g{};
   g.a = static_cast<const uint16_t*>(a); g.w = static_cast<const uint16_t*>(w);
   g.m = m; g.n = n; g.k = k; g.c = c; g.c_f32 = c_dtype == SFL_DTYPE_F32; g.accumulate = accumulate;
   g.vec16 = aligned16(c);
-  return launch_gemm<G_PLAIN>(g, static_cast<hipStream_t>(stream), "gemm_bf16");
+  return launch_gemm<G_PLAIN>(g, dtype, static_cast<hipStream_t>(stream), what);
 }
 
 extern "C" int sfl_gemm_qkv_rope(const void* a, const void* w_qkv, int m, int seq, int d_model, int heads,
                                  const float* cos_t, const float* sin_t, void* q_out, void* k_cache,
-                                 void* v_cache, int capacity, void* stream) {
+                                 void* v_cache, int capacity, int dtype, void* stream) {
   const char* what = "gemm_qkv_rope";
   if (!a || !w_qkv || !cos_t || !sin_t || !q_out || !k_cache || !v_cache)
     return set_error(SFL_ERR_INVALID, "%s: null pointer argument", what);
@@ -814,6 +849,18 @@ extern "C" int sfl_gemm_qkv_rope(const void* a, const void* w_qkv, int m, int se
   if (heads < 1 || d_model % heads || (d_model / heads) % 16)
     return set_error(SFL_ERR_UNSUPPORTED, "%s: head dim must be a multiple of 16", what);
   if (seq > capacity) return set_error(SFL_ERR_INVALID, "%s: seq exceeds the cache capacity", what);
+  if (dtype == SFL_DTYPE_F32) {
+    if (!aligned16(q_out) || !aligned16(k_cache) || !aligned16(v_cache))
+      return set_error(SFL_ERR_INVALID, "%s: fp32 q and caches must be 16-byte aligned", what);
+    F32GemmArgs f{};
+    f.a = static_cast<const float*>(a); f.w = static_cast<const float*>(w_qkv);
+    f.m = m; f.n = 3 * d_model; f.k = d_model;
+    f.cos_t = cos_t; f.sin_t = sin_t; f.seq = seq; f.heads = heads; f.head_dim = d_model / heads;
+    f.d_model = d_model; f.cap = capacity;
+    f.q_out = static_cast<float*>(q_out); f.k_cache = static_cast<float*>(k_cache);
+    f.v_cache = static_cast<float*>(v_cache);
+    return launch_gemm_f32(f, F32_QKV, static_cast<hipStream_t>(stream), what);
+  }
   GemmArgs g{};
   g.a = static_cast<const uint16_t*>(a); g.w = static_cast<const uint16_t*>(w_qkv);
   g.m = m; g.n = 3 * d_model; g.k = d_model;
@@ -822,7 +869,7 @@ extern "C" int sfl_gemm_qkv_rope(const void* a, const void* w_qkv, int m, int se
   g.q_out = static_cast<uint16_t*>(q_out); g.k_cache = static_cast<uint16_t*>(k_cache);
   g.v_cache = static_cast<uint16_t*>(v_cache);
   g.vec16 = aligned16(q_out) && aligned16(k_cache) && aligned16(v_cache);
-  return launch_gemm<G_QKV>(g, static_cast<hipStream_t>(stream), what);
+  return launch_gemm<G_QKV>(g, dtype, static_cast<hipStream_t>(stream), what);
 }
 
 // The fused-norm entry points need the 32x32 kernels (K % 64 == 0, 32-bit offsets).
@@ -832,7 +879,8 @@ static bool gemm32_path(int m, int n, int k) {
 
 extern "C" int sfl_gemm_qkv_rope_scaled(const void* a_xg, const void* w_qkv, const float* rscale, int m, int seq,
                                         int d_model, int heads, const float* cos_t, const float* sin_t,
-                                        void* q_out, void* k_cache, void* v_cache, int capacity, void* stream) {
+                                        void* q_out, void* k_cache, void* v_cache, int capacity, int dtype,
+                                        void* stream) {
   const char* what = "gemm_qkv_rope_scaled";
   if (!rscale) return set_error(SFL_ERR_INVALID, "%s: null pointer argument", what);
   if (!gemm32_path(m, 3 * d_model, d_model))
@@ -852,11 +900,11 @@ extern "C" int sfl_gemm_qkv_rope_scaled(const void* a_xg, const void* w_qkv, con
   g.v_cache = static_cast<uint16_t*>(v_cache);
   g.vec16 = aligned16(q_out) && aligned16(k_cache) && aligned16(v_cache);
   g.row_scale = rscale;
-  return launch_gemm<G_QKV>(g, static_cast<hipStream_t>(stream), what);
+  return launch_gemm<G_QKV>(g, dtype, static_cast<hipStream_t>(stream), what);
 }
 
 extern "C" int sfl_gemm_swiglu_scaled(const void* a_xg, const void* w13_interleaved, const float* rscale,
-                                      void* h_out, int m, int d_ff, int k, void* stream) {
+                                      void* h_out, int m, int d_ff, int k, int dtype, void* stream) {
   const char* what = "gemm_swiglu_scaled";
   if (!a_xg || !w13_interleaved || !rscale || !h_out)
     return set_error(SFL_ERR_INVALID, "%s: null pointer argument", what);
@@ -867,11 +915,12 @@ extern "C" int sfl_gemm_swiglu_scaled(const void* a_xg, const void* w13_interlea
   g.m = m; g.n = 2 * d_ff; g.k = k; g.h_out = static_cast<uint16_t*>(h_out);
   g.vec16 = aligned16(h_out);
   g.row_scale = rscale;
-  return launch_gemm<G_SWIGLU>(g, static_cast<hipStream_t>(stream), what);
+  return launch_gemm<G_SWIGLU>(g, dtype, static_cast<hipStream_t>(stream), what);
 }
 
 extern "C" int sfl_gemm_residual_norm(const void* a, const void* w, float* x, int m, int n, int k,
-                                      const void* gain_next, void* act_xg, float* ss_parts, void* stream) {
+                                      const void* gain_next, void* act_xg, float* ss_parts, int dtype,
+                                      void* stream) {
   const char* what = "gemm_residual_norm";
   if (!a || !w || !x || !gain_next || !act_xg || !ss_parts)
     return set_error(SFL_ERR_INVALID, "%s: null pointer argument", what);
@@ -888,7 +937,7 @@ extern "C" int sfl_gemm_residual_norm(const void* a, const void* w, float* x, in
   g.norm_act = static_cast<uint16_t*>(act_xg);
   g.norm_ss = ss_parts;
   g.vec16 = aligned16(act_xg) && n % 8 == 0;  // rows of act start 16-byte aligned
-  return launch_gemm<G_PLAIN>(g, static_cast<hipStream_t>(stream), what);
+  return launch_gemm<G_PLAIN>(g, dtype, static_cast<hipStream_t>(stream), what);
 }
 
 extern "C" int sfl_norm_scale(const float* ss_parts, int parts, int m, int d_model, float* rscale, void* stream) {
@@ -904,27 +953,38 @@ extern "C" int sfl_rmsnorm_rows_scaled(const float* x, const void* w, void* act_
   const char* what = "rmsnorm_rows_scaled";
   if (!x || !w || !act_xg || !rscale) return set_error(SFL_ERR_INVALID, "%s: null pointer argument", what);
   if (m < 1 || d_model < 1) return set_error(SFL_ERR_INVALID, "%s: sizes must be positive", what);
-  if (dtype != SFL_DTYPE_BF16) return set_error(SFL_ERR_UNSUPPORTED, "%s: dtype must be BF16", what);
+  if (!gemm_dtype_ok(dtype)) return set_error(SFL_ERR_UNSUPPORTED, "%s: dtype must be BF16 or F16", what);
   if (d_model % 4 || d_model > 4 * kWave * kNormVec || reinterpret_cast<uintptr_t>(x) % 16 ||
       reinterpret_cast<uintptr_t>(act_xg) % 8)
     return set_error(SFL_ERR_UNSUPPORTED, "%s: d_model must be a multiple of 4 and at most %d, x 16-byte and "
                      "act 8-byte aligned", what, 4 * kWave * kNormVec);
-  hipLaunchKernelGGL((rmsnorm_rows_wave_kernel<bf16_t, true>), dim3((m + 3) / 4), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), x, static_cast<const bf16_t*>(w),
-                     static_cast<uint16_t*>(act_xg), m, d_model, rscale);
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == SFL_DTYPE_BF16)
+    hipLaunchKernelGGL((rmsnorm_rows_wave_kernel<bf16_t, bf16_t, true>), dim3((m + 3) / 4), dim3(256), 0, s, x,
+                       static_cast<const bf16_t*>(w), static_cast<bf16_t*>(act_xg), m, d_model, rscale);
+  else
+    hipLaunchKernelGGL((rmsnorm_rows_wave_kernel<f16_t, f16_t, true>), dim3((m + 3) / 4), dim3(256), 0, s, x,
+                       static_cast<const f16_t*>(w), static_cast<f16_t*>(act_xg), m, d_model, rscale);
   return check_launch(what);
 }
 
 extern "C" int sfl_gemm_swiglu(const void* a, const void* w13_interleaved, void* h_out, int m, int d_ff,
-                               int k, void* stream) {
+                               int k, int dtype, void* stream) {
   const char* what = "gemm_swiglu";
   if (!a || !w13_interleaved || !h_out) return set_error(SFL_ERR_INVALID, "%s: null pointer argument", what);
   if (d_ff % 8) return set_error(SFL_ERR_UNSUPPORTED, "%s: d_ff must be a multiple of 8", what);
+  if (dtype == SFL_DTYPE_F32) {
+    if (!aligned16(h_out)) return set_error(SFL_ERR_INVALID, "%s: fp32 h must be 16-byte aligned", what);
+    F32GemmArgs f{};
+    f.a = static_cast<const float*>(a); f.w = static_cast<const float*>(w13_interleaved);
+    f.m = m; f.n = 2 * d_ff; f.k = k; f.h_out = static_cast<float*>(h_out);
+    return launch_gemm_f32(f, F32_SWIGLU, static_cast<hipStream_t>(stream), what);
+  }
   GemmArgs g{};
   g.a = static_cast<const uint16_t*>(a); g.w = static_cast<const uint16_t*>(w13_interleaved);
   g.m = m; g.n = 2 * d_ff; g.k = k; g.h_out = static_cast<uint16_t*>(h_out);
   g.vec16 = aligned16(h_out);
-  return launch_gemm<G_SWIGLU>(g, static_cast<hipStream_t>(stream), what);
+  return launch_gemm<G_SWIGLU>(g, dtype, static_cast<hipStream_t>(stream), what);
 }
 
 extern "C" int sfl_embed_rows(const int64_t* ids, const void* emb, float* x, int m, int d_model, int dtype,
@@ -934,37 +994,45 @@ extern "C" int sfl_embed_rows(const int64_t* ids, const void* emb, float* x, int
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (dtype == SFL_DTYPE_BF16)
     hipLaunchKernelGGL(embed_rows_kernel<bf16_t>, dim3(m), dim3(256), 0, s, ids, static_cast<const bf16_t*>(emb), x, d_model);
+  else if (dtype == SFL_DTYPE_F16)
+    hipLaunchKernelGGL(embed_rows_kernel<f16_t>, dim3(m), dim3(256), 0, s, ids, static_cast<const f16_t*>(emb), x, d_model);
   else if (dtype == SFL_DTYPE_F32)
     hipLaunchKernelGGL(embed_rows_kernel<float>, dim3(m), dim3(256), 0, s, ids, static_cast<const float*>(emb), x, d_model);
   else
-    return set_error(SFL_ERR_UNSUPPORTED, "embed_rows: dtype must be F32 or BF16");
+    return set_error(SFL_ERR_UNSUPPORTED, "embed_rows: dtype must be F32, BF16 or F16");
   return check_launch("embed_rows");
 }
 
-extern "C" int sfl_rmsnorm_rows(const float* x, const void* w, void* out_bf16, int m, int d_model, int dtype,
-                                void* stream) {
-  if (!x || !w || !out_bf16) return set_error(SFL_ERR_INVALID, "rmsnorm_rows: null pointer argument");
-  if (m < 1 || d_model < 1) return set_error(SFL_ERR_INVALID, "rmsnorm_rows: sizes must be positive");
-  if (dtype != SFL_DTYPE_BF16 && dtype != SFL_DTYPE_F32)
-    return set_error(SFL_ERR_UNSUPPORTED, "rmsnorm_rows: dtype must be F32 or BF16");
+template <typename T, typename O>
+static void launch_rmsnorm_rows(const float* x, const void* w, void* out, int m, int d, bool wave_rows, hipStream_t s) {
+  if (wave_rows)
+    hipLaunchKernelGGL((rmsnorm_rows_wave_kernel<T, O>), dim3((m + 3) / 4), dim3(256), 0, s, x,
+                       static_cast<const T*>(w), static_cast<O*>(out), m, d, nullptr);
+  else
+    hipLaunchKernelGGL((rmsnorm_rows_kernel<T, O>), dim3(m), dim3(256), 0, s, x, static_cast<const T*>(w),
+                       static_cast<O*>(out), d);
+}
+
+extern "C" int sfl_rmsnorm_rows(const float* x, const void* w, void* out, int m, int d_model, int dtype,
+                                int out_dtype, void* stream) {
+  const char* what = "rmsnorm_rows";
+  if (!x || !w || !out) return set_error(SFL_ERR_INVALID, "%s: null pointer argument", what);
+  if (m < 1 || d_model < 1) return set_error(SFL_ERR_INVALID, "%s: sizes must be positive", what);
+  if (dtype != SFL_DTYPE_BF16 && dtype != SFL_DTYPE_F16 && dtype != SFL_DTYPE_F32)
+    return set_error(SFL_ERR_UNSUPPORTED, "%s: dtype must be F32, BF16 or F16", what);
+  if (out_dtype != SFL_DTYPE_BF16 && out_dtype != SFL_DTYPE_F16 && out_dtype != SFL_DTYPE_F32)
+    return set_error(SFL_ERR_UNSUPPORTED, "%s: out dtype must be F32, BF16 or F16", what);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  uint16_t* out = static_cast<uint16_t*>(out_bf16);
   const bool wave_rows = d_model % 4 == 0 && d_model <= 4 * kWave * kNormVec &&
-                         reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(out) % 8 == 0;
-  if (wave_rows) {
-    const dim3 grid((m + 3) / 4);
-    if (dtype == SFL_DTYPE_BF16)
-      hipLaunchKernelGGL(rmsnorm_rows_wave_kernel<bf16_t>, grid, dim3(256), 0, s, x, static_cast<const bf16_t*>(w),
-                         out, m, d_model);
-    else
-      hipLaunchKernelGGL(rmsnorm_rows_wave_kernel<float>, grid, dim3(256), 0, s, x, static_cast<const float*>(w), out,
-                         m, d_model);
-  } else if (dtype == SFL_DTYPE_BF16) {
-    hipLaunchKernelGGL(rmsnorm_rows_kernel<bf16_t>, dim3(m), dim3(256), 0, s, x, static_cast<const bf16_t*>(w), out,
-                       d_model);
-  } else {
-    hipLaunchKernelGGL(rmsnorm_rows_kernel<float>, dim3(m), dim3(256), 0, s, x, static_cast<const float*>(w), out,
-                       d_model);
+                         reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
+                         reinterpret_cast<uintptr_t>(out) % (out_dtype == SFL_DTYPE_F32 ? 16 : 8) == 0;
+  const int key = dtype * 8 + out_dtype;
+  switch (key) {
+    case SFL_DTYPE_BF16 * 8 + SFL_DTYPE_BF16: launch_rmsnorm_rows<bf16_t, bf16_t>(x, w, out, m, d_model, wave_rows, s); break;
+    case SFL_DTYPE_F32 * 8 + SFL_DTYPE_BF16: launch_rmsnorm_rows<float, bf16_t>(x, w, out, m, d_model, wave_rows, s); break;
+    case SFL_DTYPE_F16 * 8 + SFL_DTYPE_F16: launch_rmsnorm_rows<f16_t, f16_t>(x, w, out, m, d_model, wave_rows, s); break;
+    case SFL_DTYPE_F32 * 8 + SFL_DTYPE_F32: launch_rmsnorm_rows<float, float>(x, w, out, m, d_model, wave_rows, s); break;
+    default: return set_error(SFL_ERR_UNSUPPORTED, "%s: unsupported weight / output dtype pair", what);
   }
-  return check_launch("rmsnorm_rows");
+  return check_launch(what);
 }

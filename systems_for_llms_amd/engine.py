@@ -276,21 +276,21 @@ class DecodeSession:
         Fills the KV cache at positions 0..T-1, computes the logits of position
         T-1 with the decode head, and leaves every row at position T (the next
         token written, embedded and ready for ``step``). With ``all_logits`` it
-        also returns fp32 logits ``[B, T, V]`` for every position (the
-        reference's ``forward``). bf16 models only; fp32 models use ``start`` +
-        ``run`` (one position per step). ``forced [B, L]`` (L > T, starting with
-        the prompt) makes the following positions up to L teacher-forced.
-        ``logits_dtype`` (float32 or bfloat16) is the type the all-positions
-        lm_head GEMM stores: bfloat16 rounds its fp32 sums once, as a cast of
-        the fp32 logits would, with half the stores and no cast pass.
+        also returns logits ``[B, T, V]`` for every position (the reference's
+        ``forward``). 16-bit models store their GEMM inputs in the model dtype;
+        float32 models run the same pass in fp32 (fp32 MFMA GEMMs, fp32
+        attention, separate norm passes). ``forced [B, L]`` (L > T, starting
+        with the prompt) makes the following positions up to L teacher-forced.
+        ``logits_dtype`` (float32 or the model dtype) is the type the
+        all-positions lm_head GEMM stores: a 16-bit model dtype rounds its fp32
+        sums once, as a cast of the fp32 logits would, with half the stores and
+        no cast pass.
         """
-        if self.dtype != torch.bfloat16:
-            raise TypeError("GEMM prefill needs a bfloat16 model; use start() + run() for float32")
         b, t = prompt.shape
         if b != self.batch or not 0 < t <= self.cap:
             raise ValueError("prompt must be [batch, T] with 0 < T <= capacity")
-        if logits_dtype not in (torch.float32, torch.bfloat16):
-            raise TypeError("logits_dtype must be torch.float32 or torch.bfloat16")
+        if logits_dtype not in (torch.float32, self.dtype):
+            raise TypeError("logits_dtype must be torch.float32 or the model dtype")
         low, high = torch.aminmax(prompt)
         if low.item() < 0 or high.item() >= self.vocab:
             raise ValueError("token ids must be in [0, vocab_size)")
@@ -298,6 +298,7 @@ class DecodeSession:
 
         d, h, dk, f, v = self.d, self.heads, self.dk, self.d_ff, self.vocab
         m_rows = b * t
+        F32 = _lib.DTYPE_CODES[torch.float32]
         dev, code = self.device, self.code
         w13 = self.weights.w13()
         self.tokens.zero_()
@@ -310,16 +311,18 @@ class DecodeSession:
             self.tokens[:, :forced.shape[1]] = forced.to(dev)
             self.prompt_len.fill_(forced.shape[1])
         ids = self.tokens[:, :t].contiguous().view(-1)
+        if self.dtype == torch.float32:
+            return self._prefill_f32(ids, b, t, all_logits)
         x = torch.empty((m_rows, d), device=dev, dtype=torch.float32)
-        act = torch.empty((m_rows, d), device=dev, dtype=torch.bfloat16)
-        q = torch.empty((b, h, t, dk), device=dev, dtype=torch.bfloat16)
-        attn = torch.empty((b, t, h, dk), device=dev, dtype=torch.bfloat16)
-        hid = torch.empty((m_rows, f), device=dev, dtype=torch.bfloat16)
+        act = torch.empty((m_rows, d), device=dev, dtype=self.dtype)
+        q = torch.empty((b, h, t, dk), device=dev, dtype=self.dtype)
+        attn = torch.empty((b, t, h, dk), device=dev, dtype=self.dtype)
+        hid = torch.empty((m_rows, f), device=dev, dtype=self.dtype)
         st = _lib.stream_handle(dev)
         call = _lib.call
         call("sfl_embed_rows", ids.data_ptr(), self.model.token_embeddings.weight.data_ptr(), x.data_ptr(),
              m_rows, d, code, st)
-        # Folded norms: a layer's GEMM input is bf16(x * g) and the GEMM scales its
+        # Folded norms: a layer's GEMM input is T(x * g) and the GEMM scales its
         # products by 1 / rms(x); the residual GEMM that updates x also writes the
         # next norm's input and per-128-feature sums of x^2 (one more small kernel
         # turns them into the scales), so no pass of its own re-reads x.
@@ -336,43 +339,47 @@ class DecodeSession:
             if fold:
                 call("sfl_gemm_qkv_rope_scaled", act.data_ptr(), self.wqkv[layer].data_ptr(), rsc.data_ptr(), m_rows,
                      t, d, h, self.cos_fm.data_ptr(), self.sin_fm.data_ptr(), q.data_ptr(), kc.data_ptr(),
-                     vc.data_ptr(), self.cap, st)
+                     vc.data_ptr(), self.cap, code, st)
             else:
                 call("sfl_rmsnorm_rows", x.data_ptr(), blk.attn_norm.weight.data_ptr(), act.data_ptr(), m_rows, d,
-                     code, st)
+                     code, code, st)
                 call("sfl_gemm_qkv_rope", act.data_ptr(), self.wqkv[layer].data_ptr(), m_rows, t, d, h,
                      self.cos_fm.data_ptr(), self.sin_fm.data_ptr(), q.data_ptr(), kc.data_ptr(), vc.data_ptr(),
-                     self.cap, st)
+                     self.cap, code, st)
             causal_prefill(q, kc[:, :, :t], vc[:, :, :t], attn.transpose(1, 2))
             if fold:
                 call("sfl_gemm_residual_norm", attn.data_ptr(), blk.attn.output_proj.weight.data_ptr(), x.data_ptr(),
-                     m_rows, d, d, blk.ffn_norm.weight.data_ptr(), act.data_ptr(), ss.data_ptr(), st)
+                     m_rows, d, d, blk.ffn_norm.weight.data_ptr(), act.data_ptr(), ss.data_ptr(), code, st)
                 call("sfl_norm_scale", ss.data_ptr(), parts, m_rows, d, rsc.data_ptr(), st)
                 call("sfl_gemm_swiglu_scaled", act.data_ptr(), w13[layer].data_ptr(), rsc.data_ptr(), hid.data_ptr(),
-                     m_rows, f, d, st)
+                     m_rows, f, d, code, st)
             else:
-                call("sfl_gemm_bf16", attn.data_ptr(), blk.attn.output_proj.weight.data_ptr(), x.data_ptr(),
-                     m_rows, d, d, 0, 1, st)
+                call("sfl_gemm", attn.data_ptr(), blk.attn.output_proj.weight.data_ptr(), x.data_ptr(),
+                     m_rows, d, d, code, F32, 1, st)
                 call("sfl_rmsnorm_rows", x.data_ptr(), blk.ffn_norm.weight.data_ptr(), act.data_ptr(), m_rows, d,
-                     code, st)
-                call("sfl_gemm_swiglu", act.data_ptr(), w13[layer].data_ptr(), hid.data_ptr(), m_rows, f, d, st)
+                     code, code, st)
+                call("sfl_gemm_swiglu", act.data_ptr(), w13[layer].data_ptr(), hid.data_ptr(), m_rows, f, d, code, st)
             if fold and layer + 1 < len(layers):
                 call("sfl_gemm_residual_norm", hid.data_ptr(), blk.ffn.w2.weight.data_ptr(), x.data_ptr(), m_rows,
-                     d, f, layers[layer + 1].attn_norm.weight.data_ptr(), act.data_ptr(), ss.data_ptr(), st)
+                     d, f, layers[layer + 1].attn_norm.weight.data_ptr(), act.data_ptr(), ss.data_ptr(), code, st)
                 call("sfl_norm_scale", ss.data_ptr(), parts, m_rows, d, rsc.data_ptr(), st)
             else:
-                call("sfl_gemm_bf16", hid.data_ptr(), blk.ffn.w2.weight.data_ptr(), x.data_ptr(), m_rows, d, f, 0, 1,
-                     st)
+                call("sfl_gemm", hid.data_ptr(), blk.ffn.w2.weight.data_ptr(), x.data_ptr(), m_rows, d, f, code, F32,
+                     1, st)
         logits = None
         if all_logits:
             call("sfl_rmsnorm_rows", x.data_ptr(), self.model.ln_final.weight.data_ptr(), act.data_ptr(),
-                 m_rows, d, code, st)
+                 m_rows, d, code, code, st)
             logits = torch.empty((m_rows, v), device=dev, dtype=logits_dtype)
-            call("sfl_gemm_bf16", act.data_ptr(), self.model.lm_head.weight.data_ptr(), logits.data_ptr(),
-                 m_rows, v, d, int(logits_dtype == torch.bfloat16), 0, st)
+            call("sfl_gemm", act.data_ptr(), self.model.lm_head.weight.data_ptr(), logits.data_ptr(),
+                 m_rows, v, d, code, _lib.dtype_code(logits_dtype), 0, st)
             logits = logits.view(b, t, v)
-        # Hand the last position to the decode head: pick token T and advance.
-        self.x.copy_(x.view(b, t, d)[:, t - 1])
+        self._hand_over(x, b, t, st)
+        return logits
+
+    def _hand_over(self, x, b, t, st) -> None:
+        """Hand the prompt's last position to the decode head: pick token T and advance."""
+        self.x.copy_(x.view(b, t, self.d)[:, t - 1])
         self.pos.fill_(t - 1)
         self.lengths.fill_(t)
         self.position = t
@@ -381,6 +388,50 @@ class DecodeSession:
             if status != 0:
                 raise RuntimeError(f"{fn.__name__} failed ({status}): "
                                    f"{_lib.lib().sfl_last_error().decode(errors='replace')}")
+
+    def _prefill_f32(self, ids, b, t, all_logits):
+        """``prefill`` of a float32 model: the reference's fp32 forward (transformer.py:121-139)
+        as one pass of fp32 MFMA GEMMs (q/k/v + RoPE + cache, output_proj + residual, SwiGLU,
+        w2 + residual) and fp32 causal attention, the norms as separate fp32 passes."""
+        from .attention import causal_prefill
+
+        d, h, dk, f, v = self.d, self.heads, self.dk, self.d_ff, self.vocab
+        m_rows, dev, F32 = b * t, self.device, _lib.DTYPE_CODES[torch.float32]
+        w13 = self.weights.w13()
+        x = torch.empty((m_rows, d), device=dev, dtype=torch.float32)
+        act = torch.empty((m_rows, d), device=dev, dtype=torch.float32)
+        q = torch.empty((b, h, t, dk), device=dev, dtype=torch.float32)
+        attn = torch.empty((b, t, h, dk), device=dev, dtype=torch.float32)
+        hid = torch.empty((m_rows, f), device=dev, dtype=torch.float32)
+        st = _lib.stream_handle(dev)
+        call = _lib.call
+        call("sfl_embed_rows", ids.data_ptr(), self.model.token_embeddings.weight.data_ptr(), x.data_ptr(), m_rows, d,
+             F32, st)
+        for layer, blk in enumerate(self.model.layers):
+            kc, vc = self.k_cache[layer], self.v_cache[layer]
+            call("sfl_rmsnorm_rows", x.data_ptr(), blk.attn_norm.weight.data_ptr(), act.data_ptr(), m_rows, d, F32,
+                 F32, st)
+            call("sfl_gemm_qkv_rope", act.data_ptr(), self.wqkv[layer].data_ptr(), m_rows, t, d, h,
+                 self.cos_fm.data_ptr(), self.sin_fm.data_ptr(), q.data_ptr(), kc.data_ptr(), vc.data_ptr(),
+                 self.cap, F32, st)
+            causal_prefill(q, kc[:, :, :t], vc[:, :, :t], attn.transpose(1, 2))
+            call("sfl_gemm", attn.data_ptr(), blk.attn.output_proj.weight.data_ptr(), x.data_ptr(), m_rows, d, d,
+                 F32, F32, 1, st)
+            call("sfl_rmsnorm_rows", x.data_ptr(), blk.ffn_norm.weight.data_ptr(), act.data_ptr(), m_rows, d, F32,
+                 F32, st)
+            call("sfl_gemm_swiglu", act.data_ptr(), w13[layer].data_ptr(), hid.data_ptr(), m_rows, f, d, F32, st)
+            call("sfl_gemm", hid.data_ptr(), blk.ffn.w2.weight.data_ptr(), x.data_ptr(), m_rows, d, f, F32, F32, 1,
+                 st)
+        logits = None
+        if all_logits:
+            call("sfl_rmsnorm_rows", x.data_ptr(), self.model.ln_final.weight.data_ptr(), act.data_ptr(), m_rows, d,
+                 F32, F32, st)
+            logits = torch.empty((m_rows, v), device=dev, dtype=torch.float32)
+            call("sfl_gemm", act.data_ptr(), self.model.lm_head.weight.data_ptr(), logits.data_ptr(), m_rows, v, d,
+                 F32, F32, 0, st)
+            logits = logits.view(b, t, v)
+        self.prefill_norm_folded = False
+        self._hand_over(x, b, t, st)
         return logits
 
     def _fold_norm(self, m_rows: int) -> bool:

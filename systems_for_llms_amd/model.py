@@ -7,9 +7,11 @@ loads unchanged. Parameters are initialised as the reference does
 (``layers.py:18-31,59-65,129-131``).
 
 Execution is inference-only and on the GPU: ``forward(input_ids)`` returns the
-logits of every position, computed by the HIP decode-step kernels with a KV
-cache (equal to the reference's full recompute up to float reassociation), and
-``generate`` runs the greedy token loop the reference lacks. There is no CPU
+logits of every position from one prefill pass of MFMA GEMMs and causal
+attention (in the model dtype: bf16, fp16 or fp32; equal to the reference's
+forward up to float reassociation and, for 16-bit models, the rounding of
+what the pass stores), and ``generate`` runs the greedy token loop the
+reference lacks: the prefill, then KV-cached decode steps. There is no CPU
 path: calling the model on CPU tensors raises.
 """
 
@@ -201,8 +203,11 @@ class TransformerLM(nn.Module):
         return self.d_model // self.num_heads
 
     def _gemm_prefill(self) -> bool:
-        """bf16 models whose head dim the MFMA prefill attention supports prefill in one pass."""
-        return self.lm_head.weight.dtype == torch.bfloat16 and self.head_dim in (32, 64, 128)
+        """Models whose head dim the prefill attention supports prefill in one pass (16-bit: the
+        masked MFMA kernel, head dims 32/64/128; float32: the fp32 kernel, 16/32/64/128)."""
+        if self.lm_head.weight.dtype == torch.float32:
+            return self.head_dim in (16, 32, 64, 128)
+        return self.head_dim in (32, 64, 128)
 
     def _check_ids(self, input_ids: torch.Tensor) -> None:
         if input_ids.ndim < 1:
@@ -255,7 +260,7 @@ class TransformerLM(nn.Module):
         if self._gemm_prefill():
             # One pass of MFMA GEMMs and masked attention over the whole prompt.
             session = self.decode_session(ids.shape[0], t, deterministic=self.deterministic)
-            logits = session.prefill(ids, all_logits=True, logits_dtype=torch.bfloat16)
+            logits = session.prefill(ids, all_logits=True, logits_dtype=self.lm_head.weight.dtype)
             return logits.reshape(*lead, t, self.vocab_size)
         session = self.decode_session(ids.shape[0], t, record_logits=True, deterministic=self.deterministic)
         session.start(ids)

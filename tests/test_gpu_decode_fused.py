@@ -147,8 +147,8 @@ def test_attention_out_proj_rejects_unsupported_shapes():
         _lib.call("sfl_decode_attention_out_proj", *args(16, 1))  # bf16 needs D >= 32
     with pytest.raises(RuntimeError, match="head dim"):
         _lib.call("sfl_decode_attention_out_proj", *args(48, 0))
-    with pytest.raises(RuntimeError, match="dtype"):
-        _lib.call("sfl_decode_attention_out_proj", *args(64, 2))
+    with pytest.raises(RuntimeError, match="dtype"):  # an activation-layout code is no model dtype
+        _lib.call("sfl_decode_attention_out_proj", *args(64, _lib.DTYPE_BF16X2))
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])

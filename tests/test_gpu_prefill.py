@@ -1,4 +1,4 @@
-"""GPU parity of the bf16 MFMA prefill path (GEMMs + masked attention) against the oracle."""
+"""GPU parity of the prefill path (MFMA GEMMs + causal attention; bf16, fp16, fp32) against the oracle."""
 
 import pytest
 import torch
@@ -17,23 +17,26 @@ pytestmark = pytest.mark.gpu
 
 # K % 64 == 0 takes the 32x32-MFMA kernel (ragged M and N included: rows past
 # the matrices read as zeros, stores are masked); other K the 16x16 kernel.
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("m,n,k", [(1, 16, 64), (37, 100, 72), (128, 128, 64), (300, 520, 200), (64, 3072, 1024),
                                    (300, 520, 256), (5, 10000, 128), (129, 127, 192), (1000, 36, 2752)])
-def test_gemm_matches_fp32_matmul(m, n, k):
+def test_gemm_matches_fp32_matmul(m, n, k, dtype):
     g = torch.Generator().manual_seed(m + n + k)
-    a = torch.randn((m, k), generator=g).bfloat16()
-    w = torch.randn((n, k), generator=g).bfloat16()
+    a = torch.randn((m, k), generator=g).to(dtype)
+    w = torch.randn((n, k), generator=g).to(dtype)
     ref = a.float() @ w.float().t()
     ga, gw = a.cuda(), w.cuda()  # keep the device copies alive across the launches
     out = torch.zeros((m, n), device="cuda")
     st = _lib.stream_handle()
-    _lib.call("sfl_gemm_bf16", ga.data_ptr(), gw.data_ptr(), out.data_ptr(), m, n, k, 0, 0, st)
+    code = _lib.dtype_code(dtype)
+    _lib.call("sfl_gemm", ga.data_ptr(), gw.data_ptr(), out.data_ptr(), m, n, k, code, 0, 0, st)
     torch.testing.assert_close(out.cpu(), ref, atol=1e-3, rtol=1e-4)
-    _lib.call("sfl_gemm_bf16", ga.data_ptr(), gw.data_ptr(), out.data_ptr(), m, n, k, 0, 1, st)
+    _lib.call("sfl_gemm", ga.data_ptr(), gw.data_ptr(), out.data_ptr(), m, n, k, code, 0, 1, st)
     torch.testing.assert_close(out.cpu(), 2 * ref, atol=2e-3, rtol=1e-4)
-    ob = torch.zeros((m, n), device="cuda", dtype=torch.bfloat16)
-    _lib.call("sfl_gemm_bf16", ga.data_ptr(), gw.data_ptr(), ob.data_ptr(), m, n, k, 1, 0, st)
-    torch.testing.assert_close(ob.float().cpu(), ref.bfloat16().float(), atol=1e-2, rtol=1e-2)
+    ob = torch.zeros((m, n), device="cuda", dtype=dtype)
+    _lib.call("sfl_gemm", ga.data_ptr(), gw.data_ptr(), ob.data_ptr(), m, n, k, code, code, 0, st)
+    # one rounding of the fp32 sums to the output type (bf16: 2^-8, fp16: 2^-11 relative)
+    torch.testing.assert_close(ob.float().cpu(), ref.to(dtype).float(), atol=1e-2, rtol=1e-2)
 
 
 # Grids of >= 320 tiles of 256 x 384 take the 256 x 384 kernel with its ring
@@ -48,7 +51,7 @@ def test_gemm_large_grid_matches_fp32_matmul(m, n, k):
     ref = a[rows].float() @ w.float().t()
     ga, gw = a.cuda(), w.cuda()
     out = torch.zeros((m, n), device="cuda")
-    _lib.call("sfl_gemm_bf16", ga.data_ptr(), gw.data_ptr(), out.data_ptr(), m, n, k, 0, 0, _lib.stream_handle())
+    _lib.call("sfl_gemm", ga.data_ptr(), gw.data_ptr(), out.data_ptr(), m, n, k, 1, 0, 0, _lib.stream_handle())
     torch.testing.assert_close(out[rows.cuda()].cpu(), ref, atol=1e-3 * k ** 0.5, rtol=1e-4)
 
 
@@ -67,7 +70,7 @@ def test_gemm_large_grid_accumulates_into_fp32(m, n, k):
     c = torch.full(((m + 2) * n,), 7.0, device="cuda")
     cv = c[n:n + m * n].view(m, n)  # one guard row before C, one after
     cv.copy_(c0.cuda())
-    _lib.call("sfl_gemm_bf16", ga.data_ptr(), gw.data_ptr(), cv.data_ptr(), m, n, k, 0, 1, _lib.stream_handle())
+    _lib.call("sfl_gemm", ga.data_ptr(), gw.data_ptr(), cv.data_ptr(), m, n, k, 1, 0, 1, _lib.stream_handle())
     torch.cuda.synchronize()
     torch.testing.assert_close(cv[rows.cuda()].cpu(), ref, atol=1e-3 * k ** 0.5, rtol=1e-4)
     assert bool((c[:n] == 7.0).all()) and bool((c[n + m * n:] == 7.0).all()), "wrote outside C"
@@ -77,14 +80,14 @@ def _sample_rows(m, g):
     return torch.cat([torch.arange(0, 40), torch.randint(0, m, (200,), generator=g), torch.arange(m - 40, m)])
 
 
-def _bf16_out(shape, aligned):
-    """A zeroed bf16 output on the GPU; ``aligned=False`` starts it 8 bytes past a
+def _bf16_out(shape, aligned, dtype=torch.bfloat16):
+    """A zeroed 16-bit output on the GPU; ``aligned=False`` starts it 8 bytes past a
     16-byte boundary (the kernels then store 8 bytes per lane instead of 16)."""
     n = 1
     for s in shape:
         n *= s
     off = 0 if aligned else 4
-    buf = torch.zeros(n + off, device="cuda", dtype=torch.bfloat16)
+    buf = torch.zeros(n + off, device="cuda", dtype=dtype)
     out = buf[off:].view(shape)
     assert (out.data_ptr() % 16 == 0) == aligned
     return out
@@ -93,31 +96,34 @@ def _bf16_out(shape, aligned):
 # The bf16 epilogues of the 256 x 384 kernel (q/k/v + RoPE + cache write,
 # SwiGLU, plain bf16 output) with ragged M (token tiles spanning two batch
 # rows), a ragged N, and outputs that are / are not 16-byte aligned.
-@pytest.mark.parametrize("aligned", [True, False])
-def test_gemm_large_grid_bf16_epilogues(aligned):
+@pytest.mark.parametrize("aligned,dtype", [(True, torch.bfloat16), (False, torch.bfloat16), (True, torch.float16)])
+def test_gemm_large_grid_bf16_epilogues(aligned, dtype):
+    """The 16-bit epilogues (q/k/v + RoPE + cache, SwiGLU, plain) on the large-grid kernel, in
+    bf16 (16- and 8-byte stores) and fp16."""
     d, h, f, b, t, cap = 1024, 16, 2752, 4, 3000, 3072
     dk, m = d // h, b * t
     g = torch.Generator().manual_seed(11)
-    a = torch.randn((m, d), generator=g).bfloat16()
-    wqkv = (torch.randn((3 * d, d), generator=g) * 0.03).bfloat16()
-    w1 = (torch.randn((f, d), generator=g) * 0.03).bfloat16()
-    w3 = (torch.randn((f, d), generator=g) * 0.03).bfloat16()
+    a = torch.randn((m, d), generator=g).to(dtype)
+    wqkv = (torch.randn((3 * d, d), generator=g) * 0.03).to(dtype)
+    w1 = (torch.randn((f, d), generator=g) * 0.03).to(dtype)
+    w3 = (torch.randn((f, d), generator=g) * 0.03).to(dtype)
     w13 = torch.stack([w1.view(f // 8, 8, d), w3.view(f // 8, 8, d)], dim=1).reshape(2 * f, d).contiguous()
     cos, sin = om.rope_tables(10000.0, dk, cap)
     ga, gqkv, g13 = a.cuda(), wqkv.cuda(), w13.cuda()
     gcos, gsin = cos.t().contiguous().cuda(), sin.t().contiguous().cuda()  # feature-major
-    q = _bf16_out((b, h, t, dk), aligned)
-    kc, vc = _bf16_out((b, h, cap, dk), aligned), _bf16_out((b, h, cap, dk), aligned)
-    hid = _bf16_out((m, f), aligned)
+    q = _bf16_out((b, h, t, dk), aligned, dtype)
+    kc, vc = _bf16_out((b, h, cap, dk), aligned, dtype), _bf16_out((b, h, cap, dk), aligned, dtype)
+    hid = _bf16_out((m, f), aligned, dtype)
     n_plain = 8200  # 32 x 256 + 8: the last feature block is partial
-    wp = (torch.randn((n_plain, d), generator=g) * 0.03).bfloat16()
+    wp = (torch.randn((n_plain, d), generator=g) * 0.03).to(dtype)
     gwp = wp.cuda()
-    plain = _bf16_out((m, n_plain), aligned)
+    plain = _bf16_out((m, n_plain), aligned, dtype)
     st = _lib.stream_handle()
+    code = _lib.dtype_code(dtype)
     _lib.call("sfl_gemm_qkv_rope", ga.data_ptr(), gqkv.data_ptr(), m, t, d, h, gcos.data_ptr(), gsin.data_ptr(),
-              q.data_ptr(), kc.data_ptr(), vc.data_ptr(), cap, st)
-    _lib.call("sfl_gemm_swiglu", ga.data_ptr(), g13.data_ptr(), hid.data_ptr(), m, f, d, st)
-    _lib.call("sfl_gemm_bf16", ga.data_ptr(), gwp.data_ptr(), plain.data_ptr(), m, n_plain, d, 1, 0, st)
+              q.data_ptr(), kc.data_ptr(), vc.data_ptr(), cap, code, st)
+    _lib.call("sfl_gemm_swiglu", ga.data_ptr(), g13.data_ptr(), hid.data_ptr(), m, f, d, code, st)
+    _lib.call("sfl_gemm", ga.data_ptr(), gwp.data_ptr(), plain.data_ptr(), m, n_plain, d, code, code, 0, st)
     torch.cuda.synchronize()
 
     rows = _sample_rows(m, g)
@@ -131,13 +137,15 @@ def test_gemm_large_grid_bf16_epilogues(aligned):
         out[..., 1::2] = x[..., 0::2] * s + x[..., 1::2] * c
         return out
     qr, kr, vr = (proj[:, i * d:(i + 1) * d].view(-1, h, dk) for i in range(3))
-    _ulp_close("q (RoPE)", q.cpu()[bi, :, ti], om._round(rot(qr), torch.bfloat16), 2e-3)
-    _ulp_close("k cache (RoPE)", kc.cpu()[bi, :, ti], om._round(rot(kr), torch.bfloat16), 2e-3)
-    _ulp_close("v cache", vc.cpu()[bi, :, ti], om._round(vr, torch.bfloat16), 2e-3)
+    # fp16 has 3 more mantissa bits than bf16: its 1-ulp flips from fp32 reassociation are 8x as frequent.
+    ulp, frac = (2 ** -7, 2e-3) if dtype == torch.bfloat16 else (2 ** -10, 1.6e-2)
+    _ulp_close("q (RoPE)", q.cpu()[bi, :, ti], om._round(rot(qr), dtype), frac, ulp=ulp)
+    _ulp_close("k cache (RoPE)", kc.cpu()[bi, :, ti], om._round(rot(kr), dtype), frac, ulp=ulp)
+    _ulp_close("v cache", vc.cpu()[bi, :, ti], om._round(vr, dtype), frac, ulp=ulp)
     assert not kc[:, :, t:].any() and not vc[:, :, t:].any(), "wrote cache rows past the sequence"
     g1, g3 = a[rows].float() @ w1.float().t(), a[rows].float() @ w3.float().t()
-    _ulp_close("SwiGLU hidden", hid.cpu()[rows], om._round(g1 * torch.sigmoid(g1) * g3, torch.bfloat16), 2e-3)
-    _ulp_close("plain bf16", plain.cpu()[rows], om._round(a[rows].float() @ wp.float().t(), torch.bfloat16), 2e-3)
+    _ulp_close("SwiGLU hidden", hid.cpu()[rows], om._round(g1 * torch.sigmoid(g1) * g3, dtype), frac, ulp=ulp)
+    _ulp_close("plain", plain.cpu()[rows], om._round(a[rows].float() @ wp.float().t(), dtype), frac, ulp=ulp)
 
 
 # Head dims that are not multiples of 32: a 32-feature MFMA block then holds
@@ -157,7 +165,7 @@ def test_gemm_qkv_rope_head_dims_across_feature_blocks(dk, h, b, t):
     gcos, gsin = cos.t().contiguous().cuda(), sin.t().contiguous().cuda()  # feature-major
     ga, gw = a.cuda(), wqkv.cuda()
     _lib.call("sfl_gemm_qkv_rope", ga.data_ptr(), gw.data_ptr(), m, t, d, h, gcos.data_ptr(), gsin.data_ptr(),
-              q.data_ptr(), kc.data_ptr(), vc.data_ptr(), cap, _lib.stream_handle())
+              q.data_ptr(), kc.data_ptr(), vc.data_ptr(), cap, 1, _lib.stream_handle())
     torch.cuda.synchronize()
     rows = _sample_rows(m, g) if m > 400 else torch.arange(m)
     bi, ti = rows // t, rows % t
@@ -186,7 +194,7 @@ def test_rmsnorm_rows_matches_reference(m, d, dtype):
     w = (1 + 0.5 * torch.randn(d, generator=g)).to(dtype)
     xd, wd = x.cuda(), w.cuda()
     out = torch.zeros((m + 1, d), device="cuda", dtype=torch.bfloat16)  # one guard row
-    _lib.call("sfl_rmsnorm_rows", xd.data_ptr(), wd.data_ptr(), out.data_ptr(), m, d, _lib.dtype_code(dtype),
+    _lib.call("sfl_rmsnorm_rows", xd.data_ptr(), wd.data_ptr(), out.data_ptr(), m, d, _lib.dtype_code(dtype), 1,
               _lib.stream_handle())
     x64 = x.double()
     ref = (x64 / torch.sqrt(x64.pow(2).mean(-1, keepdim=True) + 1e-5) * w.double()).float()
@@ -235,7 +243,7 @@ def test_gemm_residual_norm_and_norm_scale(m, n, k):
     ga, gw, gg = a.cuda(), w.cuda(), gain.cuda()
     st = _lib.stream_handle()
     _lib.call("sfl_gemm_residual_norm", ga.data_ptr(), gw.data_ptr(), xg[1:].data_ptr(), m, n, k, gg.data_ptr(),
-              act.data_ptr(), ss.data_ptr(), st)
+              act.data_ptr(), ss.data_ptr(), 1, st)
     _lib.call("sfl_norm_scale", ss.data_ptr(), parts, m, n, rsc.data_ptr(), st)
     x1 = xg[1:-1].cpu()
     assert bool(xg[0].isnan().all()) and bool(xg[-1].isnan().all()), "wrote outside x"
@@ -249,8 +257,8 @@ def test_gemm_residual_norm_and_norm_scale(m, n, k):
     assert rsc[m].item() == -1.0
 
 
-def gpu_model(cfg, sd):
-    model = TransformerLM.from_config(cfg, device="cuda", dtype=torch.bfloat16)
+def gpu_model(cfg, sd, dtype=torch.bfloat16):
+    model = TransformerLM.from_config(cfg, device="cuda", dtype=dtype)
     model.load_state_dict(sd)
     return model.eval()
 
@@ -346,7 +354,7 @@ def test_pilot_prefill_with_and_without_folded_norms(fold):
               ref_bf16_weights=rw, unfolded_floor=unfolded)
 
 
-def _ulp_close(name, got, ref, max_frac, cancel=2 ** -17):
+def _ulp_close(name, got, ref, max_frac, cancel=2 ** -17, ulp=2 ** -7):
     """bf16 results that differ only by rare 1-ulp rounding flips.
 
     One ulp of the larger value, plus ``cancel`` times the tensor's largest
@@ -358,11 +366,11 @@ def _ulp_close(name, got, ref, max_frac, cancel=2 ** -17):
     got, ref = got.float().cpu(), ref.float().cpu()
     diff = (got - ref).abs()
     frac = (diff > 0).float().mean().item()
-    bound = 2 ** -7 * torch.maximum(got.abs(), ref.abs()) + cancel * ref.abs().max()
+    bound = ulp * torch.maximum(got.abs(), ref.abs()) + cancel * ref.abs().max()
     worst = (diff - bound).max().item()
     print(f"{name}: {frac:.5f} of values differ, max-abs {diff.max().item():.3e}")
     assert frac <= max_frac, f"{name}: {frac} of values differ"
-    assert worst <= 0, f"{name}: a difference exceeds one bf16 ulp"
+    assert worst <= 0, f"{name}: a difference exceeds one ulp"
 
 
 @pytest.mark.parametrize("config", ["pilot-22m-s256", "scale-100m-s1024", "scale-324m-s4096"])
@@ -391,18 +399,18 @@ def test_prefill_layer_stages_match_the_bf16_format_oracle(config):
     call = _lib.call
     call("sfl_embed_rows", gid.data_ptr(), model.token_embeddings.weight.data_ptr(), x.data_ptr(), m, d, 1, st)
     x0 = x.clone()
-    call("sfl_rmsnorm_rows", x.data_ptr(), blk.attn_norm.weight.data_ptr(), act.data_ptr(), m, d, 1, st)
+    call("sfl_rmsnorm_rows", x.data_ptr(), blk.attn_norm.weight.data_ptr(), act.data_ptr(), m, d, 1, 1, st)
     act1 = act.clone()
     call("sfl_gemm_qkv_rope", act.data_ptr(), session.wqkv[0].data_ptr(), m, t, d, h, session.cos_fm.data_ptr(),
-         session.sin_fm.data_ptr(), q.data_ptr(), kc.data_ptr(), vc.data_ptr(), session.cap, st)
+         session.sin_fm.data_ptr(), q.data_ptr(), kc.data_ptr(), vc.data_ptr(), session.cap, 1, st)
     from systems_for_llms_amd.attention import causal_prefill
     causal_prefill(q, kc[:, :, :t], vc[:, :, :t], attn.transpose(1, 2))
-    call("sfl_gemm_bf16", attn.data_ptr(), blk.attn.output_proj.weight.data_ptr(), x.data_ptr(), m, d, d, 0, 1, st)
+    call("sfl_gemm", attn.data_ptr(), blk.attn.output_proj.weight.data_ptr(), x.data_ptr(), m, d, d, 1, 0, 1, st)
     x1 = x.clone()
-    call("sfl_rmsnorm_rows", x.data_ptr(), blk.ffn_norm.weight.data_ptr(), act.data_ptr(), m, d, 1, st)
+    call("sfl_rmsnorm_rows", x.data_ptr(), blk.ffn_norm.weight.data_ptr(), act.data_ptr(), m, d, 1, 1, st)
     act2 = act.clone()
-    call("sfl_gemm_swiglu", act.data_ptr(), session.weights.w13()[0].data_ptr(), hid.data_ptr(), m, f, d, st)
-    call("sfl_gemm_bf16", hid.data_ptr(), blk.ffn.w2.weight.data_ptr(), x.data_ptr(), m, d, f, 0, 1, st)
+    call("sfl_gemm_swiglu", act.data_ptr(), session.weights.w13()[0].data_ptr(), hid.data_ptr(), m, f, d, 1, st)
+    call("sfl_gemm", hid.data_ptr(), blk.ffn.w2.weight.data_ptr(), x.data_ptr(), m, d, f, 1, 0, 1, st)
     torch.cuda.synchronize()
 
     torch.set_num_threads(16)
@@ -474,15 +482,15 @@ def test_prefill_folded_norm_stages_match_the_bf16_format_oracle(config):
         args = (session.wqkv[layer].data_ptr(),) + ((scale.data_ptr(),) if scale is not None else ())
         call("sfl_gemm_qkv_rope_scaled" if scale is not None else "sfl_gemm_qkv_rope", act.data_ptr(), *args, m, t,
              d, h, session.cos_fm.data_ptr(), session.sin_fm.data_ptr(), q.data_ptr(), kc.data_ptr(), vc.data_ptr(),
-             session.cap, st)
+             session.cap, 1, st)
         return q.clone(), kc[:, :, :t].clone(), vc[:, :, :t].clone()
 
     def swiglu(layer, scale):
         if scale is None:
-            call("sfl_gemm_swiglu", act.data_ptr(), w13[layer].data_ptr(), hid.data_ptr(), m, f, d, st)
+            call("sfl_gemm_swiglu", act.data_ptr(), w13[layer].data_ptr(), hid.data_ptr(), m, f, d, 1, st)
         else:
             call("sfl_gemm_swiglu_scaled", act.data_ptr(), w13[layer].data_ptr(), scale.data_ptr(), hid.data_ptr(), m,
-                 f, d, st)
+                 f, d, 1, st)
         return hid.clone()
 
     # The prefill's own launch sequence (engine.DecodeSession.prefill with folded norms), every
@@ -504,7 +512,7 @@ def test_prefill_folded_norm_stages_match_the_bf16_format_oracle(config):
         causal_prefill(q, kc[:, :, :t], vc[:, :, :t], attn.transpose(1, 2))
         rec["attn"] = attn.clone()
         call("sfl_gemm_residual_norm", attn.data_ptr(), blk.attn.output_proj.weight.data_ptr(), x.data_ptr(), m, d,
-             d, blk.ffn_norm.weight.data_ptr(), act.data_ptr(), ss.data_ptr(), st)
+             d, blk.ffn_norm.weight.data_ptr(), act.data_ptr(), ss.data_ptr(), 1, st)
         rec["x1"], rec["act2"], rec["ss2"] = x.clone(), act.clone(), ss.clone()
         call("sfl_norm_scale", ss.data_ptr(), parts, m, d, rsc.data_ptr(), st)
         rec["r2"] = rsc.clone()
@@ -513,10 +521,10 @@ def test_prefill_folded_norm_stages_match_the_bf16_format_oracle(config):
         rec["hid"] = swiglu(layer, rsc)
         if layer + 1 < nl:
             call("sfl_gemm_residual_norm", hid.data_ptr(), blk.ffn.w2.weight.data_ptr(), x.data_ptr(), m, d, f,
-                 model.layers[layer + 1].attn_norm.weight.data_ptr(), act.data_ptr(), ss.data_ptr(), st)
+                 model.layers[layer + 1].attn_norm.weight.data_ptr(), act.data_ptr(), ss.data_ptr(), 1, st)
             call("sfl_norm_scale", ss.data_ptr(), parts, m, d, rsc.data_ptr(), st)
         else:  # the last layer's w2 only adds into x (the final norm is a separate pass)
-            call("sfl_gemm_bf16", hid.data_ptr(), blk.ffn.w2.weight.data_ptr(), x.data_ptr(), m, d, f, 0, 1, st)
+            call("sfl_gemm", hid.data_ptr(), blk.ffn.w2.weight.data_ptr(), x.data_ptr(), m, d, f, 1, 0, 1, st)
         torch.cuda.synchronize()
         recs.append({k: v.cpu() for k, v in rec.items()})
     x_end = x.cpu()
@@ -603,3 +611,92 @@ def test_generate_bf16_uses_prefill_and_matches_step_path():
     agree = (ref[:, 39:-1].argmax(-1) == ids[:, 40:].cpu()).float().mean().item()
     print("generate agreement with fp32 oracle (teacher-forced)", agree)
     assert agree >= 0.95
+
+
+# ---- float32 prefill (fp32 MFMA GEMMs, fp32 causal attention) ----------------------------
+
+@pytest.mark.parametrize("m,n,k", [(1, 16, 64), (37, 100, 72), (300, 520, 200), (129, 127, 4), (64, 10000, 512)])
+def test_gemm_f32_matches_fp64_matmul(m, n, k):
+    """sfl_gemm on fp32 operands: fp32 products and sums (v_mfma_f32_32x32x2_f32), ragged M, N and K,
+    stored and accumulated, against a float64 product rounded to fp32."""
+    g = torch.Generator().manual_seed(m * 7 + n + k)
+    a = torch.randn((m, k), generator=g)
+    w = torch.randn((n, k), generator=g)
+    ref = (a.double() @ w.double().t()).float()
+    ga, gw = a.cuda(), w.cuda()
+    out = torch.full((m, n), float("nan"), device="cuda")
+    st = _lib.stream_handle()
+    _lib.call("sfl_gemm", ga.data_ptr(), gw.data_ptr(), out.data_ptr(), m, n, k, 0, 0, 0, st)
+    tol = 2e-6 * k ** 0.5
+    torch.testing.assert_close(out.cpu(), ref, atol=tol, rtol=1e-5)
+    _lib.call("sfl_gemm", ga.data_ptr(), gw.data_ptr(), out.data_ptr(), m, n, k, 0, 0, 1, st)
+    torch.testing.assert_close(out.cpu(), 2 * ref, atol=2 * tol, rtol=1e-5)
+
+
+def test_f32_prefill_stages_match_the_oracle():
+    """The fp32 q/k/v (+ RoPE + cache), SwiGLU and causal attention stages of a float32 prefill on
+    the GPU's own inputs, against the oracle's restatement in float64."""
+    b, t, h, dk, f, cap = 3, 150, 4, 32, 320, 160
+    d, m = h * dk, b * t
+    g = torch.Generator().manual_seed(5)
+    a = torch.randn((m, d), generator=g)
+    wqkv = torch.randn((3 * d, d), generator=g) * 0.05
+    w1, w3 = (torch.randn((f, d), generator=g) * 0.05 for _ in range(2))
+    w13 = torch.stack([w1.view(f // 8, 8, d), w3.view(f // 8, 8, d)], dim=1).reshape(2 * f, d).contiguous()
+    cos, sin = om.rope_tables(10000.0, dk, cap)
+    ga, gqkv, g13 = a.cuda(), wqkv.cuda(), w13.cuda()
+    gcos, gsin = cos.t().contiguous().cuda(), sin.t().contiguous().cuda()
+    q = torch.zeros((b, h, t, dk), device="cuda")
+    kc, vc = torch.zeros((b, h, cap, dk), device="cuda"), torch.zeros((b, h, cap, dk), device="cuda")
+    hid = torch.zeros((m, f), device="cuda")
+    attn = torch.zeros((b, t, h, dk), device="cuda")
+    st = _lib.stream_handle()
+    _lib.call("sfl_gemm_qkv_rope", ga.data_ptr(), gqkv.data_ptr(), m, t, d, h, gcos.data_ptr(), gsin.data_ptr(),
+              q.data_ptr(), kc.data_ptr(), vc.data_ptr(), cap, 0, st)
+    _lib.call("sfl_gemm_swiglu", ga.data_ptr(), g13.data_ptr(), hid.data_ptr(), m, f, d, 0, st)
+    from systems_for_llms_amd.attention import causal_prefill
+    causal_prefill(q, kc[:, :, :t], vc[:, :, :t], attn.transpose(1, 2))
+    torch.cuda.synchronize()
+
+    a64 = a.double().view(b, t, d)
+    proj = a64 @ wqkv.double().t()
+    pos = torch.arange(t)
+    qr, kr, vr = (om._split_heads(proj[..., i * d:(i + 1) * d], h) for i in range(3))
+    torch.testing.assert_close(q.cpu(), om.rope(qr, cos.double(), sin.double(), pos).float(), atol=1e-5, rtol=1e-5)
+    torch.testing.assert_close(kc[:, :, :t].cpu(), om.rope(kr, cos.double(), sin.double(), pos).float(), atol=1e-5,
+                               rtol=1e-5)
+    torch.testing.assert_close(vc[:, :, :t].cpu(), vr.float(), atol=1e-5, rtol=1e-5)
+    assert not kc[:, :, t:].any() and not vc[:, :, t:].any(), "wrote cache rows past the sequence"
+    g1, g3 = a.double() @ w1.double().t(), a.double() @ w3.double().t()
+    torch.testing.assert_close(hid.cpu(), (g1 * torch.sigmoid(g1) * g3).float(), atol=1e-5, rtol=1e-5)
+    qg, kg, vg = q.cpu().double(), kc[:, :, :t].cpu().double(), vc[:, :, :t].cpu().double()
+    mask = torch.tril(torch.ones(t, t, dtype=torch.bool))
+    ref = om._merge_heads(om.attention_core(qg, kg, vg, mask)).float()
+    torch.testing.assert_close(attn.cpu().view(b, t, d), ref, atol=1e-5, rtol=1e-5)
+
+
+def test_f32_forward_is_one_prefill_pass_equal_to_the_oracle():
+    """A float32 forward() of the config-1 dims (head dim 32) over 200 positions is one prefill pass
+    (no per-position decode steps): its logits equal the oracle's fp32 forward, and the decode steps
+    that continue from it give the same logits as the step path from position 0."""
+    cfg = load_model_config("pilot-22m-s256")
+    sd = seeded_state_dict(cfg, 91)
+    model = gpu_model(cfg, sd, torch.float32)
+    assert model._gemm_prefill()
+    ids = seeded_prompt(cfg.vocab_size, 2, 200, 92)
+    logits = model(ids.cuda()).cpu()
+    assert model._sfl_session.logits is None  # the prefill path records no per-step logits
+    ref = om.forward(sd, cfg, ids)
+    err = (logits - ref).abs().max().item()
+    print(f"fp32 prefill forward vs oracle max-abs {err:.2e}")
+    torch.testing.assert_close(logits, ref, atol=2e-5, rtol=1e-4)
+    # Decode after the prefill (positions 200..239) against the step path from position 0.
+    seq = seeded_prompt(cfg.vocab_size, 2, 240, 93)
+    a = DecodeSession(model, 2, 240, record_logits=True)
+    a.prefill(seq[:, :200].cuda(), forced=seq.cuda())
+    a.run(39, use_graph=True)
+    b = DecodeSession(model, 2, 240, record_logits=True)
+    b.start(seq.cuda())
+    b.run(239, use_graph=True)
+    torch.cuda.synchronize()
+    torch.testing.assert_close(a.logits[:, 200:239].cpu(), b.logits[:, 200:239].cpu(), atol=2e-5, rtol=1e-4)
