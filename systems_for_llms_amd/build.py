@@ -33,6 +33,16 @@ HIP_FLAGS = [
 ]
 
 
+# Per-file additions. decode_linear.hip: kernel-argument preloading (gfx940+):
+# the command processor loads the first 14 argument dwords into SGPRs before
+# the waves start, which the GEMV kernels use for the pointers and sizes their
+# first loads need. The code object keeps a prologue that fetches them itself
+# for firmware without preloading.
+FILE_FLAGS = {
+    "decode_linear.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=14"],
+}
+
+
 def hipcc() -> str:
     for candidate in (shutil.which("hipcc"), "/opt/rocm/bin/hipcc"):
         if candidate and Path(candidate).exists():
@@ -42,7 +52,7 @@ def hipcc() -> str:
 
 def _compile(source: Path, verbose: bool) -> Path:
     obj = BUILD_DIR / (source.stem + ".o")
-    cmd = [hipcc(), *HIP_FLAGS, "-c", str(source), "-o", str(obj)]
+    cmd = [hipcc(), *HIP_FLAGS, *FILE_FLAGS.get(source.name, []), "-c", str(source), "-o", str(obj)]
     result = subprocess.run(cmd, capture_output=True, text=True)
     noise = "is not a recognized feature for this target"
     err = "\n".join(line for line in result.stderr.splitlines() if noise not in line)

@@ -100,15 +100,60 @@ __device__ __forceinline__ uint4 load16_stream(const void* p) {
   return make_uint4(r.x, r.y, r.z, r.w);
 }
 
+// The 32-bit value of lane (lane ^ M), exchanged on the VALU rather than
+// through an LDS permute (ds_bpermute, which __shfl_xor compiles to, adds an
+// LDS round trip per exchange): DPP inside each row of 16 lanes --
+// quad_perm [1,0,3,2] and [2,3,0,1] for M = 1, 2, row_shl:4 / row_shr:4 picked
+// per lane for M = 4, row_ror:8 for M = 8 -- and the gfx950 lane swaps across
+// rows: v_permlane16_swap / v_permlane32_swap of a value with itself leave the
+// even row's (lower half's) value in the first result and the odd row's (upper
+// half's) in the second, so a lane takes the one that is not its own. Every
+// lane of the wave must be active.
+template <int M>
+__device__ __forceinline__ uint32_t lane_xor_bits(uint32_t x) {
+  static_assert(M == 1 || M == 2 || M == 4 || M == 8 || M == 16 || M == 32, "lane mask");
+  if constexpr (M == 1) {
+    return __builtin_amdgcn_update_dpp(0, int(x), 0xB1, 0xF, 0xF, true);
+  } else if constexpr (M == 2) {
+    return __builtin_amdgcn_update_dpp(0, int(x), 0x4E, 0xF, 0xF, true);
+  } else if constexpr (M == 4) {
+    const uint32_t up = __builtin_amdgcn_update_dpp(0, int(x), 0x104, 0xF, 0xF, true);  // lane + 4
+    const uint32_t dn = __builtin_amdgcn_update_dpp(0, int(x), 0x114, 0xF, 0xF, true);  // lane - 4
+    return (__lane_id() & 4) ? dn : up;
+  } else if constexpr (M == 8) {
+    return __builtin_amdgcn_update_dpp(0, int(x), 0x128, 0xF, 0xF, true);
+  } else if constexpr (M == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+    return (__lane_id() & 16) ? r[0] : r[1];
+  } else {
+    const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+    return (__lane_id() & 32) ? r[0] : r[1];
+  }
+}
+
+// lane_xor_bits for a mask known after unrolling (a constant-folded switch).
+__device__ __forceinline__ uint32_t lane_xor_bits(uint32_t x, int m) {
+  switch (m) {
+    case 1: return lane_xor_bits<1>(x);
+    case 2: return lane_xor_bits<2>(x);
+    case 4: return lane_xor_bits<4>(x);
+    case 8: return lane_xor_bits<8>(x);
+    case 16: return lane_xor_bits<16>(x);
+    default: return lane_xor_bits<32>(x);
+  }
+}
+__device__ __forceinline__ float lane_xor(float v, int m) { return __uint_as_float(lane_xor_bits(__float_as_uint(v), m)); }
+__device__ __forceinline__ int lane_xor(int v, int m) { return int(lane_xor_bits(uint32_t(v), m)); }
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, kWave));
+  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, lane_xor(v, m));
   return v;
 }
 
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
+  for (int m = 32; m >= 1; m >>= 1) v += lane_xor(v, m);
   return v;
 }
 
@@ -116,7 +161,7 @@ __device__ __forceinline__ float wave_sum(float v) {
 template <int Width>
 __device__ __forceinline__ float group_sum(float v) {
 #pragma unroll
-  for (int m = Width / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
+  for (int m = Width / 2; m >= 1; m >>= 1) v += lane_xor(v, m);
   return v;
 }
 

@@ -275,8 +275,8 @@ __global__ __launch_bounds__(W * kWave) void decode_attn_kernel(
   for (int mask = LPT; mask < kWave; mask <<= 1) {
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      const float om = __shfl_xor(m[g], mask, kWave);
-      const float ol = __shfl_xor(l[g], mask, kWave);
+      const float om = lane_xor(m[g], mask);
+      const float ol = lane_xor(l[g], mask);
       const float mn = fmaxf(m[g], om);
       const float ms = mn == -INFINITY ? 0.f : mn;
       const float a = exp2f(m[g] - ms);
@@ -284,7 +284,7 @@ __global__ __launch_bounds__(W * kWave) void decode_attn_kernel(
       l[g] = l[g] * a + ol * c;
 #pragma unroll
       for (int e = 0; e < EPL; ++e) {
-        const float oa = __shfl_xor(acc[g][e], mask, kWave);
+        const float oa = lane_xor(acc[g][e], mask);
         acc[g][e] = acc[g][e] * a + oa * c;
       }
       m[g] = mn;
@@ -360,8 +360,8 @@ __global__ __launch_bounds__(W * kWave) void decode_attn_kernel(
 #pragma unroll
           for (int e = 0; e < EW; ++e) part = fmaf(wv[e], op[e], part);
           if (u % P::NCK == P::NCK - 1) {
-            part += __shfl_xor(part, 16, kWave);
-            part += __shfl_xor(part, 32, kWave);
+            part += lane_xor(part, 16);
+            part += lane_xor(part, 32);
             const int tile = wave + (u / P::NCK) * W;
             if (lane < 16) unsafeAtomicAdd(xb + tile * 16 + lane, part);
             part = 0.f;
@@ -449,7 +449,7 @@ __global__ __launch_bounds__(256) void decode_merge_kernel(
     for (int i = 0; i < DPL; ++i) num[i] *= keep;
 #pragma unroll
     for (int j = 0; j < kRound; ++j) {
-      const float wj = __shfl(w, j, kWave);
+      const float wj = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(w), j));  // lane j's weight
 #pragma unroll
       for (int i = 0; i < DPL; ++i) num[i] = fmaf(wj, part[j][i], num[i]);
     }
@@ -512,7 +512,7 @@ __device__ __forceinline__ void gqa32_tile(const uint4 (&kt)[kGqaTile][D / 8], c
   float mx = fmaxf(s[0], s[1]);
 #pragma unroll
   for (int j = 2; j < 16; j += 2) mx = fmaxf(fmaxf(mx, s[j]), s[j + 1]);
-  mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+  mx = fmaxf(mx, lane_xor(mx, 32));
   // Lazy maximum (as in the prefill tile): m_run moves only when a head's
   // tile maximum exceeds it by more than kLazyMax, so probabilities stay
   // below 2^kLazyMax and O is rescaled only on those tiles.
@@ -647,7 +647,7 @@ __global__ __launch_bounds__(kGqaWaves * kWave) void decode_gqa32_kernel(
     t0 = tn;
   }
 
-  const float l_tot = l_run + __shfl_xor(l_run, 32, kWave);
+  const float l_tot = l_run + lane_xor(l_run, 32);
   __syncthreads();  // every wave is done with the tile buffers the merge rows reuse
   if (c < G) {
 #pragma unroll

@@ -264,8 +264,27 @@ template <typename T> struct SrcOf<true, T> { using type = NormChunk<T>; };
 // With several, the blocks of one item go to workgroups w = 8 (g * blocks +
 // blk) + x for item 8 g + x: the same XCD (w % 8 == x), so the item's weights
 // come from HBM once and from that XCD's L2 for the other blocks.
+// The arguments every workgroup needs before its first load come first, as
+// scalars: the library builds this file with kernarg preloading, so the
+// command processor places these 14 dwords in SGPRs before the waves start
+// and the loads issue without waiting for a kernel-argument fetch (one such
+// round trip per launch measured 17 us per 324M decode step). `aux` is the
+// epilogue's first pointer: pos (QKV, LOGITS), x (RESIDUAL) or h_out (SWIGLU).
+// The rest of LinearArgs is read from the kernel arguments as usual.
 template <typename T, int E, int CPW, bool kBlocks>
-__global__ __launch_bounds__(kWaves * kWave) void linear_kernel(LinearArgs a) {
+__global__ __launch_bounds__(kWaves * kWave) void linear_kernel(const void* p_w, const void* p_src,
+                                                                const void* p_gain, const void* p_w3, void* p_aux,
+                                                                int p_batch, int p_n, int p_k, int p_ksplit,
+                                                                LinearArgs a) {
+  a.w = p_w; a.w3 = p_w3; a.gain = p_gain; a.batch = p_batch; a.n = p_n; a.k = p_k; a.ksplit = p_ksplit;
+  if constexpr (E == EPI_RESIDUAL) {
+    a.act = p_src;
+    a.x = static_cast<float*>(p_aux);
+  } else {
+    a.x_in = static_cast<const float*>(p_src);
+    if constexpr (E == EPI_SWIGLU) a.h_out = p_aux;
+    else a.pos = static_cast<const int32_t*>(p_aux);
+  }
   constexpr int KC = chunk_k<T>();
   constexpr int EPL = vec_elems<T>();
   constexpr bool kTwo = (E == EPI_SWIGLU);
@@ -435,8 +454,8 @@ __global__ __launch_bounds__(kWaves * kWave) void linear_kernel(LinearArgs a) {
   }
   if constexpr (kNorm) {
     // Lane (row b, group g) holds group g's sum over all of K: add the 4 groups.
-    sq += __shfl_xor(sq, 16, kWave);
-    sq += __shfl_xor(sq, 32, kWave);
+    sq += lane_xor(sq, 16);
+    sq += lane_xor(sq, 32);
     const float inv = 1.f / sqrtf(sq / float(K) + kEps);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -455,8 +474,8 @@ __global__ __launch_bounds__(kWaves * kWave) void linear_kernel(LinearArgs a) {
     }
 #pragma unroll
     for (int m = 16; m < kWave; m <<= 1) {
-      const float ov = __shfl_xor(bv, m, kWave);
-      const int oi = __shfl_xor(bi, m, kWave);
+      const float ov = lane_xor(bv, m);
+      const int oi = lane_xor(bi, m);
       if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
     }
     if (live) {
@@ -510,14 +529,18 @@ template <typename T, int E, int CPW>
 int launch_linear_cpw(const LinearArgs& a, hipStream_t stream, const char* what) {
   const long items = long((a.n + kTileN - 1) / kTileN) * a.ksplit;
   const long blocks = (a.batch + kBlockRows - 1) / kBlockRows;
+  const void* src = E == EPI_RESIDUAL ? a.act : static_cast<const void*>(a.x_in);
+  void* aux = E == EPI_RESIDUAL ? static_cast<void*>(a.x)
+              : E == EPI_SWIGLU ? a.h_out
+                                : const_cast<int32_t*>(a.pos);
   if (blocks == 1) {
     hipLaunchKernelGGL((linear_kernel<T, E, CPW, false>), dim3(unsigned(items)), dim3(kWaves * kWave), 0,
-                       stream, a);
+                       stream, a.w, src, a.gain, a.w3, aux, a.batch, a.n, a.k, a.ksplit, a);
   } else {
     const long grid = (items + kXcds - 1) / kXcds * kXcds * blocks;
     if (grid > (1L << 31) - 1) return set_error(SFL_ERR_UNSUPPORTED, "%s: too many workgroups", what);
     hipLaunchKernelGGL((linear_kernel<T, E, CPW, true>), dim3(unsigned(grid)), dim3(kWaves * kWave), 0,
-                       stream, a);
+                       stream, a.w, src, a.gain, a.w3, aux, a.batch, a.n, a.k, a.ksplit, a);
   }
   return check_launch(what);
 }

@@ -62,8 +62,8 @@ __global__ __launch_bounds__(64) void next_token_kernel(
   }
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) {
-    const float ov = __shfl_xor(bv, m, kWave);
-    const int oi = __shfl_xor(bi, m, kWave);
+    const float ov = lane_xor(bv, m);
+    const int oi = lane_xor(bi, m);
     if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
   }
   if (np >= cap) return;  // context full: the host never steps past capacity

@@ -188,7 +188,7 @@ __device__ __forceinline__ void store_tile(const GemmArgs& g, const f32x4& v, in
     // matching W3 features: lane groups 0,1 pair with groups 2,3.
     float c3[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) c3[e] = __shfl_xor(y[e], 32, kWave);
+    for (int e = 0; e < 4; ++e) c3[e] = lane_xor(y[e], 32);
     if (grp >= 2 || m >= g.m) return;
     const int f = nt / 2 + 4 * grp;  // hidden feature index
     if (f >= g.n / 2) return;
@@ -567,7 +567,7 @@ void gemm32_kernel(GemmArgs g) {
         __syncthreads();  // every wave has read the last stage
 #pragma unroll
         for (int j = 0; j < NBM; ++j) {
-          const float t = ssq[j] + __shfl_xor(ssq[j], 32, kWave);
+          const float t = ssq[j] + lane_xor(ssq[j], 32);
           if (hf == 0) part_s[wn * TBM + (TBM / WM) * wm + 32 * j + l32] = t;
         }
         __syncthreads();

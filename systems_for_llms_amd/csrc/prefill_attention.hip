@@ -308,8 +308,8 @@ __global__ __launch_bounds__(kThreads) void masked_attention_kernel(AttnArgs a) 
     float mx = sv[0];
 #pragma unroll
     for (int e = 1; e < 16; ++e) mx = fmaxf(mx, sv[e]);
-    mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+    mx = fmaxf(mx, lane_xor(mx, 16));
+    mx = fmaxf(mx, lane_xor(mx, 32));
     // The softmax of the other kernels of this file: a lazy running maximum
     // (it moves only when a tile's maximum exceeds it by more than kLazyMax
     // log2 units), p = 2^(s * c - m) with one FMA, p stored in T for the P V
@@ -335,8 +335,8 @@ __global__ __launch_bounds__(kThreads) void masked_attention_kernel(AttnArgs a) 
       pk[e] = pack2<T>(exp2f(fmaf(sv[2 * e], cs, -m_sub)), exp2f(fmaf(sv[2 * e + 1], cs, -m_sub)));
       psum = add_pair<T>(pk[e], psum);
     }
-    psum += __shfl_xor(psum, 16, kWave);
-    psum += __shfl_xor(psum, 32, kWave);
+    psum += lane_xor(psum, 16);
+    psum += lane_xor(psum, 32);
     l_run = l_run * alpha + psum;
 
     // O^T += V^T P^T. Step s covers subtiles 2s and 2s+1; element e of the
@@ -433,8 +433,8 @@ __device__ __forceinline__ void tile_math(const AttnArgs& a, const u32x4 (&kc)[4
 #pragma unroll
     for (int e = 3; e < 15; e += 2) mx = fmaxf(fmaxf(mx, sv[e]), sv[e + 1]);
     mx = fmaxf(mx, sv[15]);
-    mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+    mx = fmaxf(mx, lane_xor(mx, 16));
+    mx = fmaxf(mx, lane_xor(mx, 32));
     // The lazy maximum and stored-probability row sums of masked_attention32_kernel:
     // m_run (the subtracted maximum) moves only when the tile's maximum exceeds
     // it by more than kLazyMax log2 units, and l sums the T-rounded probabilities
@@ -452,8 +452,8 @@ __device__ __forceinline__ void tile_math(const AttnArgs& a, const u32x4 (&kc)[4
                        __builtin_amdgcn_exp2f(fmaf(sv[2 * e + 1], c, -ms)));
       psum = add_pair<T>(pk[e], psum);
     }
-    psum += __shfl_xor(psum, 16, kWave);
-    psum += __shfl_xor(psum, 32, kWave);
+    psum += lane_xor(psum, 16);
+    psum += lane_xor(psum, 32);
     l_run[qs] = l_run[qs] * alpha + psum;
     if (__ballot(alpha != 1.f)) {  // wave-uniform: skip the rescale while no maximum moves
 #pragma unroll

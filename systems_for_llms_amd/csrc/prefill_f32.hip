@@ -218,8 +218,8 @@ __global__ __launch_bounds__(kF32Threads) void causal_attention_f32_kernel(F32At
       float s = 0.f;
 #pragma unroll
       for (int d = 0; d < DQ; ++d) s = fmaf(qv[d], kt[j][part * DQ + d], s);
-      s += __shfl_xor(s, 1, kWave);
-      s += __shfl_xor(s, 2, kWave);
+      s += lane_xor(s, 1);
+      s += lane_xor(s, 2);
       if (k0 + j <= qrow) {  // causal (attention.py:187-197)
         if (s > m_run) {
           const float alpha = exp2f(m_run - s);  // 0 for the first key
