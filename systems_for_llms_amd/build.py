@@ -33,13 +33,16 @@ HIP_FLAGS = [
 ]
 
 
-# Per-file additions. decode_linear.hip: kernel-argument preloading (gfx940+):
-# the command processor loads the first 14 argument dwords into SGPRs before
-# the waves start, which the GEMV kernels use for the pointers and sizes their
-# first loads need. The code object keeps a prologue that fetches them itself
-# for firmware without preloading.
+# Per-file additions. Kernel-argument preloading (gfx940+) for the decode-step
+# kernels: the command processor loads the first 14 argument dwords into SGPRs
+# before the waves start, and those kernels put the pointers and sizes their
+# first loads need there. The code object keeps a prologue that fetches them
+# itself for firmware without preloading.
+_PRELOAD = ["-mllvm", "-amdgpu-kernarg-preload-count=14"]
 FILE_FLAGS = {
-    "decode_linear.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=14"],
+    "decode_linear.hip": _PRELOAD,
+    "decode_attention.hip": _PRELOAD,
+    "decode_step.hip": _PRELOAD,
 }
 
 

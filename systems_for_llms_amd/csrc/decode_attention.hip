@@ -86,12 +86,17 @@ __device__ __forceinline__ uint4 load_proj_unit(const unsigned char* w_lane, int
 // wave states are merged through LDS. With one split the workgroup writes the final
 // output (or, fused, adds its heads' share of the output projection to x);
 // otherwise it writes its (max, sum, numerator) partial for the merge kernel.
+// The arguments the prologue and the first loads need come first (14 dwords):
+// this file is built with kernel-argument preloading, so they arrive in SGPRs
+// with the wave. The index math is 32-bit, and the fused projection (always
+// one split) skips the division by the split count: a launch's first
+// instructions are fetched cold, so each one ahead of the first load counts.
 template <typename T, typename TQ, typename TO, int D, int G, int W>
 __global__ __launch_bounds__(W * kWave) void decode_attn_kernel(
     const TQ* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
-    const int32_t* __restrict__ lengths, float* __restrict__ pmax, float* __restrict__ psum,
-    float* __restrict__ pout, void* __restrict__ out, int kv_heads, int cap, int splits, int chunk,
-    float qscale, float* __restrict__ x, int d_model) {
+    const int32_t* __restrict__ lengths, int kv_heads, int cap, int splits, int chunk, float qscale,
+    int d_model, float* __restrict__ pmax, float* __restrict__ psum, float* __restrict__ pout,
+    void* __restrict__ out, float* __restrict__ x) {
   constexpr bool kProj = std::is_same<TO, resid_t>::value;
   using S = DecodeShape<T, D, G, kProj>;
   constexpr int EPL = S::EPL, LPT = S::LPT, TPL = S::TPL, NL = S::NL, TILE = S::TILE;
@@ -99,10 +104,10 @@ __global__ __launch_bounds__(W * kWave) void decode_attn_kernel(
   __shared__ float os[kProj ? G * D : 1];
   const int wave = threadIdx.x / kWave;
   const int lane = threadIdx.x % kWave;
-  const int split = int(blockIdx.x % splits);
-  const long bh = blockIdx.x / splits;
-  const int h = int(bh % kv_heads);
-  const int b = int(bh / kv_heads);
+  const unsigned bh = kProj ? blockIdx.x : blockIdx.x / unsigned(splits);
+  const int split = kProj ? 0 : int(blockIdx.x - bh * unsigned(splits));
+  const int b = int(bh / unsigned(kv_heads));
+  const int h = int(bh - unsigned(b) * unsigned(kv_heads));
   const int q_heads = kv_heads * G;
   const int slot = lane / LPT;
   const int dg = lane % LPT;
@@ -557,12 +562,12 @@ __device__ __forceinline__ void gqa32_tile(const uint4 (&kt)[kGqaTile][D / 8], c
 // One workgroup of 4 waves per (batch, kv head, split), grid order as
 // decode_attn_kernel. The host admits 16-byte aligned q/k/v and caches of
 // cap * D * 2 < 2^31 bytes per head (32-bit buffer offsets).
+// Arguments ordered as decode_attn_kernel's: the prologue's in the preloaded 13 dwords.
 template <typename T, typename TO, int D, int G>
 __global__ __launch_bounds__(kGqaWaves * kWave) void decode_gqa32_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
-    const int32_t* __restrict__ lengths, float* __restrict__ pmax, float* __restrict__ psum,
-    float* __restrict__ pout, void* __restrict__ out, int kv_heads, int cap, int splits, int chunk,
-    float cs) {
+    const int32_t* __restrict__ lengths, int kv_heads, int cap, int splits, int chunk, float cs,
+    float* __restrict__ pmax, float* __restrict__ psum, float* __restrict__ pout, void* __restrict__ out) {
   constexpr int W = kGqaWaves, BT = kGqaTile;
   constexpr int SL = D / 8;        // 16-byte slots per key row
   constexpr int RPL = kWave / SL;  // key rows one 1 KB DMA load moves
@@ -575,9 +580,10 @@ __global__ __launch_bounds__(kGqaWaves * kWave) void decode_gqa32_kernel(
   const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x) / kWave);
   const int lane = threadIdx.x % kWave;
   const int c = lane % 32, h = lane / 32;
-  const int split = int(blockIdx.x % splits);
-  const long bh = blockIdx.x / splits;
-  const int hk = int(bh % kv_heads), b = int(bh / kv_heads);
+  const unsigned bh = blockIdx.x / unsigned(splits);
+  const int split = int(blockIdx.x - bh * unsigned(splits));
+  const int b = int(bh / unsigned(kv_heads));
+  const int hk = int(bh - unsigned(b) * unsigned(kv_heads));
   const int q_heads = kv_heads * G;
 
   // Q^T operand of k-step ks: head c's dims (D/2) h + 8 ks .. +7; zero past G.
@@ -729,8 +735,8 @@ int launch_attn(const DecodeCall& c) {
       const long groups = long(c.batch) * c.kv_heads * c.splits;
       hipLaunchKernelGGL((decode_gqa32_kernel<T, TO, D, G>), dim3(unsigned(groups)), dim3(kGqaWaves * kWave), 0,
                          c.stream, static_cast<const T*>(c.q), static_cast<const T*>(c.k),
-                         static_cast<const T*>(c.v), c.lengths, c.pmax, c.psum, c.pout, c.out, c.kv_heads,
-                         c.cap, c.splits, chunk, c.scale * kLog2e);
+                         static_cast<const T*>(c.v), c.lengths, c.kv_heads, c.cap, c.splits, chunk,
+                         c.scale * kLog2e, c.pmax, c.psum, c.pout, c.out);
       return check_launch("decode_attention");
     }
   }
@@ -739,8 +745,8 @@ int launch_attn(const DecodeCall& c) {
   const long groups = long(c.batch) * c.kv_heads * c.splits;
   hipLaunchKernelGGL((decode_attn_kernel<T, TQ, TO, D, G, W>), dim3(unsigned(groups)), dim3(W * kWave), 0,
                      c.stream, static_cast<const TQ*>(c.q), static_cast<const T*>(c.k),
-                     static_cast<const T*>(c.v), c.lengths, c.pmax, c.psum, c.pout, c.out, c.kv_heads,
-                     c.cap, c.splits, chunk, c.scale * kLog2e, c.x, c.d_model);
+                     static_cast<const T*>(c.v), c.lengths, c.kv_heads, c.cap, c.splits, chunk,
+                     c.scale * kLog2e, c.d_model, c.pmax, c.psum, c.pout, c.out, c.x);
   return check_launch("decode_attention");
 }
 

@@ -298,8 +298,10 @@ __global__ __launch_bounds__(kWaves * kWave) void linear_kernel(const void* p_w,
   const int K = a.k;
 
   constexpr int CB = act_chunk_bytes<T>();
-  // The loads wait for these indices: the one-block instantiation keeps its
-  // prologue to two unsigned divisions.
+  // The loads wait for these indices, and a launch's first instructions are
+  // fetched cold: the one-block instantiations of the epilogues that never
+  // split K (all but RESIDUAL) compute them without a division.
+  constexpr bool kOnePart = E != EPI_RESIDUAL;  // ksplit is 1
   const int tiles = (a.n + kTileN - 1) / kTileN;
   unsigned item = blockIdx.x;
   int blk = 0;
@@ -310,13 +312,13 @@ __global__ __launch_bounds__(kWaves * kWave) void linear_kernel(const void* p_w,
     item = (r / blocks) * kXcds + blockIdx.x % kXcds;
     if (item >= unsigned(tiles) * unsigned(a.ksplit)) return;  // padding of the last group of 8 items
   }
-  const int tile = int(item % unsigned(tiles));
-  const int part = int(item / unsigned(tiles));
+  const int tile = kOnePart ? int(item) : int(item % unsigned(tiles));
+  const int part = kOnePart ? 0 : int(item / unsigned(tiles));
   const int n0 = tile * kTileN;
   const int grp = lane / 16;
   const int b = blk * kBlockRows + lane % 16;  // this lane's batch row
   const int nchunks = K / KC;
-  const int per = (nchunks + a.ksplit - 1) / a.ksplit;
+  const int per = kOnePart ? nchunks : (nchunks + a.ksplit - 1) / a.ksplit;
   const int cb = part * per;
   const int ce = min(nchunks, cb + per);
   if (cb >= ce) return;  // an empty K part (whole workgroup)

@@ -30,13 +30,14 @@ __global__ __launch_bounds__(256) void embed_kernel(const int64_t* __restrict__ 
 // One wave per sequence: finish the argmax over the lm_head tiles (lowest
 // index on ties), record it, pick the next token (the given one while the
 // sequence is still inside its prompt, else the argmax), gather its
-// embedding into x (fp32) and advance pos/lengths.
+// embedding into x (fp32) and advance pos/lengths. The arguments the first
+// loads need come first (13 dwords, preloaded into SGPRs with the wave).
 template <typename T>
 __global__ __launch_bounds__(64) void next_token_kernel(
-    const float* __restrict__ best_val, const int32_t* __restrict__ best_idx, int tiles, int best_stride,
-    int64_t* __restrict__ tokens, int64_t* __restrict__ predicted, long stride,
-    const int32_t* __restrict__ prompt_len, int32_t* __restrict__ pos, int32_t* __restrict__ lengths,
-    const T* __restrict__ emb, float* __restrict__ x, int d, int cap) {
+    const float* __restrict__ best_val, const int32_t* __restrict__ best_idx, int32_t* __restrict__ pos,
+    int64_t* __restrict__ tokens, long stride, int tiles, int best_stride, int cap,
+    int64_t* __restrict__ predicted, const int32_t* __restrict__ prompt_len, int32_t* __restrict__ lengths,
+    const T* __restrict__ emb, float* __restrict__ x, int d) {
   const int b = blockIdx.x;
   const int lane = threadIdx.x;
   const int p = pos[b];
@@ -131,17 +132,17 @@ extern "C" int sfl_next_token(const float* best_val, const int32_t* best_idx, in
   if (best_stride < batch) return set_error(SFL_ERR_INVALID, "next_token: best_stride must be >= batch");
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (dtype == SFL_DTYPE_BF16)
-    hipLaunchKernelGGL(next_token_kernel<bf16_t>, dim3(batch), dim3(64), 0, s, best_val, best_idx, tiles,
-                       best_stride, tokens, predicted, token_stride, prompt_len, pos, lengths,
-                       static_cast<const bf16_t*>(emb), x, d_model, capacity);
+    hipLaunchKernelGGL(next_token_kernel<bf16_t>, dim3(batch), dim3(64), 0, s, best_val, best_idx, pos, tokens,
+                       token_stride, tiles, best_stride, capacity, predicted, prompt_len, lengths,
+                       static_cast<const bf16_t*>(emb), x, d_model);
   else if (dtype == SFL_DTYPE_F16)
-    hipLaunchKernelGGL(next_token_kernel<f16_t>, dim3(batch), dim3(64), 0, s, best_val, best_idx, tiles,
-                       best_stride, tokens, predicted, token_stride, prompt_len, pos, lengths,
-                       static_cast<const f16_t*>(emb), x, d_model, capacity);
+    hipLaunchKernelGGL(next_token_kernel<f16_t>, dim3(batch), dim3(64), 0, s, best_val, best_idx, pos, tokens,
+                       token_stride, tiles, best_stride, capacity, predicted, prompt_len, lengths,
+                       static_cast<const f16_t*>(emb), x, d_model);
   else if (dtype == SFL_DTYPE_F32)
-    hipLaunchKernelGGL(next_token_kernel<float>, dim3(batch), dim3(64), 0, s, best_val, best_idx, tiles,
-                       best_stride, tokens, predicted, token_stride, prompt_len, pos, lengths,
-                       static_cast<const float*>(emb), x, d_model, capacity);
+    hipLaunchKernelGGL(next_token_kernel<float>, dim3(batch), dim3(64), 0, s, best_val, best_idx, pos, tokens,
+                       token_stride, tiles, best_stride, capacity, predicted, prompt_len, lengths,
+                       static_cast<const float*>(emb), x, d_model);
   else
     return set_error(SFL_ERR_UNSUPPORTED, "next_token: model dtype must be F32, BF16 or F16");
   return check_launch("next_token");
