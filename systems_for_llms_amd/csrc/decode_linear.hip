@@ -433,7 +433,11 @@ __global__ __launch_bounds__(kWaves * kWave) void linear_kernel(const void* p_w,
     }
   }
 
-  // Sum the waves' partial tiles (and partial sums of x^2).
+  // Sum the waves' partial tiles (and partial sums of x^2). Every thread adds
+  // up one value of the tile over the waves, in wave order, and leaves the sum
+  // in wave 0's slot, which only it reads; wave 0 then reads its lanes' sums.
+  // (Wave 0 adding all waves' values by itself waited on ~30 small groups of
+  // LDS reads while the other waves had nothing left to do.)
   float* mine = red + (wave * kWave + lane) * RS;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -442,17 +446,25 @@ __global__ __launch_bounds__(kWaves * kWave) void linear_kernel(const void* p_w,
   }
   if constexpr (kNorm) mine[RS - 1] = ssum;
   __syncthreads();
+  constexpr int NV = kWave * RS;  // values of one wave's partial tile
+  for (int q = tid; q < NV; q += kWaves * kWave) {
+    float t = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) t += red[w * NV + q];
+    red[q] = t;
+  }
+  __syncthreads();
   if (wave != 0) return;
   float v1[4] = {0.f, 0.f, 0.f, 0.f}, v3[4] = {0.f, 0.f, 0.f, 0.f};
   float sq = 0.f;
-  for (int w = 0; w < kWaves; ++w) {
-    const float* p = red + (w * kWave + lane) * RS;
+  {
+    const float* p = red + lane * RS;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      v1[i] += p[i];
-      if constexpr (kTwo) v3[i] += p[4 + i];
+      v1[i] = p[i];
+      if constexpr (kTwo) v3[i] = p[4 + i];
     }
-    if constexpr (kNorm) sq += p[RS - 1];
+    if constexpr (kNorm) sq = p[RS - 1];
   }
   if constexpr (kNorm) {
     // Lane (row b, group g) holds group g's sum over all of K: add the 4 groups.
