@@ -287,7 +287,11 @@ __global__ __launch_bounds__(kWaves * kWave) void linear_kernel(const void* p_w,
   }
   constexpr int KC = chunk_k<T>();
   constexpr int EPL = vec_elems<T>();
-  constexpr bool kTwo = (E == EPI_SWIGLU);
+  // Two accumulators sharing the x operands: W1 and W3 (SWIGLU), or two
+  // consecutive 16-row tiles of the lm_head (LOGITS), so one launch round
+  // covers the vocabulary with half as many workgroups re-reading x.
+  constexpr bool kTwo = (E == EPI_SWIGLU || E == EPI_LOGITS);
+  constexpr int kTilesPerItem = E == EPI_LOGITS ? 2 : 1;
   constexpr bool kNorm = (E != EPI_RESIDUAL);
   constexpr int RS = (kTwo ? 8 : 4) + (kNorm ? 1 : 0);  // floats per lane in the cross-wave reduction
   using Src = typename SrcOf<kNorm, T>::type;
@@ -310,9 +314,10 @@ __global__ __launch_bounds__(kWaves * kWave) void linear_kernel(const void* p_w,
     const unsigned r = blockIdx.x / kXcds;
     blk = int(r % blocks);
     item = (r / blocks) * kXcds + blockIdx.x % kXcds;
-    if (item >= unsigned(tiles) * unsigned(a.ksplit)) return;  // padding of the last group of 8 items
+    if (item >= unsigned((tiles + kTilesPerItem - 1) / kTilesPerItem) * unsigned(a.ksplit))
+      return;  // padding of the last group of 8 items
   }
-  const int tile = kOnePart ? int(item) : int(item % unsigned(tiles));
+  const int tile = kOnePart ? int(item) * kTilesPerItem : int(item % unsigned(tiles));
   const int part = kOnePart ? 0 : int(item / unsigned(tiles));
   const int n0 = tile * kTileN;
   const int grp = lane / 16;
@@ -326,7 +331,10 @@ __global__ __launch_bounds__(kWaves * kWave) void linear_kernel(const void* p_w,
   // from act + c*CB (activation format) or from row b of x and the gain.
   const unsigned char* wl = static_cast<const unsigned char*>(a.w) + (long(tile) * nchunks * kWave + lane) * 16;
   const unsigned char* w3l =
-      kTwo ? static_cast<const unsigned char*>(a.w3) + (long(tile) * nchunks * kWave + lane) * 16 : nullptr;
+      E == EPI_SWIGLU ? static_cast<const unsigned char*>(a.w3) + (long(tile) * nchunks * kWave + lane) * 16
+      : E == EPI_LOGITS ? static_cast<const unsigned char*>(a.w) +
+                              (long(min(tile + 1, tiles - 1)) * nchunks * kWave + lane) * 16  // masked at the end
+                        : nullptr;
   const bool live = b < a.batch;
   const int row = min(b, a.batch - 1);
   const unsigned char* al =
@@ -479,30 +487,37 @@ __global__ __launch_bounds__(kWaves * kWave) void linear_kernel(const void* p_w,
   }
 
   if constexpr (E == EPI_LOGITS) {
-    // Start from a valid index so a row of NaN logits still yields an in-range token.
-    float bv = -INFINITY;
-    int bi = min(n, a.n - 1);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      if (n + i < a.n && better(v1[i], n + i, bv, bi)) { bv = v1[i]; bi = n + i; }
-    }
+    for (int t = 0; t < kTilesPerItem; ++t) {
+      const int tt = tile + t;
+      if (tt >= tiles) break;  // uniform: an odd tile count leaves the last item one tile
+      const float* v = t == 0 ? v1 : v3;
+      const int nt = tt * kTileN + 4 * grp;  // this lane's features nt .. nt+3
+      // Start from a valid index so a row of NaN logits still yields an in-range token.
+      float bv = -INFINITY;
+      int bi = min(nt, a.n - 1);
 #pragma unroll
-    for (int m = 16; m < kWave; m <<= 1) {
-      const float ov = lane_xor(bv, m);
-      const int oi = lane_xor(bi, m);
-      if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
-    }
-    if (live) {
-      if (grp == 0) {
-        a.best_val[long(tile) * a.best_stride + b] = bv;
-        a.best_idx[long(tile) * a.best_stride + b] = bi;
+      for (int i = 0; i < 4; ++i) {
+        if (nt + i < a.n && better(v[i], nt + i, bv, bi)) { bv = v[i]; bi = nt + i; }
       }
-      if (a.logits && n < a.n) {
-        float* dst = static_cast<float*>(a.logits) + b * a.logits_batch_stride + n;
-        if (a.pos) dst += long(a.pos[b]) * a.logits_pos_stride;
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          if (n + i < a.n) dst[i] = v1[i];
+      for (int m = 16; m < kWave; m <<= 1) {
+        const float ov = lane_xor(bv, m);
+        const int oi = lane_xor(bi, m);
+        if (better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+      }
+      if (live) {
+        if (grp == 0) {
+          a.best_val[long(tt) * a.best_stride + b] = bv;
+          a.best_idx[long(tt) * a.best_stride + b] = bi;
+        }
+        if (a.logits && nt < a.n) {
+          float* dst = static_cast<float*>(a.logits) + b * a.logits_batch_stride + nt;
+          if (a.pos) dst += long(a.pos[b]) * a.logits_pos_stride;
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (nt + i < a.n) dst[i] = v[i];
+        }
       }
     }
     return;
@@ -541,7 +556,8 @@ __global__ __launch_bounds__(kWaves * kWave) void linear_kernel(const void* p_w,
 
 template <typename T, int E, int CPW>
 int launch_linear_cpw(const LinearArgs& a, hipStream_t stream, const char* what) {
-  const long items = long((a.n + kTileN - 1) / kTileN) * a.ksplit;
+  constexpr int kTilesPerItem = E == EPI_LOGITS ? 2 : 1;  // as linear_kernel
+  const long items = long(((a.n + kTileN - 1) / kTileN + kTilesPerItem - 1) / kTilesPerItem) * a.ksplit;
   const long blocks = (a.batch + kBlockRows - 1) / kBlockRows;
   const void* src = E == EPI_RESIDUAL ? a.act : static_cast<const void*>(a.x_in);
   void* aux = E == EPI_RESIDUAL ? static_cast<void*>(a.x)
