@@ -125,7 +125,7 @@ def time_graph(fn, inner=10, reps=12):
     return sorted(times)[len(times) // 2]
 
 
-# The reference's published attention timings (H100 80GB):
+# The reference's published attention timings (H100 80GB HBM3):
 # cuda_decode rows as (B, Hq, Hkv, N, D, custom us, Flash SDPA us) from
 # attention_lab/results/h100-extensions-20261105/decode/study/benchmark.json, and
 # interval-schedule masked attention (B=1, H=8, N=4096) as (D, mask, us) from the
